@@ -1,0 +1,179 @@
+/*
+ * prunepath_moe.h -- C ABI of the MI355X (gfx950) PrunePath sparse-MoE MLP path.
+ *
+ * Library: prune_path_openpangu-embedded-1b_amd/libprunepath_moe.so (hipcc, gfx950 only).
+ * Every entry point takes plain device pointers, sizes and a hipStream_t passed as
+ * void* (NULL = the null stream). Work is enqueued on that stream without any host
+ * synchronisation and without allocating memory, so calls can be captured in a
+ * hipGraph. Return value: PP_OK or an error code; pp_last_error() gives the message
+ * of the last failure on the calling thread. Invalid shapes are rejected before any
+ * launch.
+ *
+ * Shapes: H hidden size, E experts, G neurons per expert (I = E*G FFN width),
+ * N tokens. Supported: H % 128 == 0 and 128 <= H <= 4096, 1 <= E <= 256,
+ * G % 32 == 0 and 32 <= G <= 8192.
+ *
+ * Reference interfaces replaced (paths relative to the reference repository root):
+ *   src/tl_kernel_optimized_Ultimate_PanGU.py  -- TauSparseMoE and its Triton kernels
+ *   src/MoEBlock_origin.py                     -- softmax_thresholding / MoELayer routing
+ *   src/openpangu_moe.py                       -- physical_reorder_for_inference
+ */
+#ifndef PRUNEPATH_MOE_H
+#define PRUNEPATH_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PP_OK 0
+#define PP_ERR_INVALID 1     /* bad shape / pointer / argument */
+#define PP_ERR_HIP 2         /* a HIP runtime call failed */
+#define PP_ERR_UNSUPPORTED 3 /* shape outside the supported range */
+
+#define PP_DTYPE_F32 0
+#define PP_DTYPE_BF16 1
+
+#define PP_MAX_EXPERTS 256
+
+/* Message of the last error on this thread ("" if none). */
+const char* pp_last_error(void);
+/* ABI version (incremented on any signature change). */
+int pp_abi_version(void);
+
+/* ------------------------------------------------------------------------- *
+ * Rearrangement: one-time physical reorder of the expert weights.
+ * Replaces physical_reorder_for_inference (src/openpangu_moe.py:212-256), which
+ * argsorts neuron->expert ids and mounts W_gate/W_up [H,I], W_down [I,H] and
+ * router [H,E] in bf16 on TauSparseMoE (src/tl_kernel_optimized_Ultimate_PanGU.py:483-486).
+ *
+ * Packed expert buffer (bf16), two regions:
+ *   rows   [E*G][3][H]  for rearranged neuron j: gate row, up row, down column,
+ *                       each H contiguous values (one 6*H-byte record per neuron);
+ *   down_t [E][H][G]    the down projection of each expert with its G neurons
+ *                       contiguous (K-contiguous operand of the prefill down GEMM).
+ * Source element (neuron n, hidden h) is read at src[n*s_n + h*s_h] for gate and up
+ * and at down[n*d_n + h*d_h] for down, so both the nn.Linear layout
+ * (gate/up [I,H]: s_n=H, s_h=1; down [H,I]: d_n=1, d_h=I) and the TauSparseMoE
+ * layout (W_gate [H,I]: s_n=1, s_h=I; W_down [I,H]: d_n=H, d_h=1) are accepted.
+ * perm[j] (device int32 [I], may be NULL = identity) names the source neuron of
+ * rearranged neuron j; expert e owns rearranged neurons e*G .. e*G+G-1.
+ * ------------------------------------------------------------------------- */
+size_t pp_packed_expert_bytes(int H, int E, int G);
+int pp_pack_experts(const void* w_gate, const void* w_up, int64_t s_n, int64_t s_h,
+                    const void* w_down, int64_t d_n, int64_t d_h, int src_dtype,
+                    const int32_t* perm, int H, int E, int G, void* packed, void* stream);
+
+/* Router weights to the fp32 [Epad][H] layout the kernels read (Epad = E rounded up
+ * to 16, zero rows). Source element (expert e, hidden h) at src[e*s_e + h*s_h]:
+ * MoELayer.mlp_router[0].weight [E,H] (src/MoEBlock_origin.py:127-129) or
+ * TauSparseMoE.router [H,E] (src/tl_kernel_optimized_Ultimate_PanGU.py:486). */
+size_t pp_packed_router_bytes(int H, int E);
+int pp_pack_router(const void* w_router, int64_t s_e, int64_t s_h, int src_dtype,
+                   int H, int E, float* router_packed, void* stream);
+
+/* ------------------------------------------------------------------------- *
+ * Routing: tau cumulative-probability expert selection.
+ * Replaces softmax_thresholding (src/MoEBlock_origin.py:50-97) and the prefill
+ * moe_router_kernel + torch.sort + moe_select_expert_kernel + scatter
+ * (src/tl_kernel_optimized_Ultimate_PanGU.py:40-124, 550-564).
+ * Semantics (bit-exact with torch CPU given the same fp32 logits):
+ *   p = softmax(logits); order = torch.sort(p, descending) order; cum = fp32 of
+ *   the float64 running sum of p in that order; selected = ranks r with
+ *   cum[r] < (float)tau, and rank 0 always; gate = sigmoid(logit) on selected
+ *   experts, 0 elsewhere.
+ * Outputs (NULL = not written): logits/probs/gates fp32 [N,E]; mask uint8 [N,E];
+ * count int32 [N] (selected experts per token).
+ * ------------------------------------------------------------------------- */
+int pp_route(const void* x, int x_dtype, int64_t n_tokens, int H,
+             const float* router_packed, const float* bias, int E, float tau,
+             float* logits_out, float* probs_out, float* gates_out,
+             uint8_t* mask_out, int32_t* count_out, void* stream);
+int pp_route_logits(const float* logits, int64_t n_tokens, int E, float tau,
+                    float* probs_out, float* gates_out, uint8_t* mask_out,
+                    int32_t* count_out, void* stream);
+
+/* ------------------------------------------------------------------------- *
+ * Bucketing: token -> expert CSR layout, experts ascending, tokens ascending
+ * inside each expert (the order moe_local_scan_kernel / moe_global_scan_kernel /
+ * moe_dispatch_kernel produce, src/tl_kernel_optimized_Ultimate_PanGU.py:133-266,
+ * without the 16-row padding and without the total_tiles host sync at :581).
+ *   offsets     int32 [E+1]
+ *   token_ids   int32 [N*E] capacity, first offsets[E] used
+ *   pair_gates  fp32  [N*E] capacity
+ *   token_pairs int32 [N,E]: pair positions of token t in ascending expert id, -1 padded
+ *   tiles       int32 [pp_max_tiles(N,E,tile_m)][4]: {expert, first pair, rows, 0}
+ *   meta        int32 [4]: {number of tiles, number of pairs P, 0, 0}
+ * workspace: pp_bucket_workspace_bytes(N, E) bytes of device scratch.
+ * ------------------------------------------------------------------------- */
+size_t pp_bucket_workspace_bytes(int64_t n_tokens, int E);
+/* Row-tile height the grouped GEMMs (pp_expert_gateup / pp_expert_down) expect
+ * in the tile map; pass it as tile_m. */
+int pp_gemm_tile_m(void);
+int64_t pp_max_tiles(int64_t n_tokens, int E, int tile_m);
+int pp_bucket(const uint8_t* mask, const float* gates, int64_t n_tokens, int E, int tile_m,
+              int32_t* offsets, int32_t* token_ids, float* pair_gates, int32_t* token_pairs,
+              int32_t* tiles, int32_t* meta, void* workspace, void* stream);
+
+/* ------------------------------------------------------------------------- *
+ * Decode (N == 1): one fused kernel -- router GEMV (fp32), selection, gate/up
+ * GEMVs over the selected experts' neurons, silu(g)*u*gate, down GEMV and the
+ * cross-workgroup fp32 reduction, bf16 output.
+ * Replaces TauSparseMoE.forward_decode with moe_router_select_kernel_decode and
+ * moe_decode_swiglu_fused_kernel (src/tl_kernel_optimized_Ultimate_PanGU.py:335-462, 494-530).
+ * The workspace (pp_decode_workspace_bytes) must be zeroed once with
+ * pp_decode_workspace_init before the first call; every call leaves it ready for
+ * the next one. Calls that share a workspace must be ordered (same stream);
+ * overlapping calls on one workspace race. After a call the workspace holds the
+ * call's logits, selected experts and gates (struct pp_decode_state below).
+ * grid = number of workgroups (0 = automatic).
+ * ------------------------------------------------------------------------- */
+typedef struct pp_decode_state {
+  uint32_t router_ticket; /* internal */
+  uint32_t ready;         /* internal */
+  uint32_t done;          /* internal */
+  uint32_t error;         /* non-zero: a wait timed out, output invalid */
+  int32_t k;              /* experts selected by the last call */
+  int32_t pad[3];
+  float logits[PP_MAX_EXPERTS];
+  int32_t sel_ids[PP_MAX_EXPERTS];   /* selected experts, descending probability */
+  float sel_gates[PP_MAX_EXPERTS];   /* sigmoid(logit) of each selected expert */
+} pp_decode_state;
+
+size_t pp_decode_workspace_bytes(int H, int E);
+int pp_decode_workspace_init(void* workspace, int H, int E, void* stream);
+int pp_moe_decode(const void* x, int x_dtype, int H, const float* router_packed,
+                  const float* bias, int E, int G, float tau, const void* packed,
+                  void* out_bf16, void* workspace, int grid, void* stream);
+
+/* ------------------------------------------------------------------------- *
+ * Prefill / N > 1: route -> bucket -> grouped gate/up GEMM with fused SwiGLU
+ * epilogue (bf16 MFMA) -> grouped down GEMM -> per-token combine in fp32 -> bf16.
+ * Replaces TauSparseMoE.forward_prefill (src/tl_kernel_optimized_Ultimate_PanGU.py:532-604)
+ * and moe_fused_expert_kernel (:271-328). No host synchronisation.
+ * workspace: pp_prefill_workspace_bytes(N, H, E, G) bytes of device scratch.
+ * ------------------------------------------------------------------------- */
+size_t pp_prefill_workspace_bytes(int64_t n_tokens, int H, int E, int G);
+int pp_moe_prefill(const void* x, int x_dtype, int64_t n_tokens, int H,
+                   const float* router_packed, const float* bias, int E, int G, float tau,
+                   const void* packed, void* out_bf16, void* workspace, void* stream);
+
+/* Stages of pp_moe_prefill, exposed for testing and for callers that route
+ * elsewhere. x is bf16 [N,H]. act is bf16 [N*E][G] capacity (row = pair), y is
+ * fp32 [N*E][H] capacity (row = pair). */
+int pp_expert_gateup(const void* x_bf16, int H, int G, const void* packed, int E,
+                     const int32_t* token_ids, const float* pair_gates,
+                     const int32_t* tiles, const int32_t* meta, int64_t max_tiles,
+                     void* act_bf16, void* stream);
+int pp_expert_down(const void* act_bf16, int H, int G, const void* packed, int E,
+                   const int32_t* tiles, const int32_t* meta, int64_t max_tiles,
+                   float* y_f32, void* stream);
+int pp_combine(const float* y_f32, const int32_t* token_pairs, const int32_t* count,
+               int64_t n_tokens, int H, int E, void* out_bf16, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* PRUNEPATH_MOE_H */

@@ -1,0 +1,39 @@
+// Host-side plumbing shared by all entry points: per-thread error text, launch
+// checks, device properties.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "pp_common.h"
+
+static thread_local char g_err[512] = "";
+
+void pp_set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof g_err, fmt, ap);
+  va_end(ap);
+}
+
+int pp_check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    pp_set_error("%s: %s", what, hipGetErrorString(e));
+    return PP_ERR_HIP;
+  }
+  return PP_OK;
+}
+
+int pp_device_cus() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 256;
+  static int cached[64] = {0};
+  if (dev >= 0 && dev < 64 && cached[dev]) return cached[dev];
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    cus = 256;
+  if (dev >= 0 && dev < 64) cached[dev] = cus;
+  return cus;
+}
+
+extern "C" const char* pp_last_error(void) { return g_err; }
+extern "C" int pp_abi_version(void) { return 1; }

@@ -1,0 +1,761 @@
+// Decode (one token): a single fused kernel for the whole MoE-MLP layer.
+//
+// Replaces TauSparseMoE.forward_decode (src/tl_kernel_optimized_Ultimate_PanGU.py:494-530):
+// decode_out.zero_() + moe_router_select_kernel_decode (:335-380) +
+// moe_decode_swiglu_fused_kernel (:385-462). Differences by design: fp32 router, the
+// torch-CPU selection rule (fp64-accumulated cumsum, torch sort order), every neuron of
+// every selected expert computed (the reference's 1-D grid leaves pid_g at 0 and only
+// covers 64 neurons per expert, :398-399, 515), and an fp32 reduction instead of bf16
+// atomics.
+//
+// Routing. When the fp32 router is small (E <= 16 and 16*H*4 <= 128 KB, e.g. E=16 at
+// H=1536) every workgroup computes all logits (fixed reduction order, so every workgroup gets
+// the same bits) and runs the selection itself: no cross-workgroup wait at all.
+// Otherwise workgroups 0..R-1 compute the logits, the last of them (ticket) runs the
+// selection and publishes it, and every workgroup waits for the `ready` flag with a
+// bounded spin. Workgroups are dispatched in index order, so the producers are resident
+// before any waiter can take their slot; the bound only turns an impossible wait into
+// an error flag instead of a hang.
+//
+// Work split. The layer's weight bytes are k * G neuron records of 6*H bytes each
+// ({gate row, up row, down column}, see pack.hip). All workgroups share the k*G
+// records evenly; each wave streams whole records with 16-byte loads per lane (the next
+// record's loads are in flight while the current one is reduced), reduces the gate/up
+// dot products across the wave, applies silu(g)*u*gate in registers and accumulates
+// act * down into 8*CPL fp32 registers per lane. The workgroup's partial output goes to
+// one of DEC_NCOPY fp32 accumulators with float atomics; the last workgroup to finish
+// (ticket) folds the copies with atomic exchanges (which also clear them), writes the
+// bf16 output and resets the counters, so the next call needs no memset.
+//
+// Cross-workgroup data (logits, selection, counters, accumulators) is only accessed
+// with agent-scope atomics, and ordering between them comes from waiting for
+// completion (s_waitcnt vmcnt(0)) before the dependent atomic. Agent-scope fences are
+// avoided on purpose: on gfx950 each one writes back and invalidates the L2, which
+// hundreds of workgroups cannot afford inside a 5 us kernel.
+#include "pp_common.h"
+
+#define DEC_THREADS 256
+#define DEC_NCOPY 8
+#define DEC16_NW 8  // waves per workgroup in the E = 16 kernel
+#define DEC_SPIN_LIMIT (1u << 22)
+#define DEC_LOCAL_ROUTER_FLOATS 32768  // Epad*H at or below this: every workgroup routes
+
+static inline size_t dec_acc_offset() { return (sizeof(pp_decode_state) + 255) / 256 * 256; }
+
+__device__ __forceinline__ void vm_wait() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+template <typename T>
+__device__ __forceinline__ T ld_rlx(const T* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <typename T>
+__device__ __forceinline__ void st_rlx(T* p, T v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t add_rlx(uint32_t* p, uint32_t v) {
+  return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// 8 bf16 packed in a uint4: dot with x[8], or acc += a * w
+__device__ __forceinline__ float dot8(const uint4 w, const float* x) {
+  float s = 0.0f;
+  const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    s = __builtin_fmaf(x[2 * i], __uint_as_float(u[i] << 16), s);
+    s = __builtin_fmaf(x[2 * i + 1], __uint_as_float(u[i] & 0xffff0000u), s);
+  }
+  return s;
+}
+__device__ __forceinline__ void axpy8(float a, const uint4 w, float* acc) {
+  const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    acc[2 * i] = __builtin_fmaf(a, __uint_as_float(u[i] << 16), acc[2 * i]);
+    acc[2 * i + 1] = __builtin_fmaf(a, __uint_as_float(u[i] & 0xffff0000u), acc[2 * i + 1]);
+  }
+}
+
+// All logits of the token in this workgroup, for the local-routing mode. Wave w takes
+// experts 4w..4w+3 of each group of 16; lane l the float4 chunks l, l+64, ... of x and of
+// those router rows, all loaded up front (one memory round trip). Per-wave totals by a
+// fixed butterfly (lane l ends with expert 4w + 2*b5 + b4), so the logits are
+// deterministic and identical in every workgroup.
+template <typename XT, int CPL>
+__device__ void local_logits(const XT* __restrict__ x, int H, const float* __restrict__ router,
+                             const float* __restrict__ bias, int E, float* lg_s, int tid) {
+  constexpr int NC = 2 * CPL;  // float4 chunks per lane per row (H <= 512 * CPL)
+  const int lane = tid & 63, wv = tid >> 6;
+  const int HC4 = H >> 2;
+  float4 xv[NC];
+#pragma unroll
+  for (int i = 0; i < NC; ++i) {
+    const int c = lane + 64 * i;
+    if (c < HC4) {
+      xv[i].x = load_as_f32<XT>(x, 4 * c);
+      xv[i].y = load_as_f32<XT>(x, 4 * c + 1);
+      xv[i].z = load_as_f32<XT>(x, 4 * c + 2);
+      xv[i].w = load_as_f32<XT>(x, 4 * c + 3);
+    } else {
+      xv[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  }
+  for (int e0 = 0; e0 < E; e0 += 16) {
+    float4 wr[4][NC];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int i = 0; i < NC; ++i) {
+        const int c = lane + 64 * i;
+        wr[j][i] = c < HC4 ? *(const float4*)(router + (int64_t)(e0 + 4 * wv + j) * H + 4 * c)
+                           : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+    float part[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float sacc = 0.0f;
+#pragma unroll
+      for (int i = 0; i < NC; ++i) {
+        sacc = __builtin_fmaf(xv[i].x, wr[j][i].x, sacc);
+        sacc = __builtin_fmaf(xv[i].y, wr[j][i].y, sacc);
+        sacc = __builtin_fmaf(xv[i].z, wr[j][i].z, sacc);
+        sacc = __builtin_fmaf(xv[i].w, wr[j][i].w, sacc);
+      }
+      part[j] = sacc;
+    }
+    // butterfly: 4 values -> lane holds total of value 2*b5 + b4
+    const int b5 = (lane >> 5) & 1, b4 = (lane >> 4) & 1;
+    float a2[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      a2[i] = __fadd_rn(b5 ? part[i + 2] : part[i], __shfl_xor(b5 ? part[i] : part[i + 2], 32, PP_WAVE));
+    float t = __fadd_rn(b4 ? a2[1] : a2[0], __shfl_xor(b4 ? a2[0] : a2[1], 16, PP_WAVE));
+#pragma unroll
+    for (int o = 8; o >= 1; o >>= 1) t = __fadd_rn(t, __shfl_xor(t, o, PP_WAVE));
+    const int e = e0 + 4 * wv + 2 * b5 + b4;
+    if ((lane & 15) == 0 && e < E) lg_s[e] = bias ? __fadd_rn(t, bias[e]) : t;
+  }
+  __syncthreads();
+}
+
+template <typename XT, int CPL, bool LOCAL>
+__global__ __launch_bounds__(DEC_THREADS) void decode_kernel(
+    const XT* __restrict__ x, int H, const float* __restrict__ router, const float* __restrict__ bias,
+    int E, int G, float tau, const bf16_t* __restrict__ rows, bf16_t* __restrict__ out,
+    pp_decode_state* __restrict__ st, float* __restrict__ acc, int R) {
+  extern __shared__ __align__(16) float red[];  // [3][H] wave partials
+  __shared__ SelScratch ss;
+  __shared__ float red4[4];
+  __shared__ float lg_s[PP_MAX_EXPERTS];
+  __shared__ int flag_s;
+  __shared__ int k_s;
+  __shared__ int sel_ids_s[PP_MAX_EXPERTS];
+  __shared__ float sel_g_s[PP_MAX_EXPERTS];
+
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int W = gridDim.x, b = blockIdx.x;
+  const int HC = H >> 3;  // 16-byte chunks per row
+
+  if (LOCAL) {
+    // ---------------- every workgroup routes the token itself
+    local_logits<XT, CPL>(x, H, router, bias, E, lg_s, tid);
+    if (wv == 0) {
+      select_small<16>([&](int j) { return lg_s[j]; }, E, tau, &ss, lane);
+      const int k = ss.k;
+      for (int q = lane; q < k; q += 64) {
+        const int e = ss.order[q];
+        sel_ids_s[q] = e;
+        sel_g_s[q] = pp_sigmoid(lg_s[e]);
+      }
+      if (lane == 0) k_s = k;
+    }
+    __syncthreads();
+    if (b == 0) {  // telemetry for the caller: logits and selection of this call
+      for (int j = tid; j < E; j += DEC_THREADS) st_rlx(&st->logits[j], lg_s[j]);
+      for (int q = tid; q < k_s; q += DEC_THREADS) {
+        st_rlx(&st->sel_ids[q], sel_ids_s[q]);
+        st_rlx(&st->sel_gates[q], sel_g_s[q]);
+      }
+      if (tid == 0) st_rlx(&st->k, k_s);
+    }
+  } else {
+    // ---------------- router workgroups 0..R-1, then a flag
+    if (b < R) {
+      for (int e = b; e < E; e += R) {
+        float sacc = 0.0f;
+        for (int k = tid; k < H; k += DEC_THREADS)
+          sacc = __builtin_fmaf(load_as_f32<XT>(x, k), router[(int64_t)e * H + k], sacc);
+        sacc = wave_sum(sacc);
+        if (lane == 0) red4[wv] = sacc;
+        __syncthreads();
+        if (tid == 0) {
+          float l = __fadd_rn(__fadd_rn(__fadd_rn(red4[0], red4[1]), red4[2]), red4[3]);
+          if (bias) l = __fadd_rn(l, bias[e]);
+          st_rlx(&st->logits[e], l);
+        }
+        __syncthreads();
+      }
+      if (tid == 0) {
+        vm_wait();  // this workgroup's logits are performed before its ticket
+        flag_s = add_rlx(&st->router_ticket, 1u) == (uint32_t)(R - 1);
+      }
+      __syncthreads();
+      if (flag_s && wv == 0) {  // last router workgroup: selection, then publish
+        select_one_token([&](int j) { return ld_rlx(&st->logits[j]); }, E, tau, &ss, lane);
+        const int k = ss.k;
+        for (int q = lane; q < k; q += 64) {
+          const int e = ss.order[q];
+          st_rlx(&st->sel_ids[q], e);
+          st_rlx(&st->sel_gates[q], pp_sigmoid(ld_rlx(&st->logits[e])));
+        }
+        if (lane == 0) st_rlx(&st->k, k);
+        vm_wait();
+        if (lane == 0) st_rlx(&st->ready, 1u);
+      }
+      __syncthreads();
+    }
+    if (tid == 0) {
+      uint32_t n = 0;
+      int ok = 1;
+      while (ld_rlx(&st->ready) == 0u) {
+        __builtin_amdgcn_s_sleep(1);
+        if (++n > DEC_SPIN_LIMIT) {
+          __hip_atomic_fetch_or(&st->error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          ok = 0;
+          break;
+        }
+      }
+      k_s = ok ? ld_rlx(&st->k) : 0;
+    }
+    __syncthreads();
+    for (int q = tid; q < k_s; q += DEC_THREADS) {
+      sel_ids_s[q] = ld_rlx(&st->sel_ids[q]);
+      sel_g_s[q] = ld_rlx(&st->sel_gates[q]);
+    }
+    __syncthreads();
+  }
+  const int k = k_s;
+
+  // ---------------- stream the selected neuron records
+  // this workgroup: records [v0, v1) of the k*G selected ones; wave wv a contiguous
+  // quarter of them, loaded DEC_RB records at a time (all loads in flight together)
+  const int T = k * G;
+  const int v0 = (int)((int64_t)T * b / W), v1 = (int)((int64_t)T * (b + 1) / W);
+  const int n = v1 - v0;
+  int r = v0 + (n * wv) / 4;
+  const int r_end = v0 + (n * (wv + 1)) / 4;
+
+  // x, rounded to bf16 like the reference's x.to(bfloat16), as fp32 in registers
+  float xr[CPL][8];
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) {
+    const int ch = lane + 64 * c;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float vx = ch < HC ? load_as_f32<XT>(x, (int64_t)ch * 8 + i) : 0.0f;
+      xr[c][i] = bf16_to_f32(f32_to_bf16(vx));
+    }
+  }
+  float oacc[CPL][8];
+#pragma unroll
+  for (int c = 0; c < CPL; ++c)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) oacc[c][i] = 0.0f;
+
+  // one record per iteration (rolled loop: the code stays small, which matters because
+  // the instruction cache is cold at every launch); the next record's loads are issued
+  // before the current one is reduced
+  const uint4 zero4 = make_uint4(0, 0, 0, 0);
+  uint4 gq[CPL], uq[CPL], dq[CPL];
+  int s_cur = 0, g_cur = 0;
+  if (r < r_end) {
+    s_cur = r / G;
+    g_cur = r - s_cur * G;
+    const uint4* rec = (const uint4*)(rows + ((int64_t)sel_ids_s[s_cur] * G + g_cur) * 3 * H);
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+      const int ch = lane + 64 * c;
+      const bool in = ch < HC;
+      gq[c] = in ? rec[ch] : zero4;
+      uq[c] = in ? rec[HC + ch] : zero4;
+      dq[c] = in ? rec[2 * HC + ch] : zero4;
+    }
+  }
+  for (; r < r_end; ++r) {
+    uint4 g2[CPL], u2[CPL], d2[CPL];
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) { g2[c] = gq[c]; u2[c] = uq[c]; d2[c] = dq[c]; }
+    const float gwt = sel_g_s[s_cur];
+    if (r + 1 < r_end) {
+      if (++g_cur == G) { g_cur = 0; ++s_cur; }
+      const uint4* rec = (const uint4*)(rows + ((int64_t)sel_ids_s[s_cur] * G + g_cur) * 3 * H);
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) {
+        const int ch = lane + 64 * c;
+        const bool in = ch < HC;
+        gq[c] = in ? rec[ch] : zero4;
+        uq[c] = in ? rec[HC + ch] : zero4;
+        dq[c] = in ? rec[2 * HC + ch] : zero4;
+      }
+    }
+    float gs = 0.0f, us = 0.0f;
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+      gs += dot8(g2[c], xr[c]);
+      us += dot8(u2[c], xr[c]);
+    }
+    gs = wave_sum(gs);
+    us = wave_sum(us);
+    const float a = pp_silu(gs) * us * gwt;
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) axpy8(a, d2[c], oacc[c]);
+  }
+
+  // ---------------- workgroup reduction -> fp32 accumulator copy
+  // waves 1..3 park their partials in LDS, wave 0 adds its own into the first slot,
+  // then all threads fold the three slots for contiguous h and add to the copy.
+  const bool has_work = n > 0;
+  if (has_work && wv > 0) {
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+      const int ch = lane + 64 * c;
+      if (ch < HC) {
+        float4* dst = (float4*)(red + (size_t)(wv - 1) * H + ch * 8);
+        dst[0] = make_float4(oacc[c][0], oacc[c][1], oacc[c][2], oacc[c][3]);
+        dst[1] = make_float4(oacc[c][4], oacc[c][5], oacc[c][6], oacc[c][7]);
+      }
+    }
+  }
+  __syncthreads();
+  if (has_work && wv == 0) {
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+      const int ch = lane + 64 * c;
+      if (ch < HC) {
+        float* dst = red + ch * 8;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) dst[i] = oacc[c][i] + dst[i];
+      }
+    }
+  }
+  __syncthreads();
+  if (has_work) {
+    float* accc = acc + (size_t)(b % DEC_NCOPY) * H;
+    for (int h = tid; h < H; h += DEC_THREADS) {
+      const float sv = (red[h] + red[H + h]) + red[2 * H + h];
+      unsafeAtomicAdd(accc + h, sv);
+    }
+  }
+  vm_wait();  // every wave's accumulator atomics are performed before the ticket
+  __syncthreads();
+  if (tid == 0) flag_s = add_rlx(&st->done, 1u) == (uint32_t)(W - 1);
+  __syncthreads();
+  if (flag_s) {  // last workgroup: fold copies, write bf16, clear, reset counters
+    for (int h = tid; h < H; h += DEC_THREADS) {
+      float sv[DEC_NCOPY];
+#pragma unroll
+      for (int c = 0; c < DEC_NCOPY; ++c) sv[c] = ld_rlx(acc + (size_t)c * H + h);
+      float tot = 0.0f;
+#pragma unroll
+      for (int c = 0; c < DEC_NCOPY; ++c) tot += sv[c];
+#pragma unroll
+      for (int c = 0; c < DEC_NCOPY; ++c) st_rlx(acc + (size_t)c * H + h, 0.0f);
+      out[h] = f32_to_bf16(tot);
+    }
+    if (tid == 0) {
+      st_rlx(&st->router_ticket, 0u);
+      st_rlx(&st->done, 0u);
+      st_rlx(&st->ready, 0u);
+    }
+  }
+}
+
+// ------------------------------------------------------------------ E = 16 fast path
+// Specialisation of decode_kernel for exactly 16 experts and H = 512 * CPL (the
+// BASELINE shapes): every bound is a compile-time constant, so loads need no guards and
+// the selection is branch-free. The instruction cache is cold at each launch and every
+// workgroup executes the whole kernel, so the executed code size is latency.
+
+// x chunk ch (8 values) as fp32, bf16-rounded when asked
+template <typename XT>
+__device__ __forceinline__ void load_x8(const XT* x, int ch, float* v, bool round_bf16);
+template <>
+__device__ __forceinline__ void load_x8<float>(const float* x, int ch, float* v, bool round_bf16) {
+  const float4 a = *(const float4*)(x + ch * 8), b = *(const float4*)(x + ch * 8 + 4);
+  v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  if (round_bf16)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = bf16_to_f32(f32_to_bf16(v[i]));
+}
+template <>
+__device__ __forceinline__ void load_x8<bf16_t>(const bf16_t* x, int ch, float* v, bool) {
+  const uint4 u = *(const uint4*)(x + ch * 8);
+  const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[2 * i] = __uint_as_float(w[i] << 16);
+    v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+  }
+}
+
+template <typename XT, int CPL, int NW>
+__global__ __launch_bounds__(64 * NW) void decode16_kernel(
+    const XT* __restrict__ x, const float* __restrict__ router, const float* __restrict__ bias, int G, float tau,
+    const bf16_t* __restrict__ rows, bf16_t* __restrict__ out, pp_decode_state* __restrict__ st,
+    float* __restrict__ acc) {
+  constexpr int H = 512 * CPL;
+  constexpr int HC = H / 8;
+  constexpr int NT = 64 * NW;
+  extern __shared__ __align__(16) float red[];  // [NW-1][H]
+  __shared__ __align__(16) float lg_s[16];
+  __shared__ __align__(16) float ev_s[16];
+  __shared__ __align__(16) float srt_s[16];
+  __shared__ int ord_s[16];
+  __shared__ int flag_s;
+  __shared__ int k_s;
+  __shared__ int sel_ids_s[16];
+  __shared__ float sel_g_s[16];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int W = gridDim.x, b = blockIdx.x;
+
+  // ---- logits: wave wv -> experts EPW*wv ..; lane -> x chunks lane + 64 c (8 values each)
+  constexpr int EPW = 16 / NW;  // experts per wave (4 or 2)
+  float xf[CPL][8];
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) load_x8<XT>(x, lane + 64 * c, xf[c], false);
+  {
+    float4 wr[EPW][2 * CPL];
+#pragma unroll
+    for (int j = 0; j < EPW; ++j)
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) {
+        const float4* rp = (const float4*)(router + (EPW * wv + j) * H + (lane + 64 * c) * 8);
+        wr[j][2 * c] = rp[0];
+        wr[j][2 * c + 1] = rp[1];
+      }
+    float part[EPW];
+#pragma unroll
+    for (int j = 0; j < EPW; ++j) {
+      float sacc = 0.0f;
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) {
+        sacc = __builtin_fmaf(xf[c][0], wr[j][2 * c].x, sacc);
+        sacc = __builtin_fmaf(xf[c][1], wr[j][2 * c].y, sacc);
+        sacc = __builtin_fmaf(xf[c][2], wr[j][2 * c].z, sacc);
+        sacc = __builtin_fmaf(xf[c][3], wr[j][2 * c].w, sacc);
+        sacc = __builtin_fmaf(xf[c][4], wr[j][2 * c + 1].x, sacc);
+        sacc = __builtin_fmaf(xf[c][5], wr[j][2 * c + 1].y, sacc);
+        sacc = __builtin_fmaf(xf[c][6], wr[j][2 * c + 1].z, sacc);
+        sacc = __builtin_fmaf(xf[c][7], wr[j][2 * c + 1].w, sacc);
+      }
+      part[j] = sacc;
+    }
+    // butterfly over the wave: EPW values -> lane holds the total of value sel(lane)
+    const int b5 = (lane >> 5) & 1, b4 = (lane >> 4) & 1;
+    float t;
+    int e;
+    if (EPW == 4) {
+      float a2[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        a2[i] = __fadd_rn(b5 ? part[(i + 2) % EPW] : part[i % EPW], __shfl_xor(b5 ? part[i % EPW] : part[(i + 2) % EPW], 32, PP_WAVE));
+      t = __fadd_rn(b4 ? a2[1] : a2[0], __shfl_xor(b4 ? a2[0] : a2[1], 16, PP_WAVE));
+      e = EPW * wv + 2 * b5 + b4;
+    } else {
+      t = __fadd_rn(b5 ? part[1 % EPW] : part[0], __shfl_xor(b5 ? part[0] : part[1 % EPW], 32, PP_WAVE));
+      t = __fadd_rn(t, __shfl_xor(t, 16, PP_WAVE));
+      e = EPW * wv + b5;
+    }
+#pragma unroll
+    for (int o = 8; o >= 1; o >>= 1) t = __fadd_rn(t, __shfl_xor(t, o, PP_WAVE));
+    if ((lane & 15) == 0 && (EPW == 4 || b4 == 0)) lg_s[e] = bias ? __fadd_rn(t, bias[e]) : t;
+  }
+  __syncthreads();
+
+  // ---- selection (wave 0), branch-free for E = 16 (same arithmetic as select_small)
+  if (wv == 0) {
+    const int j = lane & 15;
+    const float xl = lg_s[j];
+    float m = xl;
+#pragma unroll
+    for (int o = 8; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, PP_WAVE));
+    const float e = pp_expf_u10(__fsub_rn(xl, m));
+    if (lane < 16) ev_s[lane] = e;
+    wave_sync_lds();
+    float ev[16];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float4 v = *(const float4*)&ev_s[4 * i];
+      ev[4 * i] = v.x; ev[4 * i + 1] = v.y; ev[4 * i + 2] = v.z; ev[4 * i + 3] = v.w;
+    }
+    float a8[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) a8[i] = __fadd_rn(ev[i], ev[i + 8]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) a8[i] = __fadd_rn(a8[i], a8[i + 4]);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) a8[i] = __fadd_rn(a8[i], a8[i + 2]);
+    const float r = __fdiv_rn(1.0f, __fadd_rn(a8[0], a8[1]));
+    const float p = __fmul_rn(e, r);
+    int rank = 0;
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      const float pq = __fmul_rn(ev[q], r);
+      rank += (kv_before(pq, p) || (pq == p && q < j)) ? 1 : 0;
+    }
+    if (lane < 16) {
+      srt_s[rank] = p;
+      ord_s[rank] = lane;
+    }
+    wave_sync_lds();
+    float sv[16];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float4 v = *(const float4*)&srt_s[4 * i];
+      sv[4 * i] = v.x; sv[4 * i + 1] = v.y; sv[4 * i + 2] = v.z; sv[4 * i + 3] = v.w;
+    }
+    // cum is non-decreasing, so the ranks with cum < tau are a prefix: count them
+    const float tau32 = tau;
+    double a = 0.0;
+    int k = 0;
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      a += (double)sv[q];
+      k += ((float)a < tau32) ? 1 : 0;
+    }
+    k = k > 0 ? k : 1;
+    if (lane < k) {
+      const int eid = ord_s[lane];
+      sel_ids_s[lane] = eid;
+      sel_g_s[lane] = pp_sigmoid(lg_s[eid]);
+    }
+    if (lane == 0) k_s = k;
+  }
+  __syncthreads();
+  const int k = k_s;
+  if (b == 0) {  // telemetry for the caller
+    if (tid < 16) st_rlx(&st->logits[tid], lg_s[tid]);
+    if (tid < k) {
+      st_rlx(&st->sel_ids[tid], sel_ids_s[tid]);
+      st_rlx(&st->sel_gates[tid], sel_g_s[tid]);
+    }
+    if (tid == 0) st_rlx(&st->k, k);
+  }
+
+  // ---- stream the selected neuron records (as decode_kernel)
+  const int T = k * G;
+  const int v0 = (int)((int64_t)T * b / W), v1 = (int)((int64_t)T * (b + 1) / W);
+  const int n = v1 - v0;
+  int r = v0 + (n * wv) / NW;
+  const int r_end = v0 + (n * (wv + 1)) / NW;
+  float xr[CPL][8];
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) load_x8<XT>(x, lane + 64 * c, xr[c], true);
+  float oacc[CPL][8];
+#pragma unroll
+  for (int c = 0; c < CPL; ++c)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) oacc[c][i] = 0.0f;
+  uint4 gq[CPL], uq[CPL], dq[CPL];
+  int s_cur = 0, g_cur = 0;
+  if (r < r_end) {
+    s_cur = r / G;
+    g_cur = r - s_cur * G;
+    const uint4* rec = (const uint4*)(rows + ((int64_t)sel_ids_s[s_cur] * G + g_cur) * 3 * H);
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+      gq[c] = rec[lane + 64 * c];
+      uq[c] = rec[HC + lane + 64 * c];
+      dq[c] = rec[2 * HC + lane + 64 * c];
+    }
+  }
+  for (; r < r_end; ++r) {
+    uint4 g2[CPL], u2[CPL], d2[CPL];
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) { g2[c] = gq[c]; u2[c] = uq[c]; d2[c] = dq[c]; }
+    const float gwt = sel_g_s[s_cur];
+    if (r + 1 < r_end) {
+      if (++g_cur == G) { g_cur = 0; ++s_cur; }
+      const uint4* rec = (const uint4*)(rows + ((int64_t)sel_ids_s[s_cur] * G + g_cur) * 3 * H);
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) {
+        gq[c] = rec[lane + 64 * c];
+        uq[c] = rec[HC + lane + 64 * c];
+        dq[c] = rec[2 * HC + lane + 64 * c];
+      }
+    }
+    float gs = 0.0f, us = 0.0f;
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+      gs += dot8(g2[c], xr[c]);
+      us += dot8(u2[c], xr[c]);
+    }
+    gs = wave_sum(gs);
+    us = wave_sum(us);
+    const float av = pp_silu(gs) * us * gwt;
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) axpy8(av, d2[c], oacc[c]);
+  }
+
+  // ---- workgroup reduction -> one of DEC_NCOPY fp32 accumulators
+  // waves 1..NW-1 park partials in LDS, wave 0 adds its own into slot 0, then every
+  // thread folds the slots in order for contiguous h and adds to the copy
+  if (n > 0) {
+    if (wv > 0) {
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) {
+        float4* dst = (float4*)(red + (wv - 1) * H + (lane + 64 * c) * 8);
+        dst[0] = make_float4(oacc[c][0], oacc[c][1], oacc[c][2], oacc[c][3]);
+        dst[1] = make_float4(oacc[c][4], oacc[c][5], oacc[c][6], oacc[c][7]);
+      }
+    }
+    __syncthreads();
+    if (wv == 0) {
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) {
+        float* dst = red + (lane + 64 * c) * 8;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) dst[i] = oacc[c][i] + dst[i];
+      }
+    }
+    __syncthreads();
+    float* accc = acc + (b % DEC_NCOPY) * H;
+#pragma unroll
+    for (int i = 0; i < (H + NT - 1) / NT; ++i) {
+      const int h = tid + NT * i;
+      if (h < H) {
+        float v = red[h];
+#pragma unroll
+        for (int w = 1; w < NW - 1; ++w) v += red[w * H + h];
+        unsafeAtomicAdd(accc + h, v);
+      }
+    }
+  }
+  vm_wait();  // every wave's accumulator atomics are performed before the ticket
+  __syncthreads();
+  if (tid == 0) flag_s = add_rlx(&st->done, 1u) == (uint32_t)(W - 1);
+  __syncthreads();
+  if (flag_s) {  // last workgroup: fold copies, write bf16, clear, reset the counter
+    // every load of the fold is issued before the first add (one round trip)
+    constexpr int HPT = (H + NT - 1) / NT;
+    float sv[HPT][DEC_NCOPY];
+#pragma unroll
+    for (int i = 0; i < HPT; ++i)
+#pragma unroll
+      for (int c = 0; c < DEC_NCOPY; ++c) {
+        const int h = tid + NT * i;
+        sv[i][c] = h < H ? ld_rlx(acc + c * H + h) : 0.0f;
+      }
+#pragma unroll
+    for (int i = 0; i < HPT; ++i) {
+      const int h = tid + NT * i;
+      if (h < H) {
+        float tot = 0.0f;
+#pragma unroll
+        for (int c = 0; c < DEC_NCOPY; ++c) tot += sv[i][c];
+#pragma unroll
+        for (int c = 0; c < DEC_NCOPY; ++c) st_rlx(acc + c * H + h, 0.0f);
+        out[h] = f32_to_bf16(tot);
+      }
+    }
+    if (tid == 0) st_rlx(&st->done, 0u);
+  }
+}
+
+__global__ void decode_ws_clear_kernel(uint32_t* p, size_t n_words) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n_words; i += (size_t)gridDim.x * blockDim.x)
+    p[i] = 0u;
+}
+
+extern "C" size_t pp_decode_workspace_bytes(int H, int E) {
+  (void)E;
+  return dec_acc_offset() + (size_t)DEC_NCOPY * H * sizeof(float);
+}
+
+extern "C" int pp_decode_workspace_init(void* workspace, int H, int E, void* stream) {
+  int rc = pp_check_shape(H, E, 32);
+  if (rc) return rc;
+  PP_REQUIRE(workspace, PP_ERR_INVALID, "pp_decode_workspace_init: null workspace");
+  size_t words = pp_decode_workspace_bytes(H, E) / 4;
+  decode_ws_clear_kernel<<<64, 256, 0, (hipStream_t)stream>>>((uint32_t*)workspace, words);
+  return pp_check_launch("pp_decode_workspace_init");
+}
+
+template <typename XT, bool LOCAL>
+static void launch_decode(int cpl, int grid, size_t smem, hipStream_t s, const XT* x, int H, const float* router,
+                          const float* bias, int E, int G, float tau, const bf16_t* rows, bf16_t* out,
+                          pp_decode_state* st, float* acc, int R) {
+#define PP_DEC_CASE(C)                                                                                  \
+  case C:                                                                                               \
+    decode_kernel<XT, C, LOCAL><<<grid, DEC_THREADS, smem, s>>>(x, H, router, bias, E, G, tau, rows, out, st, \
+                                                                acc, R);                                \
+    break;
+  switch (cpl) {
+    PP_DEC_CASE(1)
+    PP_DEC_CASE(2)
+    PP_DEC_CASE(3)
+    PP_DEC_CASE(4)
+    PP_DEC_CASE(5)
+    PP_DEC_CASE(6)
+    PP_DEC_CASE(7)
+    PP_DEC_CASE(8)
+  }
+#undef PP_DEC_CASE
+}
+
+extern "C" int pp_moe_decode(const void* x, int x_dtype, int H, const float* router_packed, const float* bias,
+                             int E, int G, float tau, const void* packed, void* out_bf16, void* workspace,
+                             int grid, void* stream) {
+  int rc = pp_check_shape(H, E, G);
+  if (rc) return rc;
+  PP_REQUIRE(x && router_packed && packed && out_bf16 && workspace, PP_ERR_INVALID,
+             "pp_moe_decode: null pointer");
+  PP_REQUIRE(x_dtype == PP_DTYPE_F32 || x_dtype == PP_DTYPE_BF16, PP_ERR_INVALID, "pp_moe_decode: x_dtype %d",
+             x_dtype);
+  PP_REQUIRE(grid >= 0 && grid <= 65536, PP_ERR_INVALID, "pp_moe_decode: grid %d", grid);
+  const int grid_in = grid;
+  const int R = E < 64 ? E : 64;
+  if (grid == 0) grid = 2 * pp_device_cus();
+  if (grid < R) grid = R;
+  const int cpl = (H / 8 + 63) / 64;  // 16-byte chunks per lane per row (H <= 4096 -> <= 8)
+  const size_t smem = (size_t)3 * H * sizeof(float);
+  pp_decode_state* st = (pp_decode_state*)workspace;
+  float* acc = (float*)((char*)workspace + dec_acc_offset());
+  hipStream_t s = (hipStream_t)stream;
+  if (E == 16 && H % 512 == 0) {
+    const int c = H / 512;
+    const size_t smem16 = (size_t)(DEC16_NW - 1) * H * sizeof(float);
+    if (grid_in == 0) grid = pp_device_cus() / 2;  // measured best: one 8-wave workgroup per two CUs
+#define PP_DEC16_CASE(C)                                                                                     \
+  case C:                                                                                                    \
+    if (x_dtype == PP_DTYPE_F32)                                                                             \
+      decode16_kernel<float, C, DEC16_NW><<<grid, 64 * DEC16_NW, smem16, s>>>((const float*)x, router_packed, bias, G, tau, \
+                                                               (const bf16_t*)packed, (bf16_t*)out_bf16, st, acc); \
+    else                                                                                                     \
+      decode16_kernel<bf16_t, C, DEC16_NW><<<grid, 64 * DEC16_NW, smem16, s>>>((const bf16_t*)x, router_packed, bias, G, tau, \
+                                                                (const bf16_t*)packed, (bf16_t*)out_bf16, st, acc); \
+    break;
+    switch (c) {
+      PP_DEC16_CASE(1)
+      PP_DEC16_CASE(2)
+      PP_DEC16_CASE(3)
+      PP_DEC16_CASE(4)
+      PP_DEC16_CASE(5)
+      PP_DEC16_CASE(6)
+      PP_DEC16_CASE(7)
+      PP_DEC16_CASE(8)
+    }
+#undef PP_DEC16_CASE
+    return pp_check_launch("pp_moe_decode");
+  }
+  const bool local = E <= 16 && (int64_t)16 * H <= DEC_LOCAL_ROUTER_FLOATS;
+  const bf16_t* rows = (const bf16_t*)packed;
+  bf16_t* o = (bf16_t*)out_bf16;
+  if (x_dtype == PP_DTYPE_F32) {
+    if (local) launch_decode<float, true>(cpl, grid, smem, s, (const float*)x, H, router_packed, bias, E, G, tau, rows, o, st, acc, R);
+    else launch_decode<float, false>(cpl, grid, smem, s, (const float*)x, H, router_packed, bias, E, G, tau, rows, o, st, acc, R);
+  } else {
+    if (local) launch_decode<bf16_t, true>(cpl, grid, smem, s, (const bf16_t*)x, H, router_packed, bias, E, G, tau, rows, o, st, acc, R);
+    else launch_decode<bf16_t, false>(cpl, grid, smem, s, (const bf16_t*)x, H, router_packed, bias, E, G, tau, rows, o, st, acc, R);
+  }
+  return pp_check_launch("pp_moe_decode");
+}

@@ -1,0 +1,489 @@
+// Shared device helpers for the PrunePath MoE kernels (gfx950, wave64).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/prunepath_moe.h"
+
+#define PP_WAVE 64
+
+typedef uint16_t bf16_t;
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
+typedef __attribute__((ext_vector_type(4))) float f32x4_t;
+typedef __attribute__((ext_vector_type(16))) float f32x16_t;
+
+// ---------------------------------------------------------------- errors (host)
+void pp_set_error(const char* fmt, ...);
+int pp_check_launch(const char* what);
+
+#define PP_REQUIRE(cond, code, ...)          \
+  do {                                       \
+    if (!(cond)) {                           \
+      pp_set_error(__VA_ARGS__);             \
+      return (code);                         \
+    }                                        \
+  } while (0)
+
+// Shape limits shared by every entry point.
+static inline int pp_check_shape(int H, int E, int G) {
+  PP_REQUIRE(H >= 128 && H <= 4096 && H % 128 == 0, PP_ERR_UNSUPPORTED,
+             "hidden size H=%d unsupported (need 128 <= H <= 4096, H %% 128 == 0)", H);
+  PP_REQUIRE(E >= 1 && E <= PP_MAX_EXPERTS, PP_ERR_UNSUPPORTED, "num_experts E=%d unsupported (1..256)", E);
+  PP_REQUIRE(G >= 32 && G % 32 == 0 && G <= 8192, PP_ERR_UNSUPPORTED,
+             "group size G=%d unsupported (need G %% 32 == 0, 32 <= G <= 8192)", G);
+  return PP_OK;
+}
+
+int pp_device_cus();
+
+// ---------------------------------------------------------------- bf16
+__device__ __forceinline__ float bf16_to_f32(bf16_t v) {
+  return __uint_as_float(((uint32_t)v) << 16);
+}
+
+// Round to nearest even, NaN kept quiet (the rounding torch uses for .to(bfloat16)).
+__device__ __forceinline__ bf16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (bf16_t)((u >> 16) | 0x40);
+  uint32_t lsb = (u >> 16) & 1u;
+  u += 0x7fffu + lsb;
+  return (bf16_t)(u >> 16);
+}
+
+__host__ __device__ __forceinline__ int pp_ceil_div(int a, int b) { return (a + b - 1) / b; }
+
+// Load one input element as fp32 (input dtype: fp32 or bf16).
+template <typename XT>
+__device__ __forceinline__ float load_as_f32(const XT* p, int64_t i);
+template <>
+__device__ __forceinline__ float load_as_f32<float>(const float* p, int64_t i) { return p[i]; }
+template <>
+__device__ __forceinline__ float load_as_f32<bf16_t>(const bf16_t* p, int64_t i) {
+  return bf16_to_f32(p[i]);
+}
+
+// ---------------------------------------------------------------- wave reductions
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, PP_WAVE);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, PP_WAVE));
+  return v;
+}
+
+// ---------------------------------------------------------------- torch-CPU exp / sigmoid
+// SLEEF expf_u10, FMA form (Shibata & Petrogalli, "SLEEF", IEEE TPDS 2020; the
+// routine torch's AVX512 Vectorized<float>::exp() calls). Every step is one IEEE
+// fp32 operation, so the result is bit-identical to the CPU.
+__device__ __forceinline__ float pp_pow2i(int q) { return __uint_as_float((uint32_t)(q + 0x7f) << 23); }
+
+__device__ __forceinline__ float pp_expf_u10(float d) {
+  const float R_LN2f = 1.442695040888963407359924681001892137426645954152985934135449406931f;
+  const float L2Uf = 0.693145751953125f;
+  const float L2Lf = 1.428606765330187045e-06f;
+  float t = __fmul_rn(d, R_LN2f);
+  int q = (int)__builtin_rintf(t);
+  float s = __builtin_fmaf((float)q, -L2Uf, d);
+  s = __builtin_fmaf((float)q, -L2Lf, s);
+  float u = 0.000198527617612853646278381f;
+  u = __builtin_fmaf(u, s, 0.00139304355252534151077271f);
+  u = __builtin_fmaf(u, s, 0.00833336077630519866943359f);
+  u = __builtin_fmaf(u, s, 0.0416664853692054748535156f);
+  u = __builtin_fmaf(u, s, 0.166666671633720397949219f);
+  u = __builtin_fmaf(u, s, 0.5f);
+  float ss = __fmul_rn(s, s);
+  u = __fadd_rn(1.0f, __builtin_fmaf(ss, u, s));
+  int qh = q >> 1;
+  u = __fmul_rn(__fmul_rn(u, pp_pow2i(qh)), pp_pow2i(q - qh));
+  if (d < -104.0f) u = 0.0f;
+  if (d > 104.0f) u = __builtin_huge_valf();
+  if (d != d) u = d;
+  return u;
+}
+
+// torch CPU sigmoid for fp32: reciprocal(exp(0 - x) + 1).
+__device__ __forceinline__ float pp_sigmoid(float x) {
+  float e = pp_expf_u10(__fsub_rn(0.0f, x));
+  return __fdiv_rn(1.0f, __fadd_rn(e, 1.0f));
+}
+
+// Fast SiLU for the expert activations (not part of the bit-exact routing).
+__device__ __forceinline__ float pp_silu(float g) { return g / (1.0f + __expf(-g)); }
+
+// ---------------------------------------------------------------- selection
+// Scratch for one token's selection, in LDS, used by one wave.
+struct SelScratch {
+  float e[PP_MAX_EXPERTS];     // exp values, then probabilities
+  float srt[PP_MAX_EXPERTS];   // probabilities in sorted order
+  int order[PP_MAX_EXPERTS];   // expert id at each rank
+  uint8_t sel[PP_MAX_EXPERTS]; // per expert: selected flag (filled by callers)
+  int stk[3 * 24];             // introsort range stack (tie path only)
+  int k;                       // number of selected experts
+  int tie;                     // a tie group straddles the selection boundary
+};
+
+// Descending comparator of torch's CPU sort on (value, index) pairs (NaN first).
+__device__ __forceinline__ bool kv_before(float a, float b) {
+  return (a != a && b == b) || a > b;
+}
+
+// torch CPU sort order for E > 16: libstdc++ std::sort (introsort) of
+// (value, index) pairs, restated from the published algorithm (bits/stl_algo.h,
+// bits/stl_heap.h): median-of-three pivot moved to the front, unguarded
+// partition while a range holds more than 16 elements, heapsort once the depth
+// limit 2*floor(log2 n) is used up, then a final insertion sort. Run by one
+// lane on the rare tokens whose selection boundary cuts through equal values.
+static __device__ void kv_adjust_heap(float* K, int* V, int hole, int len, float vk, int vv) {
+  int top = hole, sc = hole;
+  while (sc < (len - 1) / 2) {
+    sc = 2 * (sc + 1);
+    if (kv_before(K[sc], K[sc - 1])) sc--;
+    K[hole] = K[sc]; V[hole] = V[sc];
+    hole = sc;
+  }
+  if ((len & 1) == 0 && sc == (len - 2) / 2) {
+    sc = 2 * (sc + 1);
+    K[hole] = K[sc - 1]; V[hole] = V[sc - 1];
+    hole = sc - 1;
+  }
+  int parent = (hole - 1) / 2;
+  while (hole > top && kv_before(K[parent], vk)) {
+    K[hole] = K[parent]; V[hole] = V[parent];
+    hole = parent;
+    parent = (hole - 1) / 2;
+  }
+  K[hole] = vk; V[hole] = vv;
+}
+
+static __device__ void kv_heapsort(float* K, int* V, int len) {
+  if (len >= 2) {
+    for (int parent = (len - 2) / 2;; --parent) {
+      kv_adjust_heap(K, V, parent, len, K[parent], V[parent]);
+      if (parent == 0) break;
+    }
+  }
+  for (int last = len; last > 1;) {
+    --last;
+    float vk = K[last]; int vv = V[last];
+    K[last] = K[0]; V[last] = V[0];
+    kv_adjust_heap(K, V, 0, last, vk, vv);
+  }
+}
+
+static __device__ void kv_linear_insert(float* K, int* V, int last) {
+  float vk = K[last]; int vv = V[last];
+  int nxt = last - 1;
+  while (kv_before(vk, K[nxt])) {
+    K[last] = K[nxt]; V[last] = V[nxt];
+    last = nxt; --nxt;
+  }
+  K[last] = vk; V[last] = vv;
+}
+
+static __device__ void kv_introsort(float* K, int* V, int n, int* stk) {
+  int lg = 0;
+  while ((2 << lg) <= n) ++lg;
+  int* stf = stk;
+  int* stl = stk + 24;
+  int* stdp = stk + 48;
+  int sp = 0;
+  stf[0] = 0; stl[0] = n; stdp[0] = 2 * lg; sp = 1;
+  while (sp > 0) {
+    --sp;
+    int f = stf[sp], l = stl[sp], depth = stdp[sp];
+    while (l - f > 16) {
+      if (depth == 0) { kv_heapsort(K + f, V + f, l - f); break; }
+      --depth;
+      int mid = f + (l - f) / 2, a = f + 1, b = mid, c = l - 1, s;
+      if (kv_before(K[a], K[b])) {
+        if (kv_before(K[b], K[c])) s = b;
+        else if (kv_before(K[a], K[c])) s = c;
+        else s = a;
+      } else if (kv_before(K[a], K[c])) s = a;
+      else if (kv_before(K[b], K[c])) s = c;
+      else s = b;
+      { float tk = K[f]; K[f] = K[s]; K[s] = tk; int tv = V[f]; V[f] = V[s]; V[s] = tv; }
+      int lo = f + 1, hi = l;
+      for (;;) {
+        while (kv_before(K[lo], K[f])) ++lo;
+        --hi;
+        while (kv_before(K[f], K[hi])) --hi;
+        if (!(lo < hi)) break;
+        { float tk = K[lo]; K[lo] = K[hi]; K[hi] = tk; int tv = V[lo]; V[lo] = V[hi]; V[hi] = tv; }
+        ++lo;
+      }
+      // each pass pushes at most one frame and the depth drops by one per frame
+      // (2*floor(log2 256) = 16 levels), so 24 entries are never exceeded
+      stf[sp] = lo; stl[sp] = l; stdp[sp] = depth; ++sp;
+      l = lo;
+    }
+  }
+  // final insertion sort: guarded over the first 16, unguarded after
+  int head = n < 16 ? n : 16;
+  for (int i = 1; i < head; ++i) {
+    if (kv_before(K[i], K[0])) {
+      float vk = K[i]; int vv = V[i];
+      for (int j = i; j > 0; --j) { K[j] = K[j - 1]; V[j] = V[j - 1]; }
+      K[0] = vk; V[0] = vv;
+    } else {
+      kv_linear_insert(K, V, i);
+    }
+  }
+  for (int i = 16; i < n; ++i) kv_linear_insert(K, V, i);
+}
+
+// Selection for one token, executed by all 64 lanes of one wave.
+// Input: logits read through `lg(j)` for j < E. Output in `ss`: probabilities in
+// ss->e, rank order in ss->order, ss->k selected experts (ranks 0..k-1).
+// The caller must provide an LDS SelScratch private to this wave.
+// Steps follow torch CPU fp32 (softmax_thresholding, src/MoEBlock_origin.py:70-88):
+//   max; e = expf_u10(x - max); sum in vec::reduce_all order; p = e * (1/sum);
+//   descending sort (stable for E <= 16, introsort ties otherwise); fp64 running
+//   sum rounded to fp32 at each rank; keep ranks with cum < tau; keep rank 0.
+__device__ __forceinline__ void wave_sync_lds() {
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// fp64 running sum of the sorted probabilities, rounded to fp32 at each rank;
+// returns the number of leading ranks with cum < tau (at least 1). `sv(q)` gives the
+// q-th largest probability; evaluated identically by every lane.
+template <typename SV>
+__device__ __forceinline__ int tau_cut(SV sv, int E, float tau) {
+  const float tau32 = tau;
+  double a = 0.0;
+  int k = 0;
+  bool stop = false;
+  for (int q0 = 0; q0 < E && !stop; q0 += 8) {
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = (q0 + i < E) ? sv(q0 + i) : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if (!stop && q0 + i < E) {
+        a += (double)v[i];
+        if ((float)a < tau32) k = q0 + i + 1;
+        else stop = true;
+      }
+    }
+  }
+  return k == 0 ? 1 : k;
+}
+
+// Selection for E <= EMAX (16 or 64): every lane keeps all E exp values in registers
+// (read back from LDS with 16-byte broadcast reads), so the row sum, the probabilities
+// and the fp64 running sum need no cross-lane shuffles; ranks are computed per lane
+// and scattered through LDS. Same arithmetic, in the same order, as the general path.
+template <int EMAX, typename LG>
+static __device__ void select_small(LG lg, int E, float tau, SelScratch* ss, int lane) {
+  const bool act = lane < E;
+  const float x = act ? lg(lane) : -__builtin_huge_valf();
+  const float m = wave_max(x);
+  const float e = act ? pp_expf_u10(__fsub_rn(x, m)) : 0.0f;
+  if (lane < EMAX) ss->e[lane] = act ? e : 0.0f;
+  wave_sync_lds();
+  float ev[EMAX];
+#pragma unroll
+  for (int i = 0; i < EMAX / 4; ++i) {
+    const float4 v = *(const float4*)&ss->e[4 * i];
+    ev[4 * i] = v.x; ev[4 * i + 1] = v.y; ev[4 * i + 2] = v.z; ev[4 * i + 3] = v.w;
+  }
+  // row sum in torch vec::reduce_all order (16 float lanes)
+  float S;
+  if (E < 16) {
+    S = ev[0];
+#pragma unroll
+    for (int j = 1; j < (EMAX < 16 ? EMAX : 16); ++j)
+      if (j < E) S = __fadd_rn(S, ev[j]);
+  } else {
+    float a[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) a[i] = ev[i];
+    const int full_end = E - (E % 16);
+#pragma unroll
+    for (int d = 16; d < EMAX; d += 16) {
+      if (d < full_end) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) a[i] = __fadd_rn(a[i], ev[d + i]);
+      } else if (d == full_end && E - d > 0) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          if (i < E - d) a[i] = __fadd_rn(a[i], ev[d + i]);
+      }
+    }
+#pragma unroll
+    for (int st = 8; st >= 1; st >>= 1)
+#pragma unroll
+      for (int i = 0; i < st; ++i) a[i] = __fadd_rn(a[i], a[i + st]);
+    S = a[0];
+  }
+  const float r = __fdiv_rn(1.0f, S);
+  const float p = act ? __fmul_rn(e, r) : 0.0f;
+  int rank = 0;
+#pragma unroll
+  for (int q = 0; q < EMAX; ++q) {
+    const float pq = __fmul_rn(ev[q], r);
+    rank += (q < E && (kv_before(pq, p) || (pq == p && q < lane))) ? 1 : 0;
+  }
+  wave_sync_lds();
+  if (act) {
+    ss->e[lane] = p;
+    ss->srt[rank] = p;
+    ss->order[rank] = lane;
+  }
+  wave_sync_lds();
+  float sv[EMAX];
+#pragma unroll
+  for (int i = 0; i < EMAX / 4; ++i) {
+    const float4 v = *(const float4*)&ss->srt[4 * i];
+    sv[4 * i] = v.x; sv[4 * i + 1] = v.y; sv[4 * i + 2] = v.z; sv[4 * i + 3] = v.w;
+  }
+  const float tau32 = tau;
+  double acc = 0.0;
+  int k = 0;
+  bool stop = false;
+#pragma unroll
+  for (int q = 0; q < EMAX; ++q) {
+    if (!stop && q < E) {
+      acc += (double)sv[q];
+      if ((float)acc < tau32) k = q + 1;
+      else stop = true;
+    }
+  }
+  if (k == 0) k = 1;
+  bool tie = false;
+#pragma unroll
+  for (int q = 1; q < EMAX; ++q)
+    if (q == k && E > 16 && k < E) tie = sv[q - 1] == sv[q];
+  if (lane == 0) {
+    ss->k = k;
+    ss->tie = tie ? 1 : 0;
+    if (tie) {
+      for (int j = 0; j < E; ++j) { ss->srt[j] = ss->e[j]; ss->order[j] = j; }
+      kv_introsort(ss->srt, ss->order, E, ss->stk);
+    }
+  }
+  wave_sync_lds();
+}
+
+template <typename LG>
+static __device__ void select_one_token(LG lg, int E, float tau, SelScratch* ss, int lane) {
+  if (E <= 16) {
+    select_small<16>(lg, E, tau, ss, lane);
+    return;
+  }
+  if (E <= PP_WAVE) {
+    // ---- one expert per lane, exchanges through cross-lane shuffles
+    const bool act = lane < E;
+    const float x = act ? lg(lane) : -__builtin_huge_valf();
+    const float m = wave_max(x);
+    const float e = act ? pp_expf_u10(__fsub_rn(x, m)) : 0.0f;
+    float S;
+    if (E < 16) {
+      float acc = __shfl(e, 0, PP_WAVE);
+      for (int j = 1; j < E; ++j) acc = __fadd_rn(acc, __shfl(e, j, PP_WAVE));
+      S = acc;
+    } else {
+      const int li = lane & 15;
+      float acc = __shfl(e, li, PP_WAVE);
+      const int full_end = E - (E % 16);
+      int d = 16;
+      for (; d < full_end; d += 16) acc = __fadd_rn(acc, __shfl(e, d + li, PP_WAVE));
+      if (E - d > 0) {
+        const float t = __shfl(e, (d + li) & 63, PP_WAVE);
+        if (li < E - d) acc = __fadd_rn(acc, t);
+      }
+#pragma unroll
+      for (int o = 8; o >= 1; o >>= 1) acc = __fadd_rn(acc, __shfl_xor(acc, o, PP_WAVE));
+      S = __shfl(acc, 0, PP_WAVE);
+    }
+    const float p = act ? __fmul_rn(e, __fdiv_rn(1.0f, S)) : 0.0f;
+    int rank = 0;
+    for (int q = 0; q < E; ++q) {
+      const float pq = __shfl(p, q, PP_WAVE);
+      rank += (kv_before(pq, p) || (pq == p && q < lane)) ? 1 : 0;
+    }
+    if (act) {
+      ss->e[lane] = p;
+      ss->srt[rank] = p;
+      ss->order[rank] = lane;
+    }
+    wave_sync_lds();
+    const float mine = act ? ss->srt[lane] : 0.0f;  // lane q holds the q-th largest
+    const int k = tau_cut([&](int q) { return __shfl(mine, q, PP_WAVE); }, E, tau);
+    const bool tie = E > 16 && k < E && __shfl(mine, k - 1, PP_WAVE) == __shfl(mine, k & 63, PP_WAVE);
+    if (lane == 0) {
+      ss->k = k;
+      ss->tie = tie ? 1 : 0;
+      if (tie) {
+        // exact torch order for the tie group: (value, index) pairs in index order,
+        // then the introsort restatement
+        for (int j = 0; j < E; ++j) { ss->srt[j] = ss->e[j]; ss->order[j] = j; }
+        kv_introsort(ss->srt, ss->order, E, ss->stk);
+      }
+    }
+    wave_sync_lds();
+    return;
+  }
+  // ---- general path (E > 64): values in LDS
+  float m = -__builtin_huge_valf();
+  for (int j = lane; j < E; j += PP_WAVE) m = fmaxf(m, lg(j));
+  m = wave_max(m);
+  for (int j = lane; j < E; j += PP_WAVE) ss->e[j] = pp_expf_u10(__fsub_rn(lg(j), m));
+  wave_sync_lds();
+  float acc = 0.0f;
+  if (lane < 16) {
+    acc = ss->e[lane];
+    int full_end = E - (E % 16);
+    int d = 16;
+    for (; d < full_end; d += 16) acc = __fadd_rn(acc, ss->e[d + lane]);
+    if (E - d > 0 && lane < E - d) acc = __fadd_rn(acc, ss->e[d + lane]);
+  }
+#pragma unroll
+  for (int o = 8; o >= 1; o >>= 1) acc = __fadd_rn(acc, __shfl_xor(acc, o, PP_WAVE));
+  const float S = __shfl(acc, 0, PP_WAVE);
+  const float r = __fdiv_rn(1.0f, S);
+  float pv[PP_MAX_EXPERTS / PP_WAVE];
+#pragma unroll
+  for (int i = 0; i < PP_MAX_EXPERTS / PP_WAVE; ++i) {
+    int j = lane + i * PP_WAVE;
+    pv[i] = j < E ? __fmul_rn(ss->e[j], r) : 0.0f;
+  }
+  wave_sync_lds();
+#pragma unroll
+  for (int i = 0; i < PP_MAX_EXPERTS / PP_WAVE; ++i) {
+    int j = lane + i * PP_WAVE;
+    if (j < E) ss->e[j] = pv[i];
+  }
+  wave_sync_lds();
+#pragma unroll
+  for (int i = 0; i < PP_MAX_EXPERTS / PP_WAVE; ++i) {
+    int j = lane + i * PP_WAVE;
+    if (j < E) {
+      float pj = pv[i];
+      int rank = 0;
+      for (int q = 0; q < E; ++q) {
+        float pq = ss->e[q];
+        rank += (kv_before(pq, pj) || (pq == pj && q < j)) ? 1 : 0;
+      }
+      ss->srt[rank] = pj;
+      ss->order[rank] = j;
+    }
+  }
+  wave_sync_lds();
+  if (lane == 0) {
+    const int k = tau_cut([&](int q) { return ss->srt[q]; }, E, tau);
+    ss->k = k;
+    const int tie = (k < E && ss->srt[k - 1] == ss->srt[k]) ? 1 : 0;
+    if (tie) {
+      for (int j = 0; j < E; ++j) { ss->srt[j] = ss->e[j]; ss->order[j] = j; }
+      kv_introsort(ss->srt, ss->order, E, ss->stk);
+    }
+    ss->tie = tie;
+  }
+  wave_sync_lds();
+}

@@ -1,0 +1,334 @@
+"""Torch-level entry points over the C ABI (include/prunepath_moe.h).
+
+PyTorch only provides device memory and the current HIP stream here: every
+function checks shapes/devices, allocates its outputs with torch and calls the
+hand-written gfx950 kernels through ctypes. All work is enqueued on
+``torch.cuda.current_stream()``; nothing synchronises with the host, so the calls
+can be captured in a CUDA (HIP) graph.
+
+The same functions are registered as ``torch.library`` ops in the ``prunepath``
+namespace (``torch.ops.prunepath.route`` etc.) at the bottom of this file.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Optional
+
+import torch
+
+from . import _lib as L
+
+
+def _vp(t: Optional[torch.Tensor]):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
+
+
+def _stream(t: torch.Tensor):
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _need_gpu(name: str, *ts: Optional[torch.Tensor]) -> None:
+    dev = None
+    for t in ts:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise RuntimeError(f"prunepath.{name}: tensors must be on the GPU (got {t.device}); "
+                               "there is no CPU implementation")
+        if not t.is_contiguous():
+            raise RuntimeError(f"prunepath.{name}: tensors must be contiguous")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise RuntimeError(f"prunepath.{name}: tensors on different devices ({dev}, {t.device})")
+
+
+def _x_dtype(x: torch.Tensor):
+    """(tensor, PP dtype code) -- bf16 and fp32 pass through, other floats go to fp32."""
+    if x.dtype == torch.bfloat16:
+        return x, L.PP_DTYPE_BF16
+    if x.dtype == torch.float32:
+        return x, L.PP_DTYPE_F32
+    if x.is_floating_point():
+        return x.float(), L.PP_DTYPE_F32
+    raise RuntimeError(f"prunepath: unsupported input dtype {x.dtype}")
+
+
+def _src_dtype(t: torch.Tensor):
+    if t.dtype == torch.float32:
+        return L.PP_DTYPE_F32
+    if t.dtype == torch.bfloat16:
+        return L.PP_DTYPE_BF16
+    raise RuntimeError(f"prunepath: weights must be float32 or bfloat16, got {t.dtype}")
+
+
+# ----------------------------------------------------------------------------- rearrangement
+def packed_expert_numel(H: int, E: int, G: int) -> int:
+    return int(L.lib().pp_packed_expert_bytes(H, E, G)) // 2
+
+
+def pack_experts(w_gate: torch.Tensor, w_up: torch.Tensor, w_down: torch.Tensor, E: int, G: int,
+                 perm: Optional[torch.Tensor] = None, layout: str = "linear",
+                 out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """One-time physical rearrangement (physical_reorder_for_inference,
+    src/openpangu_moe.py:212-256) into the packed bf16 expert buffer.
+
+    layout="linear": nn.Linear weights, gate/up [I,H], down [H,I].
+    layout="tau":    TauSparseMoE buffers, W_gate/W_up [H,I], W_down [I,H].
+    perm[j] (int32, device) = source neuron of rearranged neuron j (None = identity).
+    """
+    if layout == "linear":
+        I, H = w_gate.shape
+        s_n, s_h, d_n, d_h = H, 1, 1, I
+        assert w_down.shape == (H, I)
+    elif layout == "tau":
+        H, I = w_gate.shape
+        s_n, s_h, d_n, d_h = 1, I, H, 1
+        assert w_down.shape == (I, H)
+    else:
+        raise ValueError(f"layout {layout!r}")
+    if w_up.shape != w_gate.shape or w_up.dtype != w_gate.dtype or w_down.dtype != w_gate.dtype:
+        raise RuntimeError("prunepath.pack_experts: gate/up/down shapes or dtypes disagree")
+    if I != E * G:
+        raise RuntimeError(f"prunepath.pack_experts: I={I} != E*G={E * G}")
+    if perm is not None:
+        if perm.dtype != torch.int32 or perm.numel() != I:
+            raise RuntimeError("prunepath.pack_experts: perm must be int32 [I]")
+    _need_gpu("pack_experts", w_gate, w_up, w_down, perm)
+    n = packed_expert_numel(H, E, G)
+    if out is None:
+        out = torch.empty(n, dtype=torch.bfloat16, device=w_gate.device)
+    elif out.numel() != n or out.dtype != torch.bfloat16:
+        raise RuntimeError("prunepath.pack_experts: bad out buffer")
+    rc = L.lib().pp_pack_experts(_vp(w_gate), _vp(w_up), s_n, s_h, _vp(w_down), d_n, d_h,
+                                 _src_dtype(w_gate), _vp(perm), H, E, G, _vp(out), _stream(w_gate))
+    L.check(rc, "pack_experts")
+    return out
+
+
+def pack_router(w_router: torch.Tensor, layout: str = "linear") -> torch.Tensor:
+    """Router weights to fp32 [Epad, H] (Epad = E rounded up to 16, zero rows).
+    layout="linear": MoELayer router weight [E,H]; layout="tau": TauSparseMoE.router [H,E]."""
+    if layout == "linear":
+        E, H = w_router.shape
+        s_e, s_h = H, 1
+    elif layout == "tau":
+        H, E = w_router.shape
+        s_e, s_h = 1, E
+    else:
+        raise ValueError(f"layout {layout!r}")
+    _need_gpu("pack_router", w_router)
+    Epad = (E + 15) // 16 * 16
+    out = torch.empty(Epad, H, dtype=torch.float32, device=w_router.device)
+    rc = L.lib().pp_pack_router(_vp(w_router), s_e, s_h, _src_dtype(w_router), H, E, _vp(out),
+                                _stream(w_router))
+    L.check(rc, "pack_router")
+    return out
+
+
+# ----------------------------------------------------------------------------- routing
+def route(x: torch.Tensor, router_packed: torch.Tensor, E: int, tau: float,
+          bias: Optional[torch.Tensor] = None, want_logits: bool = True, want_probs: bool = False):
+    """fp32 router + tau selection for x [N,H]. Returns dict with gates [N,E] fp32,
+    mask [N,E] uint8, count [N] int32 and optionally logits / probs [N,E] fp32."""
+    x, xd = _x_dtype(x)
+    N, H = x.shape
+    if bias is not None and (bias.dtype != torch.float32 or bias.numel() != E):
+        raise RuntimeError("prunepath.route: bias must be float32 [E]")
+    _need_gpu("route", x, router_packed, bias)
+    dev = x.device
+    res = {
+        "gates": torch.empty(N, E, dtype=torch.float32, device=dev),
+        "mask": torch.empty(N, E, dtype=torch.uint8, device=dev),
+        "count": torch.empty(N, dtype=torch.int32, device=dev),
+        "logits": torch.empty(N, E, dtype=torch.float32, device=dev) if want_logits else None,
+        "probs": torch.empty(N, E, dtype=torch.float32, device=dev) if want_probs else None,
+    }
+    rc = L.lib().pp_route(_vp(x), xd, N, H, _vp(router_packed), _vp(bias), E, float(tau),
+                          _vp(res["logits"]), _vp(res["probs"]), _vp(res["gates"]), _vp(res["mask"]),
+                          _vp(res["count"]), _stream(x))
+    L.check(rc, "route")
+    return res
+
+
+def route_logits(logits: torch.Tensor, tau: float):
+    """Tau selection from given fp32 logits [N,E] (bit-exact with torch CPU
+    softmax_thresholding, src/MoEBlock_origin.py:50-97). Returns (probs, gates, mask, count)."""
+    if logits.dtype != torch.float32 or logits.dim() != 2:
+        raise RuntimeError("prunepath.route_logits: logits must be float32 [N,E]")
+    _need_gpu("route_logits", logits)
+    N, E = logits.shape
+    dev = logits.device
+    probs = torch.empty(N, E, dtype=torch.float32, device=dev)
+    gates = torch.empty(N, E, dtype=torch.float32, device=dev)
+    mask = torch.empty(N, E, dtype=torch.uint8, device=dev)
+    count = torch.empty(N, dtype=torch.int32, device=dev)
+    rc = L.lib().pp_route_logits(_vp(logits), N, E, float(tau), _vp(probs), _vp(gates), _vp(mask),
+                                 _vp(count), _stream(logits))
+    L.check(rc, "route_logits")
+    return probs, gates, mask, count
+
+
+# ----------------------------------------------------------------------------- bucketing
+def gemm_tile_m() -> int:
+    return int(L.lib().pp_gemm_tile_m())
+
+
+def max_tiles(N: int, E: int, tile_m: Optional[int] = None) -> int:
+    return int(L.lib().pp_max_tiles(N, E, tile_m or gemm_tile_m()))
+
+
+def bucket(mask: torch.Tensor, gates: torch.Tensor, tile_m: Optional[int] = None):
+    """Token -> expert CSR layout (experts ascending, tokens ascending inside an expert).
+    Returns dict: offsets [E+1], token_ids [N*E], pair_gates [N*E], token_pairs [N,E],
+    tiles [max_tiles,4], meta [4] (all int32 except pair_gates fp32). Only the first
+    offsets[E] entries of token_ids / pair_gates and the first meta[0] tiles are valid."""
+    if mask.dtype != torch.uint8 or gates.dtype != torch.float32 or mask.shape != gates.shape:
+        raise RuntimeError("prunepath.bucket: mask uint8 [N,E] and gates float32 [N,E] required")
+    _need_gpu("bucket", mask, gates)
+    N, E = mask.shape
+    tm = tile_m or gemm_tile_m()
+    dev = mask.device
+    mt = max_tiles(N, E, tm)
+    r = {
+        "offsets": torch.empty(E + 1, dtype=torch.int32, device=dev),
+        "token_ids": torch.empty(max(N * E, 1), dtype=torch.int32, device=dev),
+        "pair_gates": torch.empty(max(N * E, 1), dtype=torch.float32, device=dev),
+        "token_pairs": torch.empty(N, E, dtype=torch.int32, device=dev),
+        "tiles": torch.empty(max(mt, 1), 4, dtype=torch.int32, device=dev),
+        "meta": torch.empty(4, dtype=torch.int32, device=dev),
+        "max_tiles": mt,
+    }
+    ws = torch.empty(int(L.lib().pp_bucket_workspace_bytes(N, E)), dtype=torch.uint8, device=dev)
+    rc = L.lib().pp_bucket(_vp(mask), _vp(gates), N, E, tm, _vp(r["offsets"]), _vp(r["token_ids"]),
+                           _vp(r["pair_gates"]), _vp(r["token_pairs"]), _vp(r["tiles"]), _vp(r["meta"]),
+                           _vp(ws), _stream(mask))
+    L.check(rc, "bucket")
+    return r
+
+
+# ----------------------------------------------------------------------------- decode
+def decode_workspace(H: int, E: int, device) -> torch.Tensor:
+    """Allocate and zero (with a kernel, once) a decode workspace."""
+    n = int(L.lib().pp_decode_workspace_bytes(H, E))
+    ws = torch.empty(n, dtype=torch.uint8, device=device)
+    rc = L.lib().pp_decode_workspace_init(_vp(ws), H, E, _stream(ws))
+    L.check(rc, "decode_workspace_init")
+    return ws
+
+
+def decode_state(ws: torch.Tensor, E: int) -> dict:
+    """Read the pp_decode_state header of a decode workspace (synchronises)."""
+    hdr = ws[:16 + 16 + 3 * 4 * 256].cpu()
+    u32 = hdr[:32].view(torch.int32)
+    k = int(u32[4])
+    body = hdr[32:]
+    logits = body[:1024].view(torch.float32)[:E].clone()
+    ids = body[1024:2048].view(torch.int32)[:k].clone()
+    gts = body[2048:3072].view(torch.float32)[:k].clone()
+    return {"error": int(u32[3]), "k": k, "logits": logits, "sel_ids": ids, "sel_gates": gts,
+            "router_ticket": int(u32[0]), "ready": int(u32[1]), "done": int(u32[2])}
+
+
+def moe_decode(x: torch.Tensor, router_packed: torch.Tensor, bias: Optional[torch.Tensor], E: int, G: int,
+               tau: float, packed: torch.Tensor, workspace: torch.Tensor, grid: int = 0,
+               out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Fused single-token MoE-MLP layer. x [H] or [1,H]; returns bf16 [1,H]."""
+    x, xd = _x_dtype(x.reshape(1, -1))
+    H = x.shape[1]
+    _need_gpu("moe_decode", x, router_packed, bias, packed, workspace)
+    if out is None:
+        out = torch.empty(1, H, dtype=torch.bfloat16, device=x.device)
+    rc = L.lib().pp_moe_decode(_vp(x), xd, H, _vp(router_packed), _vp(bias), E, G, float(tau), _vp(packed),
+                               _vp(out), _vp(workspace), int(grid), _stream(x))
+    L.check(rc, "moe_decode")
+    return out
+
+
+# ----------------------------------------------------------------------------- prefill
+def prefill_workspace_bytes(N: int, H: int, E: int, G: int) -> int:
+    return int(L.lib().pp_prefill_workspace_bytes(N, H, E, G))
+
+
+def moe_prefill(x: torch.Tensor, router_packed: torch.Tensor, bias: Optional[torch.Tensor], E: int, G: int,
+                tau: float, packed: torch.Tensor, workspace: Optional[torch.Tensor] = None,
+                out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Route -> bucket -> grouped gate/up GEMM (SwiGLU) -> grouped down GEMM -> combine.
+    x [N,H]; returns bf16 [N,H]."""
+    x, xd = _x_dtype(x)
+    N, H = x.shape
+    _need_gpu("moe_prefill", x, router_packed, bias, packed, workspace)
+    need = prefill_workspace_bytes(N, H, E, G)
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
+    if out is None:
+        out = torch.empty(N, H, dtype=torch.bfloat16, device=x.device)
+    rc = L.lib().pp_moe_prefill(_vp(x), xd, N, H, _vp(router_packed), _vp(bias), E, G, float(tau), _vp(packed),
+                                _vp(out), _vp(workspace), _stream(x))
+    L.check(rc, "moe_prefill")
+    return out
+
+
+def expert_gateup(x_bf16: torch.Tensor, packed: torch.Tensor, E: int, G: int, bk: dict) -> torch.Tensor:
+    """act [N*E, G] bf16 (rows = pairs in bucket order) from a bucket() layout."""
+    N, H = x_bf16.shape
+    _need_gpu("expert_gateup", x_bf16, packed)
+    act = torch.empty(max(N * E, 1), G, dtype=torch.bfloat16, device=x_bf16.device)
+    rc = L.lib().pp_expert_gateup(_vp(x_bf16), H, G, _vp(packed), E, _vp(bk["token_ids"]), _vp(bk["pair_gates"]),
+                                  _vp(bk["tiles"]), _vp(bk["meta"]), bk["max_tiles"], _vp(act), _stream(x_bf16))
+    L.check(rc, "expert_gateup")
+    return act
+
+
+def expert_down(act: torch.Tensor, packed: torch.Tensor, H: int, E: int, G: int, bk: dict) -> torch.Tensor:
+    _need_gpu("expert_down", act, packed)
+    y = torch.empty(act.shape[0], H, dtype=torch.float32, device=act.device)
+    rc = L.lib().pp_expert_down(_vp(act), H, G, _vp(packed), E, _vp(bk["tiles"]), _vp(bk["meta"]),
+                                bk["max_tiles"], _vp(y), _stream(act))
+    L.check(rc, "expert_down")
+    return y
+
+
+def combine(y: torch.Tensor, token_pairs: torch.Tensor, count: torch.Tensor, H: int, E: int) -> torch.Tensor:
+    N = token_pairs.shape[0]
+    _need_gpu("combine", y, token_pairs, count)
+    out = torch.empty(N, H, dtype=torch.bfloat16, device=y.device)
+    rc = L.lib().pp_combine(_vp(y), _vp(token_pairs), _vp(count), N, H, E, _vp(out), _stream(y))
+    L.check(rc, "combine")
+    return out
+
+
+# ----------------------------------------------------------------------------- torch.library
+@torch.library.custom_op("prunepath::route_logits", mutates_args=())
+def _route_logits_op(logits: torch.Tensor, tau: float) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor,
+                                                                  torch.Tensor]:
+    return route_logits(logits, tau)
+
+
+@_route_logits_op.register_fake
+def _(logits, tau):
+    N, E = logits.shape
+    return (logits.new_empty(N, E), logits.new_empty(N, E), logits.new_empty(N, E, dtype=torch.uint8),
+            logits.new_empty(N, dtype=torch.int32))
+
+
+@torch.library.custom_op("prunepath::moe_prefill", mutates_args=())
+def _moe_prefill_op(x: torch.Tensor, router_packed: torch.Tensor, bias: Optional[torch.Tensor], E: int, G: int,
+                    tau: float, packed: torch.Tensor) -> torch.Tensor:
+    return moe_prefill(x, router_packed, bias, E, G, tau, packed)
+
+
+@_moe_prefill_op.register_fake
+def _(x, router_packed, bias, E, G, tau, packed):
+    return x.new_empty(x.shape, dtype=torch.bfloat16)
+
+
+@torch.library.custom_op("prunepath::moe_decode", mutates_args=("workspace",))
+def _moe_decode_op(x: torch.Tensor, router_packed: torch.Tensor, bias: Optional[torch.Tensor], E: int, G: int,
+                   tau: float, packed: torch.Tensor, workspace: torch.Tensor) -> torch.Tensor:
+    return moe_decode(x, router_packed, bias, E, G, tau, packed, workspace)
+
+
+@_moe_decode_op.register_fake
+def _(x, router_packed, bias, E, G, tau, packed, workspace):
+    return x.new_empty(1, x.numel(), dtype=torch.bfloat16)

@@ -1,0 +1,153 @@
+"""Drop-in replacement for the reference ``TauSparseMoE`` block
+(src/tl_kernel_optimized_Ultimate_PanGU.py:468-615) on MI355X.
+
+Same constructor ``TauSparseMoE(hidden_size, intermediate_size, num_experts,
+group_size, tau)``, same persistent buffers and ``state_dict`` keys
+(``W_gate`` [H,I], ``W_up`` [H,I], ``W_down`` [I,H] in bf16 -- the rearranged
+layout written by ``physical_reorder_for_inference``, src/openpangu_moe.py:234-243 --
+and ``router`` [H,E]), same mutable ``tau`` attribute and the same
+``forward(x[B,L,H]) -> [B,L,H] bf16`` that takes the decode path for one token
+and the prefill path otherwise (:606-615).
+
+Differences by design (each a documented build choice, not an omission):
+* ``router`` is kept in fp32 (the reference stores bf16, :486); loading a bf16
+  state_dict converts on copy. Routing follows the masked reference
+  ``softmax_thresholding`` (src/MoEBlock_origin.py:50-97) bit for bit given the
+  fp32 logits.
+* The kernels read packed copies of the buffers (``packed_experts``,
+  ``router_packed``, non-persistent), rebuilt lazily whenever the reference
+  buffers change (``load_state_dict``, ``.data =`` assignment, in-place edits
+  through ``mark_weights_changed``).
+* Outputs are fresh tensors (the reference decode output aliases a persistent
+  buffer, :530) and no call synchronises with the host (the reference prefill
+  calls ``total_tiles.item()``, :581).
+* Every neuron of every selected expert is computed (the reference decode grid
+  covers only 64 neurons per expert, :398-399, 515).
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+import torch.nn as nn
+
+from . import ops
+
+
+class TauSparseMoE(nn.Module):
+    def __init__(self, hidden_size: int, intermediate_size: int, num_experts: int, group_size: int,
+                 tau: float, router_bias: Optional[torch.Tensor] = None):
+        super().__init__()
+        if num_experts * group_size != intermediate_size:
+            raise ValueError(f"num_experts*group_size ({num_experts}*{group_size}) != intermediate_size "
+                             f"({intermediate_size})")
+        self.hidden_size = hidden_size
+        self.intermediate_size = intermediate_size
+        self.num_experts = num_experts
+        self.group_size = group_size
+        self.tau = tau
+        self.EXPERTS_POWER2 = 1 << max(0, (num_experts - 1).bit_length())
+
+        self.register_buffer("W_gate", torch.empty(hidden_size, intermediate_size, dtype=torch.bfloat16))
+        self.register_buffer("W_up", torch.empty(hidden_size, intermediate_size, dtype=torch.bfloat16))
+        self.register_buffer("W_down", torch.empty(intermediate_size, hidden_size, dtype=torch.bfloat16))
+        self.register_buffer("router", torch.empty(hidden_size, num_experts, dtype=torch.float32))
+        # optional router bias (not in the reference; used to skew expert load in benchmarks)
+        self.register_buffer("router_bias", None if router_bias is None else router_bias.float().clone(),
+                             persistent=False)
+        # kernel-side copies
+        self.register_buffer("packed_experts", None, persistent=False)
+        self.register_buffer("router_packed", None, persistent=False)
+        self.register_buffer("decode_workspace", None, persistent=False)
+        self._packed_key = None
+
+    # ------------------------------------------------------------------ packing
+    def _weights_key(self):
+        return tuple((t.data_ptr(), t._version, t.device, t.dtype) for t in
+                     (self.W_gate, self.W_up, self.W_down, self.router))
+
+    def mark_weights_changed(self) -> None:
+        self._packed_key = None
+
+    def repack(self) -> None:
+        """Build the kernel layouts from the reference-layout buffers."""
+        dev = self.W_gate.device
+        if dev.type != "cuda":
+            raise RuntimeError("TauSparseMoE: move the module to the GPU first; there is no CPU implementation")
+        H, E, G = self.hidden_size, self.num_experts, self.group_size
+        self.packed_experts = ops.pack_experts(self.W_gate.contiguous(), self.W_up.contiguous(),
+                                               self.W_down.contiguous(), E, G, perm=None, layout="tau")
+        self.router_packed = ops.pack_router(self.router.contiguous(), layout="tau")
+        if self.decode_workspace is None or self.decode_workspace.device != dev:
+            self.decode_workspace = ops.decode_workspace(H, E, dev)
+        self._packed_key = self._weights_key()
+
+    def _ensure_packed(self) -> None:
+        if self._packed_key is None or self._packed_key != self._weights_key():
+            self.repack()
+
+    @torch.no_grad()
+    def load_from_masked(self, gate_weight: torch.Tensor, up_weight: torch.Tensor, down_weight: torch.Tensor,
+                         router_weight: torch.Tensor, experts_masks_or_ids: torch.Tensor,
+                         tau: Optional[float] = None) -> "TauSparseMoE":
+        """One-time rearrangement from the masked model's weights
+        (physical_reorder_for_inference, src/openpangu_moe.py:212-256).
+
+        gate_weight/up_weight [I,H], down_weight [H,I] (nn.Linear), router_weight [E,H],
+        experts_masks_or_ids: ``experts_masks`` [E,I] one-hot or neuron->expert ids [I].
+        Neurons are grouped by expert with a stable order inside each expert.
+        """
+        dev = self.W_gate.device
+        ids = experts_masks_or_ids
+        if ids.dim() == 2:
+            ids = torch.argmax(ids.to(torch.int32), dim=0)
+        ids = ids.to(device=dev, dtype=torch.int64)
+        counts = torch.bincount(ids, minlength=self.num_experts)
+        if counts.numel() != self.num_experts or bool((counts != self.group_size).any()):
+            raise ValueError("load_from_masked: every expert must own exactly group_size neurons")
+        perm = torch.argsort(ids, stable=True)
+        gw = gate_weight.to(dev)
+        uw = up_weight.to(dev)
+        dw = down_weight.to(dev)
+        self.W_gate = gw[perm, :].t().contiguous().to(torch.bfloat16)
+        self.W_up = uw[perm, :].t().contiguous().to(torch.bfloat16)
+        self.W_down = dw[:, perm].t().contiguous().to(torch.bfloat16)
+        self.router = router_weight.to(device=dev, dtype=torch.float32).t().contiguous()
+        if tau is not None:
+            self.tau = tau
+        # pack straight from the fp32 masked weights (one bf16 rounding, as above)
+        H, E, G = self.hidden_size, self.num_experts, self.group_size
+        self.packed_experts = ops.pack_experts(gw.contiguous(), uw.contiguous(), dw.contiguous(), E, G,
+                                               perm=perm.to(torch.int32), layout="linear")
+        self.router_packed = ops.pack_router(router_weight.to(device=dev).contiguous(), layout="linear")
+        if self.decode_workspace is None or self.decode_workspace.device != dev:
+            self.decode_workspace = ops.decode_workspace(H, E, dev)
+        self._packed_key = self._weights_key()
+        return self
+
+    # ------------------------------------------------------------------ forward
+    def forward_decode(self, x_flat: torch.Tensor, B: int, L: int, H: int) -> torch.Tensor:
+        out = ops.moe_decode(x_flat, self.router_packed, self.router_bias, self.num_experts, self.group_size,
+                             self.tau, self.packed_experts, self.decode_workspace)
+        return out.view(B, L, H)
+
+    def forward_prefill(self, N: int, x_flat: torch.Tensor, B: int, L: int, H: int) -> torch.Tensor:
+        out = ops.moe_prefill(x_flat, self.router_packed, self.router_bias, self.num_experts, self.group_size,
+                              self.tau, self.packed_experts)
+        return out.view(B, L, H)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        B, L, H = x.shape
+        if H != self.hidden_size:
+            raise ValueError(f"TauSparseMoE: hidden size {H} != {self.hidden_size}")
+        N = B * L
+        self._ensure_packed()
+        x_flat = x.reshape(N, H)
+        if x_flat.dtype not in (torch.float32, torch.bfloat16):
+            x_flat = x_flat.float()
+        x_flat = x_flat.contiguous()
+        if N == 0:
+            return torch.empty(B, L, H, dtype=torch.bfloat16, device=x.device)
+        if N == 1:
+            return self.forward_decode(x_flat, B, L, H)
+        return self.forward_prefill(N, x_flat, B, L, H)

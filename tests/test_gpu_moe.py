@@ -1,0 +1,223 @@
+"""GPU parity of the full MoE-MLP layer: fused decode and grouped-GEMM prefill.
+
+Bars:
+* selection bit-exact against the oracle applied to the kernel's own fp32 logits;
+* bf16 outputs within rtol 2e-2 / atol 2e-3, elementwise, of the float64 sparse
+  restatement on the same bf16 operands (the kernels' own arithmetic error);
+* against the fp32 masked reference (torch CPU fixture of
+  src/openpangu_moe_origin.py:96-118): rtol 2e-2 / atol 2e-3 plus the per-element
+  bf16 quantization term of the operands, and normwise relative error < 1e-2
+  (helpers.assert_close_fp32 explains why the bare tolerance is unreachable for
+  any bf16-weight implementation).
+"""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import (GOLDEN, assert_close, assert_close_fp32, bits, gi, make_module, oracle, sparse_expected,
+                     to_gpu)
+
+pytestmark = pytest.mark.gpu
+
+
+def _c1(name="c1_layer"):
+    z = np.load(os.path.join(GOLDEN, f"{name}.npz"))
+    w = gi.layer_weights(int(z["seed_w"]), balanced_random=bool(z["balanced_random"]))
+    x = gi.tokens(int(z["seed_x"]), int(z["n"]))
+    return z, w, x
+
+
+@pytest.fixture(scope="module")
+def c1(pkg):
+    z, w, x = _c1()
+    return z, w, x, make_module(pkg, w, float(z["taus"][0]))
+
+
+def _decode_one(pkg, m, xrow):
+    out = m(to_gpu(xrow[None, None, :]))
+    st = pkg.ops.decode_state(m.decode_workspace, m.num_experts)
+    return out.float().cpu().numpy()[0, 0], st
+
+
+@pytest.mark.parametrize("ti", [0, 1])
+def test_decode_c1_vs_fixture(pkg, c1, ti):
+    z, w, x, m = c1
+    tau = float(z["taus"][ti])
+    m.tau = tau
+    for t in range(x.shape[0]):
+        out, st = _decode_one(pkg, m, x[t])
+        assert st["error"] == 0 and st["ready"] == 0 and st["done"] == 0 and st["router_ticket"] == 0
+        lg = st["logits"].numpy()
+        np.testing.assert_allclose(lg, z["logits"][t], rtol=1e-5, atol=1e-5)
+        sel = oracle.select(lg[None], tau)
+        # selection: descending-probability order, gates bit-exact
+        np.testing.assert_array_equal(st["sel_ids"].numpy(), sel.ranked[0, :sel.count[0]])
+        np.testing.assert_array_equal(bits(st["sel_gates"].numpy()),
+                                      bits(sel.gates[0, sel.ranked[0, :sel.count[0]]]))
+        ref_sel = oracle.select(z["logits"][t:t + 1], tau)
+        sp = sparse_expected(x[t:t + 1], w, sel.gates)[0]
+        if np.array_equal(ref_sel.mask, sel.mask):
+            assert_close_fp32(out, z[f"tau{ti}/out"][t], sp, what=f"decode token {t} vs fp32 fixture")
+        assert_close(out, sp, what=f"decode token {t} vs fp64 sparse")
+
+
+def test_decode_repeated_calls_and_bf16_input(pkg, c1):
+    z, w, x, m = c1
+    m.tau = 0.7
+    outs = []
+    for rep in range(3):
+        for t in (0, 5, 2):
+            o, st = _decode_one(pkg, m, x[t])
+            assert st["error"] == 0
+            outs.append((t, o))
+    for t, o in outs:
+        ref = [oo for tt, oo in outs if tt == t][0]
+        np.testing.assert_allclose(o, ref, rtol=1e-2, atol=1e-3)
+    xb = torch.from_numpy(x[3]).to(torch.bfloat16)
+    o = m(xb.view(1, 1, -1).to("cuda:0")).float().cpu().numpy()[0, 0]
+    st = pkg.ops.decode_state(m.decode_workspace, m.num_experts)
+    sel = oracle.select(st["logits"].numpy()[None], 0.7)
+    xr = xb.float().numpy()
+    assert_close(o, sparse_expected(xr[None], w, sel.gates)[0], what="bf16 input decode")
+
+
+@pytest.mark.parametrize("tau", [0.0, 0.3, 1.05])
+def test_decode_tau_extremes(pkg, c1, tau):
+    z, w, x, m = c1
+    m.tau = tau
+    out, st = _decode_one(pkg, m, x[1])
+    sel = oracle.select(st["logits"].numpy()[None], tau)
+    assert st["k"] == sel.count[0]
+    if tau == 0.0:
+        assert st["k"] == 1
+    if tau > 1:
+        assert st["k"] == 16
+    assert_close(out, sparse_expected(x[1:2], w, sel.gates)[0], what=f"tau={tau}")
+
+
+@pytest.mark.parametrize("grid", [16, 64, 1000])
+def test_decode_grid_sizes(pkg, c1, grid):
+    z, w, x, m = c1
+    out = pkg.ops.moe_decode(to_gpu(x[4]), m.router_packed, None, 16, 384, 0.95, m.packed_experts,
+                             m.decode_workspace, grid=grid).float().cpu().numpy()[0]
+    st = pkg.ops.decode_state(m.decode_workspace, 16)
+    assert st["error"] == 0
+    sel = oracle.select(st["logits"].numpy()[None], 0.95)
+    assert_close(out, sparse_expected(x[4:5], w, sel.gates)[0], what=f"grid={grid}")
+
+
+def test_prefill_c1_vs_fixture(pkg, c1):
+    z, w, x, m = c1
+    for ti, tau in enumerate(z["taus"]):
+        m.tau = float(tau)
+        out = m(to_gpu(x[None])).float().cpu().numpy()[0]
+        res = pkg.ops.route(to_gpu(x), m.router_packed, 16, float(tau))
+        lg = res["logits"].cpu().numpy()
+        sel = oracle.select(lg, float(tau))
+        np.testing.assert_array_equal(res["mask"].cpu().numpy(), sel.mask)
+        ref_sel = oracle.select(z["logits"], float(tau))
+        same = np.all(ref_sel.mask == sel.mask, axis=1)
+        assert same.sum() >= 7
+        sp = sparse_expected(x, w, sel.gates)
+        assert_close_fp32(out[same], z[f"tau{ti}/out"][same], sp[same], what="prefill vs fp32 fixture")
+        assert_close(out, sp, what="prefill vs fp64 sparse")
+
+
+def _layer(seed, H=1536, E=16, G=384):
+    w = gi.layer_weights(seed, H=H, I=E * G, E=E)
+    return w
+
+
+@pytest.mark.parametrize("N,tau,zipf", [(2, 0.7, False), (37, 0.7, False), (16, 0.95, True),
+                                        (64, 0.95, True), (300, 0.7, False), (2048, 0.7, False)])
+def test_prefill_shapes_vs_oracle(pkg, N, tau, zipf):
+    w = _layer(100 + N)
+    bias = gi.zipf_bias(16) if zipf else None
+    m = make_module(pkg, w, tau, bias=bias)
+    x = gi.tokens(200 + N, N)
+    out = m(to_gpu(x[None])).float().cpu().numpy()[0]
+    res = pkg.ops.route(to_gpu(x), m.router_packed, 16, tau, bias=m.router_bias)
+    sel = oracle.select(res["logits"].cpu().numpy(), tau)
+    np.testing.assert_array_equal(res["mask"].cpu().numpy(), sel.mask)
+    rows = np.arange(N) if N <= 64 else np.random.default_rng(N).choice(N, 48, replace=False)
+    assert_close(out[rows], sparse_expected(x[rows], w, sel.gates[rows]), what=f"prefill N={N}")
+    # deterministic: bitwise identical on a second call
+    out2 = m(to_gpu(x[None])).float().cpu().numpy()[0]
+    np.testing.assert_array_equal(out2, out)
+
+
+def test_prefill_stages_vs_oracle(pkg):
+    """gate/up+SwiGLU act and down y per pair, checked separately."""
+    N, tau = 512, 0.7
+    w = _layer(7)
+    m = make_module(pkg, w, tau)
+    x = gi.tokens(8, N)
+    xb = to_gpu(x, torch.bfloat16)
+    res = pkg.ops.route(xb, m.router_packed, 16, tau)
+    bk = pkg.ops.bucket(res["mask"], res["gates"])
+    act = pkg.ops.expert_gateup(xb, m.packed_experts, 16, 384, bk)
+    y = pkg.ops.expert_down(act, m.packed_experts, 1536, 16, 384, bk)
+    out = pkg.ops.combine(y, bk["token_pairs"], res["count"], 1536, 16)
+    torch.cuda.synchronize()
+    off = bk["offsets"].cpu().numpy()
+    tok = bk["token_ids"].cpu().numpy()
+    pg = bk["pair_gates"].cpu().numpy()
+    perm = oracle.pack_permutation(w["expert_ids"])
+    from helpers import bf16_round
+    Wg = bf16_round(w["w_gate"])[perm].astype(np.float64)
+    Wu = bf16_round(w["w_up"])[perm].astype(np.float64)
+    Wd = bf16_round(w["w_down"])[:, perm].T.astype(np.float64)
+    xr = xb.float().cpu().numpy().astype(np.float64)
+    act_np = act.float().cpu().numpy()
+    y_np = y.float().cpu().numpy()
+    rng = np.random.default_rng(0)
+    for p in rng.choice(off[-1], 64, replace=False):
+        e = int(np.searchsorted(off, p, side="right") - 1)
+        sl = slice(e * 384, (e + 1) * 384)
+        g = xr[tok[p]] @ Wg[sl].T
+        u = xr[tok[p]] @ Wu[sl].T
+        a = g / (1 + np.exp(-g)) * u * pg[p]
+        assert_close(act_np[p], a, what=f"act pair {p}")
+        assert_close(y_np[p], act_np[p].astype(np.float64) @ Wd[sl], what=f"y pair {p}")
+    full = m(xb[None]).float().cpu().numpy()[0]
+    np.testing.assert_array_equal(out.float().cpu().numpy(), full)
+
+
+def test_real_checkpoint_shape_e192_g32(pkg):
+    """E=192 experts of G=32 neurons with a reference cluster map (layer 3)."""
+    ids = np.load(os.path.join(GOLDEN, "pangu_clusters_k32.npz"))["expert_ids"][3].astype(np.int32)
+    w = gi.layer_weights(31, E=192)
+    w["expert_ids"] = ids
+    m = make_module(pkg, w, 0.7)
+    x = gi.tokens(32, 96)
+    out = m(to_gpu(x[None])).float().cpu().numpy()[0]
+    res = pkg.ops.route(to_gpu(x), m.router_packed, 192, 0.7)
+    sel = oracle.select(res["logits"].cpu().numpy(), 0.7)
+    np.testing.assert_array_equal(res["mask"].cpu().numpy(), sel.mask)
+    rows = np.arange(0, 96, 6)
+    assert_close(out[rows], sparse_expected(x[rows], w, sel.gates[rows]), what="E=192 prefill")
+    od = m(to_gpu(x[None, :1])).float().cpu().numpy()[0, 0]
+    st = pkg.ops.decode_state(m.decode_workspace, 192)
+    assert st["error"] == 0
+    sel1 = oracle.select(st["logits"].numpy()[None], 0.7)
+    np.testing.assert_array_equal(np.sort(st["sel_ids"].numpy()), np.nonzero(sel1.mask[0])[0])
+    assert_close(od, sparse_expected(x[:1], w, sel1.gates)[0], what="E=192 decode")
+
+
+def test_module_state_dict_roundtrip(pkg, c1):
+    z, w, x, m = c1
+    m.tau = 0.7
+    ref = m(to_gpu(x[None])).float().cpu()
+    sd = {k: v.clone() for k, v in m.state_dict().items()}
+    m2 = pkg.TauSparseMoE(1536, 6144, 16, 384, 0.7).to("cuda:0")
+    # a reference-format state_dict stores the router in bf16; it loads by conversion
+    m2.load_state_dict(sd)
+    out2 = m2(to_gpu(x[None])).float().cpu()
+    assert torch.equal(out2, ref)
+    sd_bf = dict(sd)
+    sd_bf["router"] = sd["router"].to(torch.bfloat16)
+    m2.load_state_dict(sd_bf)
+    out3 = m2(to_gpu(x[None])).float().cpu()
+    assert out3.shape == ref.shape  # repacked from the converted router
