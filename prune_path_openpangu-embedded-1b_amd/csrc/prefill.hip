@@ -247,6 +247,239 @@ __global__ __launch_bounds__(GM_THREADS, 2) void down_kernel(
   }
 }
 
+// ------------------------------------------------------------------ pipelined grouped GEMM
+// Tile 128 rows x 128 B-rows x BK=64 on v_mfma_f32_32x32x16_bf16, 4 waves as 2 x 2
+// (wave tile 64 x 64), two workgroups per CU, persistent over (row tile, column tile)
+// items. Operands go straight from global memory into LDS (global_load_lds_dwordx4:
+// lane i of a wave writes bytes [16 i, 16 i + 16) of the wave's 1 KB block, no VGPR
+// staging), two 32 KB LDS stages: the DMA of K block kb+1 runs under the MFMAs of kb.
+//
+// A tile row holds 64 bf16 = 8 chunks of 16 bytes; chunk c of row r is stored at
+// position c ^ ((r >> 1) & 7). A fragment read (ds_read_b128) covers 32 consecutive
+// rows; any 16 of them then land in 16 distinct 16-byte slots of a 256-byte bank
+// window, and any 8 in 8 distinct slots of a 128-byte window.
+//
+// Synchronisation is explicit: the compiler cannot tell that an LDS read does not
+// alias a DMA still in flight and would drain every prefetch before each read, and
+// __syncthreads() adds a release fence that does the same. So fragment reads are
+// inline ds_read_b128 whose results are fenced by s_waitcnt lgkmcnt tied to the
+// fragment registers, and the per-K-block barrier waits only for this wave's DMA of
+// the block about to be read.
+#define GV_STAGES 2
+#define GV_TILE_BYTES (128 * 64 * 2)               // one operand tile of one stage
+#define GV_STAGE_BYTES (2 * GV_TILE_BYTES)         // A + B
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ void gl2lds(const void* src, unsigned char* lds_base) {
+  __builtin_amdgcn_global_load_lds(src, (lds_void_t*)lds_base, 16, 0, 0);
+}
+
+__device__ __forceinline__ int gv_swz(int r) { return (r >> 1) & 7; }
+
+template <int IMM>
+__device__ __forceinline__ u32x4 gv_read(uint32_t lds_addr) {
+  u32x4 v;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(lds_addr), "i"(IMM));
+  return v;
+}
+
+// Wait until at most N LDS reads are outstanding; ties the four fragments of the
+// current k-step so that their MFMAs cannot be scheduled above the wait.
+template <int N>
+__device__ __forceinline__ void gv_wait(u32x4& a0, u32x4& a1, u32x4& b0, u32x4& b1) {
+  asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(a0), "+v"(a1), "+v"(b0), "+v"(b1) : "n"(N));
+}
+
+__device__ __forceinline__ f32x16_t mfma32v(u32x4 a, u32x4 b, f32x16_t c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c,
+                                                 0, 0, 0);
+}
+
+// Item order: workgroup b runs on XCD b % 8 (round-robin dispatch); XCD x takes the
+// contiguous item range [x * chunk, (x + 1) * chunk), so the column tiles of one row
+// tile, and the row tiles of one expert, share that XCD's L2. gridDim.x is a multiple
+// of 8.
+struct GvItems {
+  int first, last, step;
+  __device__ GvItems(int n_items) {
+    const int xcd = blockIdx.x & 7, per = gridDim.x >> 3;
+    const int chunk = (n_items + 7) >> 3;
+    first = xcd * chunk + (blockIdx.x >> 3);
+    last = min(n_items, (xcd + 1) * chunk);
+    step = per;
+  }
+};
+
+// One item = (tile t, column block nt). A rows: a_row(i) = element offset of the tile's
+// row i (i < 128, already clamped to a valid row); B rows: b_row(j) likewise (j < 128).
+// Accumulates the 128 x 128 product over K (multiple of 64) into acc[2][2] of each wave.
+template <typename AROW, typename BROW>
+__device__ __forceinline__ void gv_mainloop(unsigned char* smem, AROW a_row, BROW b_row, int K,
+                                            f32x16_t (&acc)[2][2]) {
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int wm = w >> 1, wn = w & 1;
+  // DMA assignment: instruction i covers rows 32 i + 8 w + lane/8, chunk position lane%8
+  int64_t aoff[4], boff[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = 32 * i + 8 * w + (lane >> 3);
+    const int pchunk = ((lane & 7) ^ gv_swz(r)) * 8;  // logical chunk stored at this lane's position
+    aoff[i] = a_row(r) + pchunk;
+    boff[i] = b_row(r) + pchunk;
+  }
+  // fragment read addresses per k-step: row (lane & 31) of the wave's 32-row blocks
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void_t*)smem;
+  uint32_t offA[4], offB[4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    const int r = lane & 31, c = ks * 2 + (lane >> 5);
+    const uint32_t o = (uint32_t)(r * 8 + (c ^ gv_swz(r))) * 16;
+    offA[ks] = lds0 + wm * 64 * 128 + o;
+    offB[ks] = lds0 + GV_TILE_BYTES + wn * 64 * 128 + o;
+  }
+  const int nkb = K / 64;
+  auto issue = [&](int kb, int st) {
+    unsigned char* sb = smem + st * GV_STAGE_BYTES;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int blk = (32 * i + 8 * w) * 128;  // wave's 1 KB block
+      gl2lds(a_row.base + aoff[i] + kb * 64, sb + blk);
+      gl2lds(b_row.base + boff[i] + kb * 64, sb + GV_TILE_BYTES + blk);
+    }
+  };
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int q = 0; q < 16; ++q) acc[i][j][q] = 0.0f;
+  issue(0, 0);
+  int st = 0;
+  for (int kb = 0; kb < nkb; ++kb) {
+    // this wave's DMA of block kb has landed, every wave's after the barrier; all
+    // waves are also done reading the other stage (block kb-1)
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    const uint32_t sbase = st * GV_STAGE_BYTES;
+    u32x4 fa[2][2], fb[2][2];
+    fa[0][0] = gv_read<0>(offA[0] + sbase);
+    fa[0][1] = gv_read<4096>(offA[0] + sbase);
+    fb[0][0] = gv_read<0>(offB[0] + sbase);
+    fb[0][1] = gv_read<4096>(offB[0] + sbase);
+    // unconditional: past the end the last block is fetched again into the stage
+    // everyone finished before the barrier, and never read
+    issue(kb + 1 < nkb ? kb + 1 : nkb - 1, st ^ 1);
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const int cur = ks & 1, nxt = cur ^ 1;
+      if (ks < 3) {
+        fa[nxt][0] = gv_read<0>(offA[ks + 1] + sbase);
+        fa[nxt][1] = gv_read<4096>(offA[ks + 1] + sbase);
+        fb[nxt][0] = gv_read<0>(offB[ks + 1] + sbase);
+        fb[nxt][1] = gv_read<4096>(offB[ks + 1] + sbase);
+        gv_wait<4>(fa[cur][0], fa[cur][1], fb[cur][0], fb[cur][1]);
+      } else {
+        gv_wait<0>(fa[cur][0], fa[cur][1], fb[cur][0], fb[cur][1]);
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = mfma32v(fa[cur][i], fb[cur][j], acc[i][j]);
+    }
+    st ^= 1;
+  }
+  // the next item reuses both stages: drain the redundant tail DMA first
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+struct GvRows {  // row source: base pointer + per-row element offset function
+  const bf16_t* base;
+};
+
+// gate/up with SwiGLU epilogue. B rows 0..63 = gate rows of neurons nb0..nb0+63,
+// rows 64..127 = up rows of the same neurons; wave (wm, wn) takes rows wm*64.. and
+// gate/up columns wn*32.. of each half, so lane-wise accG and accU line up.
+__global__ __launch_bounds__(GM_THREADS, 2) void gateup_v2_kernel(
+    const bf16_t* __restrict__ xb, int H, int G, const bf16_t* __restrict__ wrows,
+    const int32_t* __restrict__ token_ids, const float* __restrict__ pair_gates,
+    const int32_t* __restrict__ tiles, const int32_t* __restrict__ meta, bf16_t* __restrict__ act) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int wm = w >> 1, wn = w & 1;
+  const int n_ntile = G / 64;
+  const GvItems it(meta[0] * n_ntile);
+  for (int item = it.first; item < it.last; item += it.step) {
+    const int t = item / n_ntile, nt = item % n_ntile;
+    const int e = tiles[t * 4 + 0], p0 = tiles[t * 4 + 1], rows = tiles[t * 4 + 2];
+    const int nb0 = nt * 64;
+    struct ARow { const bf16_t* base; const int32_t* tok; int p0, rows, H;
+      __device__ int64_t operator()(int r) const { return (int64_t)tok[p0 + (r < rows ? r : 0)] * H; } };
+    struct BRow { const bf16_t* base; int e, G, nb0, H;
+      __device__ int64_t operator()(int r) const {
+        const int part = r < 64 ? 0 : 1;
+        return ((int64_t)(e * G + nb0 + (r & 63)) * 3 + part) * H; } };
+    ARow ar{xb, token_ids, p0, rows, H};
+    BRow br{wrows, e, G, nb0, H};
+    f32x16_t acc[2][2];
+    // wave columns: gate block j=0 -> B rows wn*32.., up block j=1 -> B rows 64 + wn*32..
+    // gv_mainloop takes B rows wn*64 + j*32; remap so that j=0 is gate and j=1 is up
+    struct BRowPerm { const bf16_t* base; BRow inner;
+      __device__ int64_t operator()(int r) const {
+        // tile row r = wn*64 + j*32 + q  ->  gate/up row (j*64) + wn*32 + q
+        const int wn_ = r >> 6, j = (r >> 5) & 1, q = r & 31;
+        return inner(j * 64 + wn_ * 32 + q); } };
+    BRowPerm bp{wrows, br};
+    gv_mainloop(smem, ar, bp, H, acc);
+    const int neuron = nb0 + wn * 32 + (lane & 31);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+#pragma unroll
+      for (int q = 0; q < 16; ++q) {
+        const int r = wm * 64 + i * 32 + mfma32_row(q, lane);
+        if (r < rows) {
+          const int p = p0 + r;
+          act[(int64_t)p * G + neuron] = f32_to_bf16(pp_silu(acc[i][0][q]) * acc[i][1][q] * pair_gates[p]);
+        }
+      }
+    }
+  }
+}
+
+// down projection: A = act rows (pairs), B = down_t rows (hidden columns), K = G
+__global__ __launch_bounds__(GM_THREADS, 2) void down_v2_kernel(
+    const bf16_t* __restrict__ act, int H, int G, const bf16_t* __restrict__ down_t,
+    const int32_t* __restrict__ tiles, const int32_t* __restrict__ meta, float* __restrict__ y) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int wm = w >> 1, wn = w & 1;
+  const int n_ntile = H / 128;
+  const GvItems it(meta[0] * n_ntile);
+  for (int item = it.first; item < it.last; item += it.step) {
+    const int t = item / n_ntile, nt = item % n_ntile;
+    const int e = tiles[t * 4 + 0], p0 = tiles[t * 4 + 1], rows = tiles[t * 4 + 2];
+    const int h0 = nt * 128;
+    struct ARow { const bf16_t* base; int p0, rows, G;
+      __device__ int64_t operator()(int r) const { return (int64_t)(p0 + (r < rows ? r : 0)) * G; } };
+    struct BRow { const bf16_t* base; int e, H, h0, G;
+      __device__ int64_t operator()(int r) const { return ((int64_t)e * H + h0 + r) * G; } };
+    ARow ar{act, p0, rows, G};
+    BRow br{down_t, e, H, h0, G};
+    f32x16_t acc[2][2];
+    gv_mainloop(smem, ar, br, G, acc);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int h = h0 + wn * 64 + j * 32 + (lane & 31);
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+          const int r = wm * 64 + i * 32 + mfma32_row(q, lane);
+          if (r < rows) y[(int64_t)(p0 + r) * H + h] = acc[i][j][q];
+        }
+      }
+  }
+}
+
 // ------------------------------------------------------------------ combine
 __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ y,
                                                       const int32_t* __restrict__ token_pairs,
@@ -283,13 +516,21 @@ static int gemm_grid(int64_t items) {
   return (int)(g < 1 ? 1 : g);
 }
 
+static int gemm_grid_v2(int64_t items) {  // two workgroups per CU, a multiple of 8 (XCD order)
+  int64_t g = 2 * (int64_t)pp_device_cus();
+  if (items < g) g = items;
+  g = (g + 7) / 8 * 8;
+  return (int)(g < 8 ? 8 : g);
+}
+
 static int gateup_launch(const bf16_t* xb, int H, int G, const bf16_t* wrows, int E, const int32_t* token_ids,
                          const float* pair_gates, const int32_t* tiles, const int32_t* meta, int64_t max_tiles,
                          bf16_t* act, hipStream_t st) {
   (void)E;
   if (G % 64 == 0) {
-    int grid = gemm_grid(max_tiles * (G / 64));
-    gateup_kernel<2, 2, 2><<<grid, GM_THREADS, 0, st>>>(xb, H, G, wrows, token_ids, pair_gates, tiles, meta, act);
+    int grid = gemm_grid_v2(max_tiles * (G / 64));
+    gateup_v2_kernel<<<grid, GM_THREADS, GV_STAGES * GV_STAGE_BYTES, st>>>(xb, H, G, wrows, token_ids, pair_gates,
+                                                                          tiles, meta, act);
   } else {
     int grid = gemm_grid(max_tiles * (G / 32));
     gateup_kernel<4, 1, 1><<<grid, GM_THREADS, 0, st>>>(xb, H, G, wrows, token_ids, pair_gates, tiles, meta, act);
@@ -299,8 +540,13 @@ static int gateup_launch(const bf16_t* xb, int H, int G, const bf16_t* wrows, in
 
 static int down_launch(const bf16_t* act, int H, int G, const bf16_t* down_t, const int32_t* tiles,
                        const int32_t* meta, int64_t max_tiles, float* y, hipStream_t st) {
-  int grid = gemm_grid(max_tiles * (H / 128));
-  down_kernel<<<grid, GM_THREADS, 0, st>>>(act, H, G, down_t, tiles, meta, y);
+  if (G % 64 == 0) {
+    int grid = gemm_grid_v2(max_tiles * (H / 128));
+    down_v2_kernel<<<grid, GM_THREADS, GV_STAGES * GV_STAGE_BYTES, st>>>(act, H, G, down_t, tiles, meta, y);
+  } else {
+    int grid = gemm_grid(max_tiles * (H / 128));
+    down_kernel<<<grid, GM_THREADS, 0, st>>>(act, H, G, down_t, tiles, meta, y);
+  }
   return pp_check_launch("down_kernel");
 }
 
