@@ -239,7 +239,8 @@ __global__ __launch_bounds__(DEC_THREADS) void decode_kernel(
   // this workgroup: records [v0, v1) of the k*G selected ones; wave wv a contiguous
   // quarter of them, loaded DEC_RB records at a time (all loads in flight together)
   const int T = k * G;
-  const int v0 = (int)((int64_t)T * b / W), v1 = (int)((int64_t)T * (b + 1) / W);
+  int v0, v1;
+  pp_split((uint32_t)T, (uint32_t)W, (uint32_t)b, v0, v1);
   const int n = v1 - v0;
   int r = v0 + (n * wv) / 4;
   const int r_end = v0 + (n * (wv + 1)) / 4;
@@ -268,7 +269,7 @@ __global__ __launch_bounds__(DEC_THREADS) void decode_kernel(
   uint4 gq[CPL], uq[CPL], dq[CPL];
   int s_cur = 0, g_cur = 0;
   if (r < r_end) {
-    s_cur = r / G;
+    s_cur = (int)((uint32_t)r / (uint32_t)G);
     g_cur = r - s_cur * G;
     const uint4* rec = (const uint4*)(rows + ((int64_t)sel_ids_s[s_cur] * G + g_cur) * 3 * H);
 #pragma unroll
@@ -543,7 +544,8 @@ __global__ __launch_bounds__(64 * NW) void decode16_kernel(
 
   // ---- stream the selected neuron records (as decode_kernel)
   const int T = k * G;
-  const int v0 = (int)((int64_t)T * b / W), v1 = (int)((int64_t)T * (b + 1) / W);
+  int v0, v1;
+  pp_split((uint32_t)T, (uint32_t)W, (uint32_t)b, v0, v1);
   const int n = v1 - v0;
   int r = v0 + (n * wv) / NW;
   const int r_end = v0 + (n * (wv + 1)) / NW;
@@ -558,7 +560,7 @@ __global__ __launch_bounds__(64 * NW) void decode16_kernel(
   uint4 gq[CPL], uq[CPL], dq[CPL];
   int s_cur = 0, g_cur = 0;
   if (r < r_end) {
-    s_cur = r / G;
+    s_cur = (int)((uint32_t)r / (uint32_t)G);
     g_cur = r - s_cur * G;
     const uint4* rec = (const uint4*)(rows + ((int64_t)sel_ids_s[s_cur] * G + g_cur) * 3 * H);
 #pragma unroll

@@ -41,16 +41,21 @@ __device__ __forceinline__ float bf16_to_f32(bf16_t v) {
   return __uint_as_float(((uint32_t)v) << 16);
 }
 
-// Round to nearest even, NaN kept quiet (the rounding torch uses for .to(bfloat16)).
-__device__ __forceinline__ bf16_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (bf16_t)((u >> 16) | 0x40);
-  uint32_t lsb = (u >> 16) & 1u;
-  u += 0x7fffu + lsb;
-  return (bf16_t)(u >> 16);
-}
+// Round to nearest even, NaN kept quiet (the rounding torch uses for .to(bfloat16)):
+// one v_cvt_pk_bf16_f32. The software form (add 0x7fff + lsb, NaN branch) costs ~10
+// instructions and a branch per value, which matters in kernels whose executed code
+// size is part of their latency.
+__device__ __forceinline__ bf16_t f32_to_bf16(float f) { return __builtin_bit_cast(bf16_t, (__bf16)f); }
 
 __host__ __device__ __forceinline__ int pp_ceil_div(int a, int b) { return (a + b - 1) / b; }
+
+// Balanced contiguous split of [0, T) into W parts: part b is [lo, hi). One 32-bit
+// division of uniform values (a 64-bit T * b / W costs ~130 instructions per use).
+__device__ __forceinline__ void pp_split(uint32_t T, uint32_t W, uint32_t b, int& lo, int& hi) {
+  const uint32_t q = T / W, rem = T - q * W;
+  lo = (int)(b * q + (b < rem ? b : rem));
+  hi = lo + (int)q + (b < rem ? 1 : 0);
+}
 
 // Load one input element as fp32 (input dtype: fp32 or bf16).
 template <typename XT>

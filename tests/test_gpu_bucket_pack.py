@@ -111,3 +111,29 @@ def test_pack_with_reference_cluster_maps(pkg):
         owned = np.nonzero(ids == e)[0]
         np.testing.assert_array_equal(rows[e * G:(e + 1) * G, 0], src[owned])
     del m
+
+
+def test_pack_bf16_rounding_bits(pkg):
+    """fp32 -> bf16 conversion of the packer, bit for bit against torch's CPU
+    .to(bfloat16) (round to nearest even): halfway ties both ways, denormals, the
+    overflow boundary, infinities, random bit patterns; NaN stays NaN."""
+    H, E, G = 128, 2, 32
+    I = E * G
+    rng = np.random.default_rng(11)
+    bits_u = rng.integers(0, 2**32, size=(I, H), dtype=np.uint64).astype(np.uint32)
+    special = np.array([0x00000000, 0x80000000, 0x3f800000, 0xbf800000, 0x00000001, 0x80000001, 0x007fffff,
+                        0x00800000, 0x00008000, 0x00018000, 0x00017fff, 0x00018001, 0x3f808000, 0x3f818000,
+                        0x3f807fff, 0x3f818001, 0x7f7fffff, 0xff7fffff, 0x7f7f8000, 0x7f7f7fff, 0x7f800000,
+                        0xff800000, 0x7fc00000, 0x7f800001, 0xffffffff, 0x4b3fffff], dtype=np.uint32)
+    bits_u[0, :special.size] = special
+    wg = bits_u.view(np.float32)
+    wu = np.zeros((I, H), np.float32)
+    wd = np.zeros((H, I), np.float32)
+    out = pkg.ops.pack_experts(to_gpu(wg), to_gpu(wu), to_gpu(wd), E, G, layout="linear")
+    got = out[: I * 3 * H].view(I, 3, H)[:, 0, :].cpu().view(torch.int16).numpy().view(np.uint16)
+    want = torch.from_numpy(wg).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    nan_in = np.isnan(wg)
+    np.testing.assert_array_equal(got[~nan_in], want[~nan_in])
+    g_exp = (got[nan_in] >> 7) & 0xFF
+    g_man = got[nan_in] & 0x7F
+    assert np.all(g_exp == 0xFF) and np.all(g_man != 0), "NaN input must stay NaN"
