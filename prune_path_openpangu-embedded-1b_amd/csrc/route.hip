@@ -126,6 +126,150 @@ __global__ __launch_bounds__(256) void route_kernel(
   }
 }
 
+// ------------------------------------------------------------------ E = 16 fast path
+// 16 tokens x 16 experts per workgroup of 8 waves. Wave w owns the contiguous K slice
+// [w H/8, (w+1) H/8) and issues all of its x and router loads before the first MFMA
+// (RT16_CHUNK 16-wide K blocks at a time, the next chunk in flight under the current
+// one); the four float4 components feed four independent MFMA chains, added in
+// component order, then the eight wave partials are added in wave order through LDS
+// (fixed order: deterministic logits). Selection: four tokens per wave at once, one
+// per 16-lane group, branch-free, same arithmetic as select_small<16> (torch's sort is
+// stable for E <= 16, so rank = number of (greater, or equal with smaller index)).
+#define RT16_WAVES 8
+#define RT16_CHUNK 8
+
+template <typename XT>
+__device__ __forceinline__ void rt16_load(const XT* __restrict__ x, const float* __restrict__ router, int64_t t,
+                                          bool valid, int H, int kb0, int nkb, int r, int g, float4 (&xa)[RT16_CHUNK],
+                                          float4 (&wa)[RT16_CHUNK]) {
+#pragma unroll
+  for (int i = 0; i < RT16_CHUNK; ++i) {
+    const int kk = (kb0 + i) * 16 + 4 * g;
+    const bool in = i < nkb;
+    xa[i] = (in && valid) ? load_x4<XT>(x, t * H + kk) : make_float4(0.f, 0.f, 0.f, 0.f);
+    wa[i] = in ? *(const float4*)(router + (int64_t)r * H + kk) : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+}
+
+template <typename XT>
+__global__ __launch_bounds__(64 * RT16_WAVES) void route16_kernel(
+    const XT* __restrict__ x, int64_t N, int H, const float* __restrict__ router, const float* __restrict__ bias,
+    float tau, float* __restrict__ logits_out, float* __restrict__ probs_out, float* __restrict__ gates_out,
+    uint8_t* __restrict__ mask_out, int32_t* __restrict__ count_out, bf16_t* __restrict__ xbf_out) {
+  __shared__ __align__(16) float part[RT16_WAVES][16][16];
+  __shared__ __align__(16) float lg_s[16][16];
+  __shared__ __align__(16) float ev_s[16][16];
+  __shared__ __align__(16) float srt_s[16][16];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int64_t tok0 = (int64_t)blockIdx.x * 16;
+  {
+    const int r = lane & 15, g = lane >> 4;
+    const int64_t t = tok0 + r;
+    const bool valid = t < N;
+    const int nkb_w = H / (16 * RT16_WAVES);  // 16-wide K blocks per wave
+    const int kbase = w * nkb_w;
+    f32x4_t acc[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[j] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+    float4 xa[RT16_CHUNK], wa[RT16_CHUNK], xn[RT16_CHUNK], wn[RT16_CHUNK];
+    rt16_load<XT>(x, router, t, valid, H, kbase, nkb_w, r, g, xa, wa);
+    for (int c0 = 0; c0 < nkb_w; c0 += RT16_CHUNK) {
+      const int left = nkb_w - c0 - RT16_CHUNK;
+      if (left > 0) rt16_load<XT>(x, router, t, valid, H, kbase + c0 + RT16_CHUNK, left, r, g, xn, wn);
+#pragma unroll
+      for (int i = 0; i < RT16_CHUNK; ++i) {
+        if (c0 + i < nkb_w) {
+          acc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[i].x, wa[i].x, acc[0], 0, 0, 0);
+          acc[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[i].y, wa[i].y, acc[1], 0, 0, 0);
+          acc[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[i].z, wa[i].z, acc[2], 0, 0, 0);
+          acc[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[i].w, wa[i].w, acc[3], 0, 0, 0);
+          if (xbf_out && valid) {
+            uint2 pk;
+            pk.x = (uint32_t)f32_to_bf16(xa[i].x) | ((uint32_t)f32_to_bf16(xa[i].y) << 16);
+            pk.y = (uint32_t)f32_to_bf16(xa[i].z) | ((uint32_t)f32_to_bf16(xa[i].w) << 16);
+            *(uint2*)(xbf_out + t * H + (kbase + c0 + i) * 16 + 4 * g) = pk;
+          }
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < RT16_CHUNK; ++i) { xa[i] = xn[i]; wa[i] = wn[i]; }
+    }
+    // lane l, element q: token 4 (l / 16) + q, expert l % 16
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      part[w][4 * g + q][r] = __fadd_rn(__fadd_rn(__fadd_rn(acc[0][q], acc[1][q]), acc[2][q]), acc[3][q]);
+  }
+  __syncthreads();
+  if (tid < 256) {
+    const int rr = tid >> 4, e = tid & 15;
+    float l = part[0][rr][e];
+#pragma unroll
+    for (int ww = 1; ww < RT16_WAVES; ++ww) l = __fadd_rn(l, part[ww][rr][e]);
+    if (bias) l = __fadd_rn(l, bias[e]);
+    lg_s[rr][e] = l;
+  }
+  __syncthreads();
+  if (w >= 4) return;
+  // ---- selection: wave w, group q4 = lane / 16 -> token 4 w + q4, lane j = expert
+  const int rr = 4 * w + (lane >> 4), j = lane & 15;
+  const int64_t t = tok0 + rr;
+  const float xl = lg_s[rr][j];
+  float m = xl;
+#pragma unroll
+  for (int o = 8; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, PP_WAVE));
+  const float e = pp_expf_u10(__fsub_rn(xl, m));
+  ev_s[rr][j] = e;
+  wave_sync_lds();
+  float ev[16];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float4 v = *(const float4*)&ev_s[rr][4 * i];
+    ev[4 * i] = v.x; ev[4 * i + 1] = v.y; ev[4 * i + 2] = v.z; ev[4 * i + 3] = v.w;
+  }
+  float a8[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) a8[i] = __fadd_rn(ev[i], ev[i + 8]);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) a8[i] = __fadd_rn(a8[i], a8[i + 4]);
+#pragma unroll
+  for (int i = 0; i < 2; ++i) a8[i] = __fadd_rn(a8[i], a8[i + 2]);
+  const float rs = __fdiv_rn(1.0f, __fadd_rn(a8[0], a8[1]));
+  const float p = __fmul_rn(e, rs);
+  int rank = 0;
+#pragma unroll
+  for (int q = 0; q < 16; ++q) {
+    const float pq = __fmul_rn(ev[q], rs);
+    rank += (kv_before(pq, p) || (pq == p && q < j)) ? 1 : 0;
+  }
+  srt_s[rr][rank] = p;
+  wave_sync_lds();
+  float sv[16];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float4 v = *(const float4*)&srt_s[rr][4 * i];
+    sv[4 * i] = v.x; sv[4 * i + 1] = v.y; sv[4 * i + 2] = v.z; sv[4 * i + 3] = v.w;
+  }
+  // (float) of the fp64 running sum is non-decreasing: the ranks with cum < tau are a
+  // prefix, so counting them gives k (NaN compares false from its rank on)
+  const float tau32 = tau;
+  double a = 0.0;
+  int k = 0;
+#pragma unroll
+  for (int q = 0; q < 16; ++q) {
+    a += (double)sv[q];
+    k += ((float)a < tau32) ? 1 : 0;
+  }
+  k = k > 0 ? k : 1;
+  if (t < N) {
+    const bool s = rank < k;
+    if (logits_out) logits_out[t * 16 + j] = xl;
+    if (probs_out) probs_out[t * 16 + j] = p;
+    if (gates_out) gates_out[t * 16 + j] = s ? pp_sigmoid(xl) : 0.0f;
+    if (mask_out) mask_out[t * 16 + j] = (uint8_t)s;
+    if (count_out && j == 0) count_out[t] = k;
+  }
+}
+
 int pp_route_impl(const void* x, int x_dtype, const float* logits_in, int64_t N, int H,
                   const float* router, const float* bias, int E, float tau, float* logits_out,
                   float* probs_out, float* gates_out, uint8_t* mask_out, int32_t* count_out,
@@ -134,6 +278,17 @@ int pp_route_impl(const void* x, int x_dtype, const float* logits_in, int64_t N,
   const int grid = (int)((N + ROUTE_TOK - 1) / ROUTE_TOK);
   const size_t smem = 0;
   const int threads = 256;
+  if (!logits_in && E == 16) {
+    const int g16 = (int)((N + 15) / 16);
+    if (x_dtype == PP_DTYPE_F32)
+      route16_kernel<float><<<g16, 64 * RT16_WAVES, 0, st>>>((const float*)x, N, H, router, bias, tau, logits_out,
+                                                            probs_out, gates_out, mask_out, count_out, xbf_out);
+    else
+      route16_kernel<bf16_t><<<g16, 64 * RT16_WAVES, 0, st>>>((const bf16_t*)x, N, H, router, bias, tau,
+                                                             logits_out, probs_out, gates_out, mask_out,
+                                                             count_out, xbf_out);
+    return pp_check_launch("route16_kernel");
+  }
   if (logits_in) {
     route_kernel<float, true><<<grid, threads, smem, st>>>(nullptr, logits_in, N, H, router, bias, E, tau,
                                                        logits_out, probs_out, gates_out, mask_out,
@@ -172,23 +327,44 @@ extern "C" int pp_route_logits(const float* logits, int64_t n_tokens, int E, flo
 }
 
 // ------------------------------------------------------------------ bucketing
-#define BKT_TOK 256  // tokens per bucketing block
+// Blocks of BKT_TOK = 64 tokens; every (token, expert) pair of a block is one work
+// item (pair i -> token i / E, expert i % E, so the mask and gate loads are coalesced
+// and independent). A block summarises its selections as bit words in LDS:
+//   tokw[e]     bit l set when token l of the block selected expert e,
+//   expw[l][q]  bit e' = e - 64 q set when token l selected expert e.
+// count:   per (block, expert) totals = popcount(tokw[e]);
+// scan:    one workgroup: expert offsets, per-block bases, GEMM tile map;
+// scatter: pair (l, e) -> position base[b][e] + popcount(tokw[e] below l) inside
+//          expert e's segment (tokens ascending), slot = number of the token's
+//          selected experts below e; the token's unselected slots are set to -1.
+#define BKT_TOK 64
+#define BKT_THREADS 256
+#define BKT_QW (PP_MAX_EXPERTS / 64)
+#define BKT_SCAN_CHUNK 8192  // ints of block counts staged in LDS at a time
 
-// Per 256-token block: count of selected tokens per expert.
-__global__ __launch_bounds__(256) void bucket_count_kernel(const uint8_t* __restrict__ mask, int64_t N,
-                                                           int E, int32_t* __restrict__ blkcnt) {
-  __shared__ int wcnt[4][PP_MAX_EXPERTS];
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int64_t t = (int64_t)blockIdx.x * BKT_TOK + threadIdx.x;
-  const bool valid = t < N;
-  for (int e = 0; e < E; ++e) {
-    const bool m = valid && mask[t * E + e];
-    const unsigned long long b = __ballot(m);
-    if (lane == 0) wcnt[w][e] = __popcll(b);
+__device__ __forceinline__ void bucket_block_words(const uint8_t* __restrict__ mask, int64_t N, int E, int64_t t0,
+                                                   unsigned long long* tokw, unsigned long long (*expw)[BKT_QW]) {
+  for (int e = threadIdx.x; e < E; e += BKT_THREADS) tokw[e] = 0ull;
+  for (int l = threadIdx.x; l < BKT_TOK * BKT_QW; l += BKT_THREADS) expw[l / BKT_QW][l % BKT_QW] = 0ull;
+  __syncthreads();
+  const int pairs = BKT_TOK * E;
+  for (int i = threadIdx.x; i < pairs; i += BKT_THREADS) {
+    const int l = i / E, e = i - l * E;
+    const int64_t t = t0 + l;
+    if (t < N && mask[t * E + e]) {
+      atomicOr(&tokw[e], 1ull << l);
+      atomicOr(&expw[l][e >> 6], 1ull << (e & 63));
+    }
   }
   __syncthreads();
-  for (int e = threadIdx.x; e < E; e += 256)
-    blkcnt[(int64_t)blockIdx.x * E + e] = wcnt[0][e] + wcnt[1][e] + wcnt[2][e] + wcnt[3][e];
+}
+
+__global__ __launch_bounds__(BKT_THREADS) void bucket_count_kernel(const uint8_t* __restrict__ mask, int64_t N,
+                                                                   int E, int32_t* __restrict__ blkcnt) {
+  __shared__ unsigned long long tokw[PP_MAX_EXPERTS];
+  __shared__ unsigned long long expw[BKT_TOK][BKT_QW];
+  bucket_block_words(mask, N, E, (int64_t)blockIdx.x * BKT_TOK, tokw, expw);
+  for (int e = threadIdx.x; e < E; e += BKT_THREADS) blkcnt[(int64_t)blockIdx.x * E + e] = __popcll(tokw[e]);
 }
 
 // One workgroup: expert totals, CSR offsets, per-block write offsets, GEMM tile map.
@@ -201,10 +377,21 @@ __global__ __launch_bounds__(256) void bucket_scan_kernel(const int32_t* __restr
   __shared__ int ntl[PP_MAX_EXPERTS];
   __shared__ int off_s[PP_MAX_EXPERTS + 1];
   __shared__ int toff_s[PP_MAX_EXPERTS + 1];
+  __shared__ int cnt_s[BKT_SCAN_CHUNK];
   const int e = threadIdx.x;
+  // block counts pass through LDS in coalesced chunks of whole blocks, so the
+  // per-expert loops below read LDS instead of one dependent load per block
+  const int cb = BKT_SCAN_CHUNK / E;  // blocks per chunk
+  int s = 0;
+  for (int b0 = 0; b0 < nblk; b0 += cb) {
+    const int nb = min(cb, nblk - b0);
+    __syncthreads();
+    for (int i = threadIdx.x; i < nb * E; i += 256) cnt_s[i] = blkcnt[(int64_t)b0 * E + i];
+    __syncthreads();
+    if (e < E)
+      for (int b = 0; b < nb; ++b) s += cnt_s[b * E + e];
+  }
   if (e < E) {
-    int s = 0;
-    for (int b = 0; b < nblk; ++b) s += blkcnt[(int64_t)b * E + e];
     tot[e] = s;
     ntl[e] = (s + tile_m - 1) / tile_m;
   }
@@ -226,54 +413,70 @@ __global__ __launch_bounds__(256) void bucket_scan_kernel(const int32_t* __restr
   }
   __syncthreads();
   for (int j = threadIdx.x; j <= E; j += 256) offsets[j] = off_s[j];
-  if (e < E) {
-    int run = off_s[e];
-    for (int b = 0; b < nblk; ++b) {
-      blkoff[(int64_t)b * E + e] = run;
-      run += blkcnt[(int64_t)b * E + e];
-    }
-    const int n = tot[e];
-    for (int i = 0; i < ntl[e]; ++i) {
-      int32_t* tp = tiles + (int64_t)(toff_s[e] + i) * 4;
-      tp[0] = e;
-      tp[1] = off_s[e] + i * tile_m;
+  int run = e < E ? off_s[e] : 0;
+  for (int b0 = 0; b0 < nblk; b0 += cb) {
+    const int nb = min(cb, nblk - b0);
+    __syncthreads();
+    for (int i = threadIdx.x; i < nb * E; i += 256) cnt_s[i] = blkcnt[(int64_t)b0 * E + i];
+    __syncthreads();
+    if (e < E)
+      for (int b = 0; b < nb; ++b) {
+        const int c = cnt_s[b * E + e];
+        cnt_s[b * E + e] = run;  // this expert's column only: no other thread touches it
+        run += c;
+      }
+    __syncthreads();
+    for (int i = threadIdx.x; i < nb * E; i += 256) blkoff[(int64_t)b0 * E + i] = cnt_s[i];
+  }
+  for (int j = 0; j < E; ++j) {  // tile i of expert j
+    const int n = tot[j];
+    for (int i = threadIdx.x; i < ntl[j]; i += 256) {
+      int32_t* tp = tiles + (int64_t)(toff_s[j] + i) * 4;
+      tp[0] = j;
+      tp[1] = off_s[j] + i * tile_m;
       tp[2] = min(tile_m, n - i * tile_m);
       tp[3] = 0;
     }
   }
 }
 
-// Per 256-token block: write pairs in token order into each expert's segment.
-__global__ __launch_bounds__(256) void bucket_scatter_kernel(
+__device__ __forceinline__ int popc_below(const unsigned long long* w, int bit) {
+  int c = 0;
+  for (int q = 0; q < (bit >> 6); ++q) c += __popcll(w[q]);
+  const int r = bit & 63;
+  if (r) c += __popcll(w[bit >> 6] & (~0ull >> (64 - r)));
+  return c;
+}
+
+__global__ __launch_bounds__(BKT_THREADS) void bucket_scatter_kernel(
     const uint8_t* __restrict__ mask, const float* __restrict__ gates, int64_t N, int E,
     const int32_t* __restrict__ blkoff, int32_t* __restrict__ token_ids, float* __restrict__ pair_gates,
     int32_t* __restrict__ token_pairs) {
-  __shared__ unsigned long long bal[4][PP_MAX_EXPERTS];
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int64_t t = (int64_t)blockIdx.x * BKT_TOK + threadIdx.x;
-  const bool valid = t < N;
-  for (int e = 0; e < E; ++e) {
-    const bool m = valid && mask[t * E + e];
-    const unsigned long long b = __ballot(m);
-    if (lane == 0) bal[w][e] = b;
+  __shared__ unsigned long long tokw[PP_MAX_EXPERTS];
+  __shared__ unsigned long long expw[BKT_TOK][BKT_QW];
+  __shared__ int base_s[PP_MAX_EXPERTS];
+  const int64_t t0 = (int64_t)blockIdx.x * BKT_TOK;
+  for (int e = threadIdx.x; e < E; e += BKT_THREADS) base_s[e] = blkoff[(int64_t)blockIdx.x * E + e];
+  bucket_block_words(mask, N, E, t0, tokw, expw);
+  const int pairs = BKT_TOK * E;
+  for (int i = threadIdx.x; i < pairs; i += BKT_THREADS) {
+    const int l = i / E, e = i - l * E;
+    const int64_t t = t0 + l;
+    if (t >= N) break;  // pairs of later tokens are later too
+    const unsigned long long* ew = expw[l];
+    const bool sel = (ew[e >> 6] >> (e & 63)) & 1ull;
+    const int below = popc_below(ew, e);  // selected experts of this token below e
+    if (sel) {
+      const int pos = base_s[e] + (l ? __popcll(tokw[e] & (~0ull >> (64 - l))) : 0);
+      token_ids[pos] = (int32_t)t;
+      if (pair_gates) pair_gates[pos] = gates ? gates[t * E + e] : 0.0f;
+      if (token_pairs) token_pairs[t * E + below] = pos;
+    } else if (token_pairs) {
+      int cnt = 0;
+      for (int q = 0; q < BKT_QW; ++q) cnt += __popcll(ew[q]);
+      token_pairs[t * E + cnt + (e - below)] = -1;  // unselected experts fill the tail in order
+    }
   }
-  __syncthreads();
-  if (!valid) return;
-  const unsigned long long lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  int slot = 0;
-  for (int e = 0; e < E; ++e) {
-    const unsigned long long b = bal[w][e];
-    if (!((b >> lane) & 1ull)) continue;
-    int base = blkoff[(int64_t)blockIdx.x * E + e];
-    for (int v = 0; v < w; ++v) base += __popcll(bal[v][e]);
-    const int pos = base + __popcll(b & lt);
-    token_ids[pos] = (int32_t)t;
-    if (pair_gates) pair_gates[pos] = gates ? gates[t * E + e] : 0.0f;
-    if (token_pairs) token_pairs[t * E + slot] = pos;
-    ++slot;
-  }
-  if (token_pairs)
-    for (int s = slot; s < E; ++s) token_pairs[t * E + s] = -1;
 }
 
 extern "C" size_t pp_bucket_workspace_bytes(int64_t n_tokens, int E) {
@@ -296,10 +499,10 @@ int pp_bucket_impl(const uint8_t* mask, const float* gates, int64_t N, int E, in
   int64_t nblk = (N + BKT_TOK - 1) / BKT_TOK;
   int32_t* blkcnt = (int32_t*)workspace;
   int32_t* blkoff = blkcnt + (nblk < 1 ? 1 : nblk) * E;
-  if (nblk > 0) bucket_count_kernel<<<(unsigned)nblk, 256, 0, st>>>(mask, N, E, blkcnt);
+  if (nblk > 0) bucket_count_kernel<<<(unsigned)nblk, BKT_THREADS, 0, st>>>(mask, N, E, blkcnt);
   bucket_scan_kernel<<<1, 256, 0, st>>>(blkcnt, (int)nblk, E, tile_m, blkoff, offsets, tiles, meta);
   if (nblk > 0)
-    bucket_scatter_kernel<<<(unsigned)nblk, 256, 0, st>>>(mask, gates, N, E, blkoff, token_ids, pair_gates,
+    bucket_scatter_kernel<<<(unsigned)nblk, BKT_THREADS, 0, st>>>(mask, gates, N, E, blkoff, token_ids, pair_gates,
                                                           token_pairs);
   return pp_check_launch("pp_bucket");
 }

@@ -36,7 +36,9 @@ def _check_bucket(pkg, mask, gates):
 
 
 @pytest.mark.parametrize("N,E,p", [(1, 16, 0.4), (37, 16, 0.4), (256, 16, 0.38), (300, 16, 0.9),
-                                   (2048, 16, 0.38), (513, 192, 0.05), (64, 24, 0.0), (64, 16, 1.0)])
+                                   (2048, 16, 0.38), (513, 192, 0.05), (64, 24, 0.0), (64, 16, 1.0),
+                                   (100, 40, 0.3), (4096, 64, 0.1), (4097, 16, 0.3), (5000, 16, 0.4),
+                                   (0, 16, 0.5), (3000, 192, 0.02)])
 def test_bucket_random_vs_oracle(pkg, N, E, p):
     rng = np.random.default_rng(N * 31 + E)
     mask = (rng.random((N, E)) < p).astype(np.uint8)

@@ -85,3 +85,83 @@ def test_route_router_layouts_agree(pkg):
     assert a.shape == (16, H)
     c = pkg.ops.pack_router(to_gpu(wr[:10]), layout="linear")
     assert c.shape == (16, H) and torch.all(c[10:] == 0) and torch.equal(c[:10], a[:10])
+
+
+def _identity_router(pkg, E, H):
+    w = np.zeros((E, H), np.float32)
+    w[np.arange(E), np.arange(E)] = 1.0
+    return pkg.ops.pack_router(to_gpu(w), layout="linear")
+
+
+def test_route16_selection_vs_golden(pkg):
+    """E = 16 path computing logits from x: with an identity router the GPU logits are
+    x itself (exact: one non-zero product per sum), so the torch-CPU golden families
+    pin the fused selection bit for bit (rows with non-finite logits excluded: inf * 0
+    would turn them into NaN)."""
+    E, H = 16, 128
+    z = np.load(os.path.join(GOLDEN, "routing_E16.npz"))
+    rp = _identity_router(pkg, E, H)
+    fams = sorted({k.split("/")[0] for k in z.files if "/" in k})
+    for fam in fams:
+        lg = z[f"{fam}/logits"]
+        keep = np.all(np.isfinite(lg), axis=1)
+        x = np.zeros((int(keep.sum()), H), np.float32)
+        x[:, :E] = lg[keep]
+        for ti, tau in enumerate(TAUS):
+            res = pkg.ops.route(to_gpu(x), rp, E, tau, want_logits=True, want_probs=True)
+            np.testing.assert_array_equal(bits(res["logits"].cpu().numpy()), bits(lg[keep]))
+            ref_mask = np.unpackbits(z[f"{fam}/tau{ti}/mask"], axis=-1, count=E)[keep]
+            np.testing.assert_array_equal(res["mask"].cpu().numpy(), ref_mask, err_msg=f"{fam} tau={tau}")
+            np.testing.assert_array_equal(bits(res["gates"].cpu().numpy()), bits(z[f"{fam}/tau{ti}/gates"][keep]),
+                                          err_msg=f"{fam} tau={tau}")
+            np.testing.assert_array_equal(res["count"].cpu().numpy(), ref_mask.sum(-1))
+            if ti == 0:
+                np.testing.assert_array_equal(bits(res["probs"].cpu().numpy()), bits(z[f"{fam}/probs"][keep]))
+
+
+@pytest.mark.parametrize("H", [128, 640, 4096])
+def test_route16_hidden_sizes(pkg, H):
+    """K split over eight waves with partial chunks (H/128 = 1, 5, 32 blocks per wave)."""
+    E, n = 16, 40
+    rng = np.random.default_rng(H)
+    x = rng.standard_normal((n, H)).astype(np.float32)
+    wr = rng.normal(0, 0.02, (E, H)).astype(np.float32)
+    rp = pkg.ops.pack_router(to_gpu(wr), layout="linear")
+    res = pkg.ops.route(to_gpu(x), rp, E, 0.7, want_logits=True, want_probs=True)
+    lg = res["logits"].cpu().numpy()
+    np.testing.assert_allclose(lg, x.astype(np.float64) @ wr.astype(np.float64).T, rtol=1e-5, atol=1e-5)
+    sel = oracle.select(lg, 0.7)
+    np.testing.assert_array_equal(res["mask"].cpu().numpy(), sel.mask)
+    np.testing.assert_array_equal(bits(res["gates"].cpu().numpy()), bits(sel.gates))
+    np.testing.assert_array_equal(bits(res["probs"].cpu().numpy()), bits(sel.probs))
+
+
+def test_decode16_selection_vs_golden(pkg):
+    """The fused decode kernel's in-kernel selection (E = 16), pinned the same way:
+    identity router, x = golden logits, one token per call."""
+    E, H, G = 16, 512, 32
+    z = np.load(os.path.join(GOLDEN, "routing_E16.npz"))
+    rp = _identity_router(pkg, E, H)
+    rng = np.random.default_rng(1)
+    I = E * G
+    wg, wu = (rng.normal(0, 0.02, (I, H)).astype(np.float32) for _ in range(2))
+    wd = rng.normal(0, 0.02, (H, I)).astype(np.float32)
+    packed = pkg.ops.pack_experts(to_gpu(wg), to_gpu(wu), to_gpu(wd), E, G, layout="linear")
+    ws = pkg.ops.decode_workspace(H, E, torch.device("cuda:0"))
+    fams = sorted({k.split("/")[0] for k in z.files if "/" in k})
+    for fam in fams:
+        lg = z[f"{fam}/logits"]
+        rows = [i for i in range(0, lg.shape[0], 23) if np.all(np.isfinite(lg[i]))][:20]
+        for ti, tau in enumerate(TAUS):
+            ref_mask = np.unpackbits(z[f"{fam}/tau{ti}/mask"], axis=-1, count=E)
+            for i in rows:
+                x = np.zeros(H, np.float32)
+                x[:E] = lg[i]
+                pkg.ops.moe_decode(to_gpu(x), rp, None, E, G, tau, packed, ws)
+                st = pkg.ops.decode_state(ws, E)
+                assert st["error"] == 0
+                np.testing.assert_array_equal(bits(st["logits"].numpy()), bits(lg[i]))
+                k = int(st["k"])
+                ids = st["sel_ids"].numpy()[:k]
+                np.testing.assert_array_equal(np.sort(ids), np.nonzero(ref_mask[i])[0], err_msg=f"{fam} row {i} tau={tau}")
+                np.testing.assert_array_equal(bits(st["sel_gates"].numpy()[:k]), bits(z[f"{fam}/tau{ti}/gates"][i][ids]))
