@@ -17,6 +17,11 @@ tokens/s + MFMA util.
   (FLOPs = P*6*H*G over selected pairs P, no padding) against 2.5 PFLOP/s bf16 dense.
 * cpu_baseline: the oracle's dense masked layer (oracle/oracle.py masked_moe_mlp,
   numpy float64) on one token per call, timed on this host for ~10 s.
+* roofline.traffic: HBM bytes per decode launch from rocprofv3 FETCH_SIZE and
+  WRITE_SIZE (two --pmc runs of this script with --calibrate-copy-mib), each scaled
+  by the ratio of known bytes to the same counter on a plain elementwise pass of
+  known size; read from profiles/decode16_hbm_traffic.txt (written from the output
+  of --pmc-summary), null when that file is absent.
 """
 from __future__ import annotations
 
@@ -51,11 +56,57 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--grid", type=int, default=0, help="decode workgroups (0 = library default)")
+    ap.add_argument("--calibrate-copy-mib", type=int, default=0,
+                    help="run 5 plain elementwise passes (torch.neg, fp32) over this many MiB first "
+                         "(counter calibration for --pmc)")
+    ap.add_argument("--pmc-summary", default=None,
+                    help="summarise rocprofv3 --pmc csv output under this directory and exit")
     return ap.parse_args()
+
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode16_hbm_traffic.txt")
+
+
+def pmc_summary(d):
+    """Per-kernel mean of each counter per dispatch from rocprofv3 csv output; the
+    calibration pass (kernel name containing 'neg') gives bytes-per-counter-unit."""
+    import collections
+    import csv
+    import glob
+    files = glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)
+    if not files:
+        sys.exit(f"no counter_collection.csv under {d}")
+    agg = collections.defaultdict(lambda: collections.defaultdict(float))
+    disp = collections.defaultdict(set)
+    for f in files:
+        for r in csv.DictReader(open(f)):
+            k = r["Kernel_Name"]
+            agg[k][r["Counter_Name"]] += float(r["Counter_Value"])
+            disp[k].add(r["Dispatch_Id"])
+    calib = {}
+    for k, cs in sorted(agg.items(), key=lambda kv: -len(disp[kv[0]])):
+        n = len(disp[k])
+        line = " ".join(f"{c}={v / n:.6g}" for c, v in sorted(cs.items()))
+        print(f"{n:6d} dispatches  {line}  {k[:90]}")
+        if "neg" in k:
+            calib = {c: v / n for c, v in cs.items()}
+    return calib
+
+
+def read_traffic():
+    if not os.path.exists(TRAFFIC_FILE):
+        return None
+    for line in open(TRAFFIC_FILE):
+        if line.startswith("hbm_bytes_per_launch:"):
+            return float(line.split(":", 1)[1])
+    return None
 
 
 def main():
     args = parse()
+    if args.pmc_summary:
+        pmc_summary(args.pmc_summary)
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (every box has one MI355X); "
               "--gpus must be 1", file=sys.stderr)
@@ -69,6 +120,17 @@ def main():
     ops = pkg.ops
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+
+    if args.calibrate_copy_mib > 0:
+        n = args.calibrate_copy_mib * (1 << 20) // 4
+        src = torch.randn(n, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            torch.neg(src, out=dst)
+        torch.cuda.synchronize()
+        print(f"calibration: 5 x torch.neg over {args.calibrate_copy_mib} MiB fp32 "
+              f"(reads {n * 4} B, writes {n * 4} B per dispatch)", file=sys.stderr)
+        del src, dst
 
     # ---------------- layers (random init, packed once; reference-layout copies not kept)
     layers = []
@@ -249,7 +311,7 @@ def main():
                    "hidden": H, "experts": E, "group_size": G, "tau": args.tau, "batch": 1,
                    "weight_sets": args.layers, "router": "fp32", "x": "fresh N(0,1) fp32 per step"},
         "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": gbs / PEAK_HBM_GBS, "traffic": None,
+                     "frac": gbs / PEAK_HBM_GBS, "traffic": read_traffic(),
                      "bytes_per_step": float(bytes_steps.mean()), "k_mean": float(ks.mean()),
                      "k_min": int(ks.min()), "k_max": int(ks.max())},
         "decode": {"us_per_layer": us_per_step, "hbm_gbs": gbs, "k_mean": float(ks.mean())},

@@ -221,3 +221,32 @@ def test_module_state_dict_roundtrip(pkg, c1):
     m2.load_state_dict(sd_bf)
     out3 = m2(to_gpu(x[None])).float().cpu()
     assert out3.shape == ref.shape  # repacked from the converted router
+
+
+def test_reference_reorder_data_assignment(pkg):
+    """Drop-in as the reference mounts weights: physical_reorder_for_inference
+    (src/openpangu_moe.py:226-244) argsorts the neuron->expert ids, assigns .data of
+    W_gate/W_up [H,I], W_down [I,H] in bf16 and router [H,E] in bf16. The module
+    repacks on the next forward (prefill and decode) and routes from the bf16 router."""
+    H, I, E, G = 1536, 6144, 16, 384
+    w = _layer(55)
+    m = pkg.TauSparseMoE(H, I, E, G, 0.7).to("cuda:0")
+    sort_idx = torch.argsort(torch.from_numpy(w["expert_ids"]).long(), stable=True)
+    dev = torch.device("cuda:0")
+    m.W_gate.data = torch.from_numpy(w["w_gate"])[sort_idx, :].t().contiguous().to(dev, torch.bfloat16)
+    m.W_up.data = torch.from_numpy(w["w_up"])[sort_idx, :].t().contiguous().to(dev, torch.bfloat16)
+    m.W_down.data = torch.from_numpy(w["w_down"])[:, sort_idx].t().contiguous().to(dev, torch.bfloat16)
+    m.router.data = torch.from_numpy(w["w_router"]).T.contiguous().to(dev, torch.bfloat16)
+    x = gi.tokens(56, 40)
+    out = m(to_gpu(x[None])).float().cpu().numpy()[0]
+    res = pkg.ops.route(to_gpu(x), m.router_packed, E, 0.7)
+    lg = res["logits"].cpu().numpy()
+    wr_bf = torch.from_numpy(w["w_router"]).to(torch.bfloat16).double().numpy()
+    np.testing.assert_allclose(lg, x.astype(np.float64) @ wr_bf.T, rtol=1e-5, atol=1e-5)
+    sel = oracle.select(lg, 0.7)
+    np.testing.assert_array_equal(res["mask"].cpu().numpy(), sel.mask)
+    assert_close(out, sparse_expected(x, w, sel.gates), what="prefill after .data mount")
+    od = m(to_gpu(x[None, :1])).float().cpu().numpy()[0, 0]
+    st = pkg.ops.decode_state(m.decode_workspace, E)
+    sel1 = oracle.select(st["logits"].numpy()[None], 0.7)
+    assert_close(od, sparse_expected(x[:1], w, sel1.gates)[0], what="decode after .data mount")
