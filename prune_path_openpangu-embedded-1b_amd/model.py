@@ -1,0 +1,140 @@
+"""Model-side drop-in for the openPangu MoE MLP, eval path.
+
+Mirrors the module tree the reference builds around its kernels, so reference
+checkpoints and model code line up key for key:
+
+* ``IntegratedOpenPanguMoEMLP`` (src/openpangu_moe.py:43-130): ``gate_proj``,
+  ``up_proj``, ``down_proj`` (nn.Linear, taken from the original MLP), ``moelayer``
+  (``MoELayer``: ``mlp_router.0.weight``, ``experts_masks`` and the telemetry
+  buffers), ``tau_moe`` (``TauSparseMoE``: ``W_gate``, ``W_up``, ``W_down``, ``router``).
+  In eval mode ``forward`` runs the MI355X kernels through ``tau_moe``.
+* ``physical_reorder_for_inference`` (src/openpangu_moe.py:212-256): neuron -> expert
+  ids from ``experts_masks``, permuted weights into ``tau_moe`` (one packing pass),
+  then the training-time projections and the masked layer are dropped.
+* ``load_cluster_ids`` reads the reference's partition files
+  (``Pangu_Clusters/layer_{i}_k{G}.txt``, written by ``np.savetxt`` as floats,
+  src/openpangu_moe.py:188-209).
+
+The masked training forward (dense projections + ``MoELayer`` masking and its losses)
+is not part of this build: ``forward`` in training mode raises.
+"""
+from __future__ import annotations
+
+from typing import Any, Iterable, List, Optional
+
+import numpy as np
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from .tau_sparse_moe import TauSparseMoE
+
+
+def load_cluster_ids(path: str) -> np.ndarray:
+    """Neuron -> expert ids from a reference partition file (one id per line, float
+    formatted by np.savetxt). Raises if an entry is not an integer."""
+    v = np.loadtxt(path, dtype=np.float64, ndmin=1)
+    ids = np.rint(v)
+    if not np.array_equal(ids, v):
+        raise ValueError(f"{path}: non-integer expert id")
+    return ids.astype(np.int32)
+
+
+def experts_masks_from_ids(ids, num_experts: int, dtype=torch.float32) -> torch.Tensor:
+    """[E, I] one-hot expert masks (MoELayer.experts_masks layout, src/MoEBlock.py:133-143)."""
+    t = torch.as_tensor(np.asarray(ids), dtype=torch.long)
+    return F.one_hot(t, num_classes=num_experts).t().to(dtype)
+
+
+class MoELayer(nn.Module):
+    """State of the reference's masked routing layer (src/MoEBlock.py:110-152): the
+    router projection and the expert partition, under the reference's names. Only
+    the state is kept; the masked forward belongs to the training path."""
+
+    def __init__(self, hidden_size: int, intermediate_size: int, experts: int, tau: float = 0.95,
+                 experts_id=None):
+        super().__init__()
+        if intermediate_size % experts:
+            raise ValueError("intermediate_size must be divisible by the number of experts")
+        self.experts = experts
+        self.dimension = intermediate_size
+        self.dimension_per_expert = intermediate_size // experts
+        self.tau = tau
+        self.mlp_router = nn.Sequential(nn.Linear(hidden_size, experts, bias=False))
+        if experts_id is None:
+            experts_id = np.repeat(np.arange(experts), self.dimension_per_expert)
+        self.register_buffer("experts_masks", experts_masks_from_ids(experts_id, experts,
+                                                                      self.mlp_router[0].weight.dtype))
+        self.register_buffer("activated_statistics", torch.zeros(experts, dtype=torch.long))
+        self.register_buffer("sparsity_accumulator", torch.zeros(1, dtype=torch.double))
+        self.register_buffer("element_counter", torch.zeros(1, dtype=torch.long))
+
+    def expert_ids(self) -> torch.Tensor:
+        """Neuron -> expert id [I] (argmax over the one-hot masks, src/openpangu_moe.py:229-230)."""
+        return torch.argmax(self.experts_masks.to(torch.int32), dim=0)
+
+    def forward(self, *args, **kwargs):
+        raise NotImplementedError("MoELayer: the masked training forward is not part of this build")
+
+
+class IntegratedOpenPanguMoEMLP(nn.Module):
+    """Eval-mode MoE MLP with the reference's module tree (src/openpangu_moe.py:43-130).
+
+    ``config`` needs ``hidden_size`` (and optionally ``intermediate_size``, default
+    4 * hidden_size); ``train_args`` needs ``group_size`` (and optionally ``tau``).
+    ``original_mlp`` supplies ``gate_proj``/``up_proj``/``down_proj`` (nn.Linear); new
+    ones are created when it is None (for loading a checkpoint)."""
+
+    def __init__(self, config: Any, train_args: Any, original_mlp: Optional[nn.Module] = None,
+                 penalize_logits_list: Optional[List[torch.Tensor]] = None):
+        super().__init__()
+        self.config = config
+        self.train_args = train_args
+        H = getattr(config, "hidden_size", 1536)
+        I = getattr(config, "intermediate_size", H * 4)
+        G = train_args.group_size
+        tau = getattr(train_args, "tau", 0.5)
+        E = I // G
+        if original_mlp is not None:
+            self.gate_proj = getattr(original_mlp, "gate_proj", None)
+            self.up_proj = getattr(original_mlp, "up_proj", None)
+            self.down_proj = getattr(original_mlp, "down_proj", None)
+            self.act_fn = getattr(original_mlp, "act_fn", None) or nn.SiLU()
+        else:
+            self.gate_proj = nn.Linear(H, I, bias=False)
+            self.up_proj = nn.Linear(H, I, bias=False)
+            self.down_proj = nn.Linear(I, H, bias=False)
+            self.act_fn = nn.SiLU()
+        self.penalize_logits_list = penalize_logits_list
+        self.moelayer = MoELayer(H, I, E, tau=getattr(train_args, "tau", 0.95))
+        self.tau_moe = TauSparseMoE(H, I, E, G, tau)
+
+    def forward(self, hidden_states: torch.Tensor, *args, **kwargs) -> torch.Tensor:
+        if self.training:
+            raise NotImplementedError("IntegratedOpenPanguMoEMLP: only the eval (inference) path is built")
+        return self.tau_moe(hidden_states)
+
+    @torch.no_grad()
+    def physical_reorder_for_inference(self, tau: float) -> None:
+        """One layer of src/openpangu_moe.py:222-250: permuted weights into ``tau_moe``
+        (fp32 router), then the projections and the masked layer are dropped."""
+        if self.moelayer is None:
+            raise RuntimeError("physical_reorder_for_inference: already reordered")
+        self.tau_moe.load_from_masked(self.gate_proj.weight, self.up_proj.weight, self.down_proj.weight,
+                                      self.moelayer.mlp_router[0].weight, self.moelayer.experts_masks, tau)
+        self.gate_proj = None
+        self.up_proj = None
+        self.down_proj = None
+        self.moelayer = None
+
+
+def physical_reorder_for_inference(layers: Iterable[nn.Module], tau: float) -> None:
+    """Model-level reorder (src/openpangu_moe.py:212-256): every ``layer.mlp`` that is an
+    ``IntegratedOpenPanguMoEMLP`` is reordered in place; the caching allocator is
+    flushed at the end, as the reference does."""
+    for layer in layers:
+        mlp = getattr(layer, "mlp", layer)
+        if isinstance(mlp, IntegratedOpenPanguMoEMLP):
+            mlp.physical_reorder_for_inference(tau)
+    if torch.cuda.is_available():
+        torch.cuda.empty_cache()

@@ -250,3 +250,60 @@ def test_reference_reorder_data_assignment(pkg):
     st = pkg.ops.decode_state(m.decode_workspace, E)
     sel1 = oracle.select(st["logits"].numpy()[None], 0.7)
     assert_close(od, sparse_expected(x[:1], w, sel1.gates)[0], what="decode after .data mount")
+
+
+def _wrapper(pkg, w, tau, G=384):
+    import types
+    I, H = w["w_gate"].shape
+    cfg = types.SimpleNamespace(hidden_size=H, intermediate_size=I)
+    ta = types.SimpleNamespace(group_size=G, tau=tau)
+    m = pkg.IntegratedOpenPanguMoEMLP(cfg, ta)
+    with torch.no_grad():
+        m.gate_proj.weight.copy_(torch.from_numpy(w["w_gate"]))
+        m.up_proj.weight.copy_(torch.from_numpy(w["w_up"]))
+        m.down_proj.weight.copy_(torch.from_numpy(w["w_down"]))
+        m.moelayer.mlp_router[0].weight.copy_(torch.from_numpy(w["w_router"]))
+        m.moelayer.experts_masks.copy_(pkg.experts_masks_from_ids(w["expert_ids"], w["w_router"].shape[0]))
+    return m.to("cuda:0").eval()
+
+
+@pytest.mark.parametrize("E,G", [(16, 384), (192, 32)])
+def test_model_wrapper_reorder_and_forward(pkg, E, G):
+    """Model-side drop-in: reference module tree -> physical_reorder_for_inference ->
+    eval forward through the kernels (E=192/G=32 with a reference cluster map)."""
+    w = gi.layer_weights(70 + E, E=E)
+    if E == 192:
+        w["expert_ids"] = np.load(os.path.join(GOLDEN, "pangu_clusters_k32.npz"))["expert_ids"][7].astype(np.int32)
+    m = _wrapper(pkg, w, 0.7, G)
+    layer = torch.nn.Module()
+    layer.mlp = m
+    pkg.physical_reorder_for_inference([layer], 0.7)
+    assert m.gate_proj is None and m.moelayer is None
+    x = gi.tokens(71, 24)
+    out = m(to_gpu(x[None])).float().cpu().numpy()[0]
+    res = pkg.ops.route(to_gpu(x), m.tau_moe.router_packed, E, 0.7)
+    sel = oracle.select(res["logits"].cpu().numpy(), 0.7)
+    assert_close(out, sparse_expected(x, w, sel.gates), what=f"wrapper prefill E={E}")
+    od = m(to_gpu(x[None, :1])).float().cpu().numpy()[0, 0]
+    st = pkg.ops.decode_state(m.tau_moe.decode_workspace, E)
+    sel1 = oracle.select(st["logits"].numpy()[None], 0.7)
+    assert_close(od, sparse_expected(x[:1], w, sel1.gates)[0], what=f"wrapper decode E={E}")
+
+
+def test_model_wrapper_reference_checkpoint_roundtrip(pkg):
+    """A checkpoint with the reference's keys (before reorder) loads into a fresh
+    wrapper and gives the same outputs after the reorder."""
+    import types
+    w = gi.layer_weights(73)
+    m = _wrapper(pkg, w, 0.7)
+    sd = {k: v.detach().cpu().clone() for k, v in m.state_dict().items()}
+    cfg = types.SimpleNamespace(hidden_size=1536, intermediate_size=6144)
+    m2 = pkg.IntegratedOpenPanguMoEMLP(cfg, types.SimpleNamespace(group_size=384, tau=0.7))
+    m2.load_state_dict(sd)
+    m2 = m2.to("cuda:0").eval()
+    m.physical_reorder_for_inference(0.7)
+    m2.physical_reorder_for_inference(0.7)
+    x = gi.tokens(74, 16)
+    a = m(to_gpu(x[None])).float().cpu()
+    b = m2(to_gpu(x[None])).float().cpu()
+    assert torch.equal(a, b)
