@@ -55,6 +55,8 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the small-batch (config 3) and E=192/G=32 side measurements")
     ap.add_argument("--grid", type=int, default=0, help="decode workgroups (0 = library default)")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="run 5 plain elementwise passes (torch.neg, fp32) over this many MiB first "
@@ -285,6 +287,88 @@ def main():
             "layer_mfma_util": (6.0 * P_mean * H * G) / (pf_ms * 1e-3) / (PEAK_BF16_TFLOPS * 1e12),
         }
 
+    # ---------------- side measurements (not the headline value)
+    extra = None
+    if not args.no_extra:
+        extra = {}
+        # config 3: small-batch decode, bs 16 and 64, tau 0.95, Zipf(1.2) router bias;
+        # bytes = union of the selected experts' records + router + x
+        bias = torch.from_numpy(gi.zipf_bias(E)).to(dev)
+        for nb in (16, 64):
+            R = 32
+            xq = torch.randn(R, nb, H, device=dev, generator=g)
+            wsq = torch.empty(ops.prefill_workspace_bytes(nb, H, E, G), dtype=torch.uint8, device=dev)
+            outq = torch.empty(nb, H, dtype=torch.bfloat16, device=dev)
+            union = []
+            for r in range(R):
+                packed, rp, _ = layers[r % len(layers)]
+                m = ops.route(xq[r], rp, E, 0.95, bias=bias, want_logits=False)["mask"]
+                union.append(int((m.sum(0) > 0).sum()))
+                ops.moe_prefill(xq[r], rp, bias, E, G, 0.95, packed, workspace=wsq, out=outq)
+            torch.cuda.synchronize()
+            gq = torch.cuda.CUDAGraph()
+            sq = torch.cuda.Stream()
+            sq.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(sq):
+                with torch.cuda.graph(gq, stream=sq):
+                    for r in range(R):
+                        packed, rp, _ = layers[r % len(layers)]
+                        ops.moe_prefill(xq[r], rp, bias, E, G, 0.95, packed, workspace=wsq, out=outq)
+            torch.cuda.current_stream().wait_stream(sq)
+            gq.replay()
+            torch.cuda.synchronize()
+            e0.record()
+            gq.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) * 1000.0 / R
+            u = float(np.mean(union))
+            byt = u * 3 * H * G * 2 + Epad * H * 4 + nb * H * 4 + nb * H * 2
+            extra[f"bs{nb}"] = {"us_per_layer": us, "tokens_per_s": nb / (us * 1e-6), "experts_hit_mean": u,
+                                "hbm_gbs": byt / (us * 1e-6) / 1e9, "tau": 0.95, "router_bias": "zipf(1.2)"}
+        # real-checkpoint shape: E=192 experts of G=32, one layer, decode bs=1 and prefill 2048
+        E2, G2 = 192, 32
+        l192 = []
+        NS = 8
+        for l in range(NS):
+            g.manual_seed(2000 + l)
+            wg = torch.randn(I, H, device=dev, generator=g) * 0.02
+            wu = torch.randn(I, H, device=dev, generator=g) * 0.02
+            wd = torch.randn(H, I, device=dev, generator=g) * 0.02
+            wr = torch.randn(E2, H, device=dev, generator=g) * 0.02
+            perm = torch.randperm(I, device=dev, generator=g).to(torch.int32)
+            l192.append((ops.pack_experts(wg, wu, wd, E2, G2, perm=perm, layout="linear"),
+                         ops.pack_router(wr, layout="linear"), ops.decode_workspace(H, E2, dev)))
+            del wg, wu, wd
+        R = 64
+        xd = torch.randn(R, H, device=dev, generator=g)
+        od = torch.empty(R, H, dtype=torch.bfloat16, device=dev)
+        kk = []
+        for r in range(R):
+            packed, rp, ws = l192[r % NS]
+            ops.moe_decode(xd[r], rp, None, E2, G2, args.tau, packed, ws, out=od[r:r + 1])
+            kk.append(ops.decode_state(ws, E2)["k"])
+        gd = torch.cuda.CUDAGraph()
+        sd_ = torch.cuda.Stream()
+        sd_.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(sd_):
+            with torch.cuda.graph(gd, stream=sd_):
+                for r in range(R):
+                    packed, rp, ws = l192[r % NS]
+                    ops.moe_decode(xd[r], rp, None, E2, G2, args.tau, packed, ws, out=od[r:r + 1])
+        torch.cuda.current_stream().wait_stream(sd_)
+        gd.replay()
+        torch.cuda.synchronize()
+        e0.record()
+        gd.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1000.0 / R
+        k2 = float(np.mean(kk))
+        byt = k2 * 3 * H * G2 * 2 + 192 * H * 4 + H * 6
+        extra["e192_g32_decode"] = {"us_per_layer": us, "k_mean": k2, "hbm_gbs": byt / (us * 1e-6) / 1e9,
+                                    "weight_sets": NS}
+
     # ---------------- CPU baseline: oracle dense masked layer, one token per call
     cpu = None
     if not args.no_cpu:
@@ -316,6 +400,7 @@ def main():
                      "k_min": int(ks.min()), "k_max": int(ks.max())},
         "decode": {"us_per_layer": us_per_step, "hbm_gbs": gbs, "k_mean": float(ks.mean())},
         "prefill": prefill,
+        "side": extra,
         "cpu_baseline": cpu,
     }
     print(json.dumps(res))

@@ -178,60 +178,75 @@ __global__ __launch_bounds__(DEC_THREADS) void decode_kernel(
       if (tid == 0) st_rlx(&st->k, k_s);
     }
   } else {
-    // ---------------- router workgroups 0..R-1, then a flag
-    if (b < R) {
-      for (int e = b; e < E; e += R) {
-        float sacc = 0.0f;
-        for (int k = tid; k < H; k += DEC_THREADS)
-          sacc = __builtin_fmaf(load_as_f32<XT>(x, k), router[(int64_t)e * H + k], sacc);
-        sacc = wave_sum(sacc);
-        if (lane == 0) red4[wv] = sacc;
-        __syncthreads();
-        if (tid == 0) {
-          float l = __fadd_rn(__fadd_rn(__fadd_rn(red4[0], red4[1]), red4[2]), red4[3]);
-          if (bias) l = __fadd_rn(l, bias[e]);
-          st_rlx(&st->logits[e], l);
-        }
-        __syncthreads();
+    // ---------------- router workgroups 0..E-1 (one expert each) publish their logit
+    // as {tag, value} in one 64-bit store to their own slot; every workgroup gathers
+    // the E slots (bounded spin) and selects for itself. The tag is this call's
+    // epoch + 1; the last workgroup of the call stores it as the new epoch. No counter
+    // is shared while routing (192 increments of one address serialise at the memory
+    // side), and no second round trip for a published selection.
+    unsigned long long* slots = (unsigned long long*)(acc + (size_t)DEC_NCOPY * H);
+    const uint32_t tag = ld_rlx(&st->router_ticket) + 1u;
+    if (b < E) {
+      const int e = b;
+      // H <= 4096: at most 16 elements per thread, all loaded before the first FMA
+      // (one memory round trip), then added in k order
+      constexpr int KPT = 4096 / DEC_THREADS;
+      float xv[KPT], wr[KPT];
+#pragma unroll
+      for (int i = 0; i < KPT; ++i) {
+        const int kk = tid + i * DEC_THREADS;
+        xv[i] = kk < H ? load_as_f32<XT>(x, kk) : 0.0f;
+        wr[i] = kk < H ? router[(int64_t)e * H + kk] : 0.0f;
       }
+      float sacc = 0.0f;
+#pragma unroll
+      for (int i = 0; i < KPT; ++i)
+        if (tid + i * DEC_THREADS < H) sacc = __builtin_fmaf(xv[i], wr[i], sacc);
+      sacc = wave_sum(sacc);
+      if (lane == 0) red4[wv] = sacc;
+      __syncthreads();
       if (tid == 0) {
-        vm_wait();  // this workgroup's logits are performed before its ticket
-        flag_s = add_rlx(&st->router_ticket, 1u) == (uint32_t)(R - 1);
+        float l = __fadd_rn(__fadd_rn(__fadd_rn(red4[0], red4[1]), red4[2]), red4[3]);
+        if (bias) l = __fadd_rn(l, bias[e]);
+        st_rlx(&slots[e], ((unsigned long long)tag << 32) | __float_as_uint(l));
       }
-      __syncthreads();
-      if (flag_s && wv == 0) {  // last router workgroup: selection, then publish
-        select_one_token([&](int j) { return ld_rlx(&st->logits[j]); }, E, tau, &ss, lane);
-        const int k = ss.k;
-        for (int q = lane; q < k; q += 64) {
-          const int e = ss.order[q];
-          st_rlx(&st->sel_ids[q], e);
-          st_rlx(&st->sel_gates[q], pp_sigmoid(ld_rlx(&st->logits[e])));
-        }
-        if (lane == 0) st_rlx(&st->k, k);
-        vm_wait();
-        if (lane == 0) st_rlx(&st->ready, 1u);
-      }
-      __syncthreads();
     }
-    if (tid == 0) {
+    for (int j = tid; j < E; j += DEC_THREADS) {
+      unsigned long long v = ld_rlx(&slots[j]);
       uint32_t n = 0;
-      int ok = 1;
-      while (ld_rlx(&st->ready) == 0u) {
+      while ((uint32_t)(v >> 32) != tag) {
         __builtin_amdgcn_s_sleep(1);
         if (++n > DEC_SPIN_LIMIT) {
           __hip_atomic_fetch_or(&st->error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          ok = 0;
           break;
         }
+        v = ld_rlx(&slots[j]);
       }
-      k_s = ok ? ld_rlx(&st->k) : 0;
+      lg_s[j] = __uint_as_float((uint32_t)v);
     }
     __syncthreads();
-    for (int q = tid; q < k_s; q += DEC_THREADS) {
-      sel_ids_s[q] = ld_rlx(&st->sel_ids[q]);
-      sel_g_s[q] = ld_rlx(&st->sel_gates[q]);
+    if (E <= 16) {
+      if (wv == 0) select_one_token([&](int j) { return lg_s[j]; }, E, tau, &ss, lane);
+      __syncthreads();
+    } else {
+      select_one_token_wg([&](int j) { return lg_s[j]; }, E, tau, &ss, tid, DEC_THREADS);
     }
+    const int kq = ss.k;
+    for (int q = tid; q < kq; q += DEC_THREADS) {
+      const int e = ss.order[q];
+      sel_ids_s[q] = e;
+      sel_g_s[q] = pp_sigmoid(lg_s[e]);
+    }
+    if (tid == 0) k_s = kq;
     __syncthreads();
+    if (b == 0) {  // telemetry for the caller: logits and selection of this call
+      for (int j = tid; j < E; j += DEC_THREADS) st_rlx(&st->logits[j], lg_s[j]);
+      for (int q = tid; q < k_s; q += DEC_THREADS) {
+        st_rlx(&st->sel_ids[q], sel_ids_s[q]);
+        st_rlx(&st->sel_gates[q], sel_g_s[q]);
+      }
+      if (tid == 0) st_rlx(&st->k, k_s);
+    }
   }
   const int k = k_s;
 
@@ -351,19 +366,32 @@ __global__ __launch_bounds__(DEC_THREADS) void decode_kernel(
   if (tid == 0) flag_s = add_rlx(&st->done, 1u) == (uint32_t)(W - 1);
   __syncthreads();
   if (flag_s) {  // last workgroup: fold copies, write bf16, clear, reset counters
-    for (int h = tid; h < H; h += DEC_THREADS) {
-      float sv[DEC_NCOPY];
+    // DEC_FOLD_H values of h per thread per pass, every load of a pass issued before
+    // the first add (one round trip per pass; one pass for H <= 2048)
+    constexpr int DEC_FOLD_H = 8;
+    for (int h0 = 0; h0 < H; h0 += DEC_THREADS * DEC_FOLD_H) {
+      float sv[DEC_FOLD_H][DEC_NCOPY];
 #pragma unroll
-      for (int c = 0; c < DEC_NCOPY; ++c) sv[c] = ld_rlx(acc + (size_t)c * H + h);
-      float tot = 0.0f;
+      for (int i = 0; i < DEC_FOLD_H; ++i) {
+        const int h = h0 + tid + i * DEC_THREADS;
 #pragma unroll
-      for (int c = 0; c < DEC_NCOPY; ++c) tot += sv[c];
+        for (int c = 0; c < DEC_NCOPY; ++c) sv[i][c] = h < H ? ld_rlx(acc + (size_t)c * H + h) : 0.0f;
+      }
 #pragma unroll
-      for (int c = 0; c < DEC_NCOPY; ++c) st_rlx(acc + (size_t)c * H + h, 0.0f);
-      out[h] = f32_to_bf16(tot);
+      for (int i = 0; i < DEC_FOLD_H; ++i) {
+        const int h = h0 + tid + i * DEC_THREADS;
+        if (h < H) {
+          float tot = 0.0f;
+#pragma unroll
+          for (int c = 0; c < DEC_NCOPY; ++c) tot += sv[i][c];
+#pragma unroll
+          for (int c = 0; c < DEC_NCOPY; ++c) st_rlx(acc + (size_t)c * H + h, 0.0f);
+          out[h] = f32_to_bf16(tot);
+        }
+      }
     }
     if (tid == 0) {
-      st_rlx(&st->router_ticket, 0u);
+      if (!LOCAL) st_rlx(&st->router_ticket, ld_rlx(&st->router_ticket) + 1u);  // routing epoch
       st_rlx(&st->done, 0u);
       st_rlx(&st->ready, 0u);
     }
@@ -668,9 +696,10 @@ __global__ void decode_ws_clear_kernel(uint32_t* p, size_t n_words) {
     p[i] = 0u;
 }
 
+// state | DEC_NCOPY x H fp32 accumulators | PP_MAX_EXPERTS 64-bit logit slots
 extern "C" size_t pp_decode_workspace_bytes(int H, int E) {
   (void)E;
-  return dec_acc_offset() + (size_t)DEC_NCOPY * H * sizeof(float);
+  return dec_acc_offset() + (size_t)DEC_NCOPY * H * sizeof(float) + PP_MAX_EXPERTS * sizeof(unsigned long long);
 }
 
 extern "C" int pp_decode_workspace_init(void* workspace, int H, int E, void* stream) {
@@ -715,9 +744,9 @@ extern "C" int pp_moe_decode(const void* x, int x_dtype, int H, const float* rou
              x_dtype);
   PP_REQUIRE(grid >= 0 && grid <= 65536, PP_ERR_INVALID, "pp_moe_decode: grid %d", grid);
   const int grid_in = grid;
-  const int R = E < 64 ? E : 64;
-  if (grid == 0) grid = 2 * pp_device_cus();
-  if (grid < R) grid = R;
+  const int R = E;  // router workgroups: one expert each
+  if (grid == 0) grid = pp_device_cus();
+  if (grid < R) grid = R;  // every expert has its router workgroup
   const int cpl = (H / 8 + 63) / 64;  // 16-byte chunks per lane per row (H <= 4096 -> <= 8)
   const size_t smem = (size_t)3 * H * sizeof(float);
   pp_decode_state* st = (pp_decode_state*)workspace;

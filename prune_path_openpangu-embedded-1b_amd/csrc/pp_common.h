@@ -465,18 +465,34 @@ static __device__ void select_one_token(LG lg, int E, float tau, SelScratch* ss,
     if (j < E) ss->e[j] = pv[i];
   }
   wave_sync_lds();
+  // ranks of this lane's experts: one pass over the E values, 16 per step read as
+  // float4 (independent LDS reads, shared by the lane's up to four experts)
+  int rank[PP_MAX_EXPERTS / PP_WAVE];
+#pragma unroll
+  for (int i = 0; i < PP_MAX_EXPERTS / PP_WAVE; ++i) rank[i] = 0;
+  for (int q0 = 0; q0 < E; q0 += 16) {
+    float pq[16];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const float4 v4 = *(const float4*)&ss->e[q0 + 4 * u];
+      pq[4 * u] = v4.x; pq[4 * u + 1] = v4.y; pq[4 * u + 2] = v4.z; pq[4 * u + 3] = v4.w;
+    }
+#pragma unroll
+    for (int i = 0; i < PP_MAX_EXPERTS / PP_WAVE; ++i) {
+      const int j = lane + i * PP_WAVE;
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        const int q = q0 + u;
+        rank[i] += (q < E && (kv_before(pq[u], pv[i]) || (pq[u] == pv[i] && q < j))) ? 1 : 0;
+      }
+    }
+  }
 #pragma unroll
   for (int i = 0; i < PP_MAX_EXPERTS / PP_WAVE; ++i) {
-    int j = lane + i * PP_WAVE;
+    const int j = lane + i * PP_WAVE;
     if (j < E) {
-      float pj = pv[i];
-      int rank = 0;
-      for (int q = 0; q < E; ++q) {
-        float pq = ss->e[q];
-        rank += (kv_before(pq, pj) || (pq == pj && q < j)) ? 1 : 0;
-      }
-      ss->srt[rank] = pj;
-      ss->order[rank] = j;
+      ss->srt[rank[i]] = pv[i];
+      ss->order[rank[i]] = j;
     }
   }
   wave_sync_lds();
@@ -491,4 +507,125 @@ static __device__ void select_one_token(LG lg, int E, float tau, SelScratch* ss,
     ss->tie = tie;
   }
   wave_sync_lds();
+}
+
+// Selection of one token by a whole workgroup of nthreads threads, E > 16, with the
+// same result as select_one_token:
+// * softmax by wave 0 in torch's reduce order (16 lane columns summed chunk by chunk,
+//   the tail into the low lanes, then the halves tree);
+// * ranks counted by all threads on 64-bit keys (~bits(p) << 32 | index): for p >= 0
+//   and NaN their unsigned order is exactly "NaN first, then descending, equal values
+//   by index" (kv_before plus the index tie-break);
+// * the fp64 running-sum cut: when every selected-candidate p is 0 or >= 2^-29, every
+//   partial sum of the sorted p (< 2) is an exact multiple of 2^-52 and so exact in
+//   double, whatever the order of the additions -- wave 0 computes the prefix in
+//   parallel; otherwise lane 0 runs the sequential sum;
+// * a tie straddling the cut falls back to the introsort restatement (lane 0).
+// Every thread of the workgroup must call it.
+__device__ __forceinline__ unsigned long long sel_key(float p, int j) {
+  const uint32_t b = (p != p) ? 0xffffffffu : __float_as_uint(p);
+  return ((unsigned long long)(~b) << 32) | (uint32_t)j;
+}
+
+template <typename LG>
+static __device__ void select_one_token_wg(LG lg, int E, float tau, SelScratch* ss, int tid, int nthreads) {
+  const int lane = tid & 63;
+  if (tid < PP_WAVE) {
+    float m = -__builtin_huge_valf();
+    for (int j = lane; j < E; j += PP_WAVE) m = fmaxf(m, lg(j));
+    m = wave_max(m);
+    for (int j = lane; j < E; j += PP_WAVE) ss->e[j] = pp_expf_u10(__fsub_rn(lg(j), m));
+    wave_sync_lds();
+    float acc = 0.0f;
+    if (lane < 16) {
+      // column `lane` of the 16-wide chunks, all loads first, then added in chunk order
+      float col[PP_MAX_EXPERTS / 16];
+#pragma unroll
+      for (int c = 0; c < PP_MAX_EXPERTS / 16; ++c) col[c] = (16 * c + lane < E) ? ss->e[16 * c + lane] : 0.0f;
+      acc = col[0];
+#pragma unroll
+      for (int c = 1; c < PP_MAX_EXPERTS / 16; ++c)
+        if (16 * c + lane < E) acc = __fadd_rn(acc, col[c]);
+    }
+#pragma unroll
+    for (int o = 8; o >= 1; o >>= 1) acc = __fadd_rn(acc, __shfl_xor(acc, o, PP_WAVE));
+    const float r = __fdiv_rn(1.0f, __shfl(acc, 0, PP_WAVE));
+    float pv[PP_MAX_EXPERTS / PP_WAVE];
+#pragma unroll
+    for (int i = 0; i < PP_MAX_EXPERTS / PP_WAVE; ++i) {
+      const int j = lane + i * PP_WAVE;
+      pv[i] = j < E ? __fmul_rn(ss->e[j], r) : 0.0f;
+    }
+    wave_sync_lds();
+#pragma unroll
+    for (int i = 0; i < PP_MAX_EXPERTS / PP_WAVE; ++i) {
+      const int j = lane + i * PP_WAVE;
+      if (j < E) ss->e[j] = pv[i];
+    }
+  }
+  __syncthreads();
+  for (int j = tid; j < E; j += nthreads) {
+    const float pj = ss->e[j];
+    const unsigned long long kj = sel_key(pj, j);
+    int rank = 0;
+    for (int q0 = 0; q0 < E; q0 += 16) {
+      float pq[16];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const float4 v4 = *(const float4*)&ss->e[q0 + 4 * u];
+        pq[4 * u] = v4.x; pq[4 * u + 1] = v4.y; pq[4 * u + 2] = v4.z; pq[4 * u + 3] = v4.w;
+      }
+#pragma unroll
+      for (int u = 0; u < 16; ++u) rank += (q0 + u < E && sel_key(pq[u], q0 + u) < kj) ? 1 : 0;
+    }
+    ss->srt[rank] = pj;
+    ss->order[rank] = j;
+  }
+  __syncthreads();
+  if (tid < PP_WAVE) {
+    constexpr int QPL = PP_MAX_EXPERTS / PP_WAVE;  // sorted positions per lane
+    float v[QPL];
+    bool exact = true;
+#pragma unroll
+    for (int i = 0; i < QPL; ++i) {
+      const int q = lane * QPL + i;
+      v[i] = q < E ? ss->srt[q] : 0.0f;
+      exact = exact && (v[i] == 0.0f || v[i] >= 0x1p-29f);  // NaN fails both
+    }
+    int k;
+    if (__all(exact)) {
+      double s[QPL], run = 0.0;
+#pragma unroll
+      for (int i = 0; i < QPL; ++i) {
+        run += (double)v[i];
+        s[i] = run;
+      }
+      double incl = run;
+#pragma unroll
+      for (int o = 1; o < PP_WAVE; o <<= 1) {
+        const double t = __shfl_up(incl, o, PP_WAVE);
+        if (lane >= o) incl += t;
+      }
+      const double excl = incl - run;
+      const float tau32 = tau;
+      int c = 0;
+#pragma unroll
+      for (int i = 0; i < QPL; ++i) c += (lane * QPL + i < E && (float)(excl + s[i]) < tau32) ? 1 : 0;
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) c += __shfl_xor(c, o, PP_WAVE);
+      k = c > 0 ? c : 1;
+    } else {
+      k = tau_cut([&](int q) { return ss->srt[q]; }, E, tau);
+    }
+    if (lane == 0) {
+      ss->k = k;
+      const int tie = (k < E && ss->srt[k - 1] == ss->srt[k]) ? 1 : 0;
+      ss->tie = tie;
+      if (tie) {
+        for (int j = 0; j < E; ++j) { ss->srt[j] = ss->e[j]; ss->order[j] = j; }
+        kv_introsort(ss->srt, ss->order, E, ss->stk);
+      }
+    }
+  }
+  __syncthreads();
 }

@@ -136,11 +136,13 @@ def test_route16_hidden_sizes(pkg, H):
     np.testing.assert_array_equal(bits(res["probs"].cpu().numpy()), bits(sel.probs))
 
 
-def test_decode16_selection_vs_golden(pkg):
-    """The fused decode kernel's in-kernel selection (E = 16), pinned the same way:
-    identity router, x = golden logits, one token per call."""
-    E, H, G = 16, 512, 32
-    z = np.load(os.path.join(GOLDEN, "routing_E16.npz"))
+@pytest.mark.parametrize("E", [16, 24, 32, 192])
+def test_decode_selection_vs_golden(pkg, E):
+    """The fused decode kernels' in-kernel selection, pinned the same way: identity
+    router, x = golden logits, one token per call (E = 16: decode16_kernel; otherwise
+    the gathered-logits path of decode_kernel with the workgroup selection)."""
+    H, G = 512, 32
+    z = np.load(os.path.join(GOLDEN, f"routing_E{E}.npz"))
     rp = _identity_router(pkg, E, H)
     rng = np.random.default_rng(1)
     I = E * G
