@@ -131,7 +131,7 @@ int pp_bucket(const uint8_t* mask, const float* gates, int64_t n_tokens, int E, 
  * grid = number of workgroups (0 = automatic).
  * ------------------------------------------------------------------------- */
 typedef struct pp_decode_state {
-  uint32_t router_ticket; /* internal */
+  uint32_t router_ticket; /* internal: call epoch, advanced by one per call */
   uint32_t ready;         /* internal */
   uint32_t done;          /* internal */
   uint32_t error;         /* non-zero: a wait timed out, output invalid */

@@ -42,6 +42,7 @@
 
 static inline size_t dec_acc_offset() { return (sizeof(pp_decode_state) + 255) / 256 * 256; }
 
+
 __device__ __forceinline__ void vm_wait() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 template <typename T>
 __device__ __forceinline__ T ld_rlx(const T* p) {
@@ -53,6 +54,26 @@ __device__ __forceinline__ void st_rlx(T* p, T v) {
 }
 __device__ __forceinline__ uint32_t add_rlx(uint32_t* p, uint32_t v) {
   return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Accumulators: two sets of DEC_NCOPY x H fp32, used by alternate calls (parity of the
+// call epoch, st->router_ticket, which the last workgroup of every call advances).
+// Call N adds into set N & 1 and its last workgroup only reads it; the workgroups of
+// call N+1 clear set N & 1 early in the call, off the critical path, so call N+2
+// finds it zero. 64-bit logit slots follow the two sets.
+__device__ __forceinline__ float* dec_acc_set(float* acc, int H, uint32_t epoch) {
+  return acc + (size_t)(epoch & 1u) * DEC_NCOPY * H;
+}
+__device__ __forceinline__ unsigned long long* dec_slots(float* acc, int H) {
+  return (unsigned long long*)(acc + (size_t)2 * DEC_NCOPY * H);
+}
+// this workgroup's share of clearing the other set (the previous call's)
+__device__ __forceinline__ void dec_clear_previous(float* acc, int H, uint32_t epoch, int b, int W, int tid,
+                                                   int nthreads) {
+  float* prev = dec_acc_set(acc, H, epoch + 1u);
+  int lo, hi;
+  pp_split((uint32_t)(DEC_NCOPY * H), (uint32_t)W, (uint32_t)b, lo, hi);
+  for (int i = lo + tid; i < hi; i += nthreads) st_rlx(prev + i, 0.0f);
 }
 
 // 8 bf16 packed in a uint4: dot with x[8], or acc += a * w
@@ -145,6 +166,7 @@ __global__ __launch_bounds__(DEC_THREADS) void decode_kernel(
   extern __shared__ __align__(16) float red[];  // [3][H] wave partials
   __shared__ SelScratch ss;
   __shared__ float red4[4];
+  __shared__ unsigned long long keys_s[PP_MAX_EXPERTS];
   __shared__ float lg_s[PP_MAX_EXPERTS];
   __shared__ int flag_s;
   __shared__ int k_s;
@@ -154,6 +176,7 @@ __global__ __launch_bounds__(DEC_THREADS) void decode_kernel(
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int W = gridDim.x, b = blockIdx.x;
   const int HC = H >> 3;  // 16-byte chunks per row
+  const uint32_t epoch = ld_rlx(&st->router_ticket);
 
   if (LOCAL) {
     // ---------------- every workgroup routes the token itself
@@ -184,10 +207,9 @@ __global__ __launch_bounds__(DEC_THREADS) void decode_kernel(
     // epoch + 1; the last workgroup of the call stores it as the new epoch. No counter
     // is shared while routing (192 increments of one address serialise at the memory
     // side), and no second round trip for a published selection.
-    unsigned long long* slots = (unsigned long long*)(acc + (size_t)DEC_NCOPY * H);
-    const uint32_t tag = ld_rlx(&st->router_ticket) + 1u;
+    unsigned long long* slots = dec_slots(acc, H);
+    const uint32_t tag = epoch + 1u;
     if (b < E) {
-      const int e = b;
       // H <= 4096: at most 16 elements per thread, all loaded before the first FMA
       // (one memory round trip), then added in k order
       constexpr int KPT = 4096 / DEC_THREADS;
@@ -196,7 +218,7 @@ __global__ __launch_bounds__(DEC_THREADS) void decode_kernel(
       for (int i = 0; i < KPT; ++i) {
         const int kk = tid + i * DEC_THREADS;
         xv[i] = kk < H ? load_as_f32<XT>(x, kk) : 0.0f;
-        wr[i] = kk < H ? router[(int64_t)e * H + kk] : 0.0f;
+        wr[i] = kk < H ? router[(int64_t)b * H + kk] : 0.0f;
       }
       float sacc = 0.0f;
 #pragma unroll
@@ -207,10 +229,13 @@ __global__ __launch_bounds__(DEC_THREADS) void decode_kernel(
       __syncthreads();
       if (tid == 0) {
         float l = __fadd_rn(__fadd_rn(__fadd_rn(red4[0], red4[1]), red4[2]), red4[3]);
-        if (bias) l = __fadd_rn(l, bias[e]);
-        st_rlx(&slots[e], ((unsigned long long)tag << 32) | __float_as_uint(l));
+        if (bias) l = __fadd_rn(l, bias[b]);
+        st_rlx(&slots[b], ((unsigned long long)tag << 32) | __float_as_uint(l));
       }
     }
+    // router workgroup e publishes {tag, logit} in its own 64-bit slot; every workgroup
+    // gathers the E slots (bounded spin). No counter is shared while routing (E
+    // increments of one address serialise at the memory side).
     for (int j = tid; j < E; j += DEC_THREADS) {
       unsigned long long v = ld_rlx(&slots[j]);
       uint32_t n = 0;
@@ -229,7 +254,7 @@ __global__ __launch_bounds__(DEC_THREADS) void decode_kernel(
       if (wv == 0) select_one_token([&](int j) { return lg_s[j]; }, E, tau, &ss, lane);
       __syncthreads();
     } else {
-      select_one_token_wg([&](int j) { return lg_s[j]; }, E, tau, &ss, tid, DEC_THREADS);
+      select_one_token_wg([&](int j) { return lg_s[j]; }, E, tau, &ss, keys_s, red4, tid, DEC_THREADS);
     }
     const int kq = ss.k;
     for (int q = tid; q < kq; q += DEC_THREADS) {
@@ -249,6 +274,7 @@ __global__ __launch_bounds__(DEC_THREADS) void decode_kernel(
     }
   }
   const int k = k_s;
+  dec_clear_previous(acc, H, epoch, b, W, tid, DEC_THREADS);
 
   // ---------------- stream the selected neuron records
   // this workgroup: records [v0, v1) of the k*G selected ones; wave wv a contiguous
@@ -355,7 +381,7 @@ __global__ __launch_bounds__(DEC_THREADS) void decode_kernel(
   }
   __syncthreads();
   if (has_work) {
-    float* accc = acc + (size_t)(b % DEC_NCOPY) * H;
+    float* accc = dec_acc_set(acc, H, epoch) + (size_t)(b % DEC_NCOPY) * H;
     for (int h = tid; h < H; h += DEC_THREADS) {
       const float sv = (red[h] + red[H + h]) + red[2 * H + h];
       unsafeAtomicAdd(accc + h, sv);
@@ -365,17 +391,18 @@ __global__ __launch_bounds__(DEC_THREADS) void decode_kernel(
   __syncthreads();
   if (tid == 0) flag_s = add_rlx(&st->done, 1u) == (uint32_t)(W - 1);
   __syncthreads();
-  if (flag_s) {  // last workgroup: fold copies, write bf16, clear, reset counters
+  if (flag_s) {  // last workgroup: fold copies, write bf16, advance the epoch, reset counters
     // DEC_FOLD_H values of h per thread per pass, every load of a pass issued before
     // the first add (one round trip per pass; one pass for H <= 2048)
     constexpr int DEC_FOLD_H = 8;
+    const float* accs = dec_acc_set(acc, H, epoch);
     for (int h0 = 0; h0 < H; h0 += DEC_THREADS * DEC_FOLD_H) {
       float sv[DEC_FOLD_H][DEC_NCOPY];
 #pragma unroll
       for (int i = 0; i < DEC_FOLD_H; ++i) {
         const int h = h0 + tid + i * DEC_THREADS;
 #pragma unroll
-        for (int c = 0; c < DEC_NCOPY; ++c) sv[i][c] = h < H ? ld_rlx(acc + (size_t)c * H + h) : 0.0f;
+        for (int c = 0; c < DEC_NCOPY; ++c) sv[i][c] = h < H ? ld_rlx(accs + (size_t)c * H + h) : 0.0f;
       }
 #pragma unroll
       for (int i = 0; i < DEC_FOLD_H; ++i) {
@@ -384,14 +411,12 @@ __global__ __launch_bounds__(DEC_THREADS) void decode_kernel(
           float tot = 0.0f;
 #pragma unroll
           for (int c = 0; c < DEC_NCOPY; ++c) tot += sv[i][c];
-#pragma unroll
-          for (int c = 0; c < DEC_NCOPY; ++c) st_rlx(acc + (size_t)c * H + h, 0.0f);
           out[h] = f32_to_bf16(tot);
         }
       }
     }
     if (tid == 0) {
-      if (!LOCAL) st_rlx(&st->router_ticket, ld_rlx(&st->router_ticket) + 1u);  // routing epoch
+      st_rlx(&st->router_ticket, epoch + 1u);  // next call: other accumulator set, new slot tag
       st_rlx(&st->done, 0u);
       st_rlx(&st->ready, 0u);
     }
@@ -445,6 +470,7 @@ __global__ __launch_bounds__(64 * NW) void decode16_kernel(
   __shared__ float sel_g_s[16];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int W = gridDim.x, b = blockIdx.x;
+  const uint32_t epoch = ld_rlx(&st->router_ticket);  // accumulator set parity
 
   // ---- logits: wave wv -> experts EPW*wv ..; lane -> x chunks lane + 64 c (8 values each)
   constexpr int EPW = 16 / NW;  // experts per wave (4 or 2)
@@ -570,6 +596,8 @@ __global__ __launch_bounds__(64 * NW) void decode16_kernel(
     if (tid == 0) st_rlx(&st->k, k);
   }
 
+  dec_clear_previous(acc, H, epoch, b, W, tid, NT);
+
   // ---- stream the selected neuron records (as decode_kernel)
   const int T = k * G;
   int v0, v1;
@@ -648,7 +676,7 @@ __global__ __launch_bounds__(64 * NW) void decode16_kernel(
       }
     }
     __syncthreads();
-    float* accc = acc + (b % DEC_NCOPY) * H;
+    float* accc = dec_acc_set(acc, H, epoch) + (b % DEC_NCOPY) * H;
 #pragma unroll
     for (int i = 0; i < (H + NT - 1) / NT; ++i) {
       const int h = tid + NT * i;
@@ -664,16 +692,17 @@ __global__ __launch_bounds__(64 * NW) void decode16_kernel(
   __syncthreads();
   if (tid == 0) flag_s = add_rlx(&st->done, 1u) == (uint32_t)(W - 1);
   __syncthreads();
-  if (flag_s) {  // last workgroup: fold copies, write bf16, clear, reset the counter
+  if (flag_s) {  // last workgroup: fold copies, write bf16, advance the epoch, reset the counter
     // every load of the fold is issued before the first add (one round trip)
     constexpr int HPT = (H + NT - 1) / NT;
+    const float* accs = dec_acc_set(acc, H, epoch);
     float sv[HPT][DEC_NCOPY];
 #pragma unroll
     for (int i = 0; i < HPT; ++i)
 #pragma unroll
       for (int c = 0; c < DEC_NCOPY; ++c) {
         const int h = tid + NT * i;
-        sv[i][c] = h < H ? ld_rlx(acc + c * H + h) : 0.0f;
+        sv[i][c] = h < H ? ld_rlx(accs + c * H + h) : 0.0f;
       }
 #pragma unroll
     for (int i = 0; i < HPT; ++i) {
@@ -682,12 +711,13 @@ __global__ __launch_bounds__(64 * NW) void decode16_kernel(
         float tot = 0.0f;
 #pragma unroll
         for (int c = 0; c < DEC_NCOPY; ++c) tot += sv[i][c];
-#pragma unroll
-        for (int c = 0; c < DEC_NCOPY; ++c) st_rlx(acc + c * H + h, 0.0f);
         out[h] = f32_to_bf16(tot);
       }
     }
-    if (tid == 0) st_rlx(&st->done, 0u);
+    if (tid == 0) {
+      st_rlx(&st->router_ticket, epoch + 1u);
+      st_rlx(&st->done, 0u);
+    }
   }
 }
 
@@ -696,10 +726,10 @@ __global__ void decode_ws_clear_kernel(uint32_t* p, size_t n_words) {
     p[i] = 0u;
 }
 
-// state | DEC_NCOPY x H fp32 accumulators | PP_MAX_EXPERTS 64-bit logit slots
+// state | 2 x DEC_NCOPY x H fp32 accumulators | PP_MAX_EXPERTS 64-bit logit slots
 extern "C" size_t pp_decode_workspace_bytes(int H, int E) {
   (void)E;
-  return dec_acc_offset() + (size_t)DEC_NCOPY * H * sizeof(float) + PP_MAX_EXPERTS * sizeof(unsigned long long);
+  return dec_acc_offset() + (size_t)2 * DEC_NCOPY * H * sizeof(float) + PP_MAX_EXPERTS * sizeof(unsigned long long);
 }
 
 extern "C" int pp_decode_workspace_init(void* workspace, int H, int E, void* stream) {

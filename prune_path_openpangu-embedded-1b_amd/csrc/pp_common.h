@@ -248,6 +248,10 @@ static __device__ void kv_introsort(float* K, int* V, int n, int* stk) {
 //   max; e = expf_u10(x - max); sum in vec::reduce_all order; p = e * (1/sum);
 //   descending sort (stable for E <= 16, introsort ties otherwise); fp64 running
 //   sum rounded to fp32 at each rank; keep ranks with cum < tau; keep rank 0.
+// Workgroup barrier for LDS traffic only: this wave's LDS operations are complete,
+// then s_barrier. Unlike __syncthreads() it does not wait for global loads in flight.
+__device__ __forceinline__ void wg_lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 __device__ __forceinline__ void wave_sync_lds() {
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -509,79 +513,73 @@ static __device__ void select_one_token(LG lg, int E, float tau, SelScratch* ss,
   wave_sync_lds();
 }
 
-// Selection of one token by a whole workgroup of nthreads threads, E > 16, with the
-// same result as select_one_token:
-// * softmax by wave 0 in torch's reduce order (16 lane columns summed chunk by chunk,
-//   the tail into the low lanes, then the halves tree);
-// * ranks counted by all threads on 64-bit keys (~bits(p) << 32 | index): for p >= 0
-//   and NaN their unsigned order is exactly "NaN first, then descending, equal values
-//   by index" (kv_before plus the index tie-break);
-// * the fp64 running-sum cut: when every selected-candidate p is 0 or >= 2^-29, every
-//   partial sum of the sorted p (< 2) is an exact multiple of 2^-52 and so exact in
-//   double, whatever the order of the additions -- wave 0 computes the prefix in
-//   parallel; otherwise lane 0 runs the sequential sum;
+// Selection of one token by a whole workgroup of nthreads >= E threads, E > 16, with
+// the same result as select_one_token. Thread t owns expert t:
+// * max (block reduction), e_t = expf_u10(x_t - max); e is zero-padded up to a
+//   multiple of 16, so the torch-order sum (16 lane columns added chunk by chunk, the
+//   tail into the low lanes, then the halves tree) needs no guards: adding +0.0 to a
+//   non-negative running sum changes nothing;
+// * p_t = e_t * (1/S) and its 64-bit rank key (~bits(p) << 32 | t) into LDS: for p >= 0
+//   and NaN the unsigned key order is exactly "NaN first, then descending, equal
+//   values by index" (kv_before plus the index tie-break); padding keys are all ones;
+// * rank_t = number of keys below key_t (guard-free loop over the padded keys);
+// * the fp64 running-sum cut by wave 0: when every sorted p is 0 or >= 2^-29, every
+//   partial sum (< 2) is an exact multiple of 2^-52 and so exact in double, whatever
+//   the order of the additions -- a parallel prefix; otherwise the sequential sum;
 // * a tie straddling the cut falls back to the introsort restatement (lane 0).
-// Every thread of the workgroup must call it.
+// keys: LDS scratch of PP_MAX_EXPERTS 64-bit words. Every thread must call it. Its
+// barriers order LDS traffic only (global loads of the caller may stay in flight).
 __device__ __forceinline__ unsigned long long sel_key(float p, int j) {
   const uint32_t b = (p != p) ? 0xffffffffu : __float_as_uint(p);
   return ((unsigned long long)(~b) << 32) | (uint32_t)j;
 }
 
 template <typename LG>
-static __device__ void select_one_token_wg(LG lg, int E, float tau, SelScratch* ss, int tid, int nthreads) {
-  const int lane = tid & 63;
-  if (tid < PP_WAVE) {
-    float m = -__builtin_huge_valf();
-    for (int j = lane; j < E; j += PP_WAVE) m = fmaxf(m, lg(j));
-    m = wave_max(m);
-    for (int j = lane; j < E; j += PP_WAVE) ss->e[j] = pp_expf_u10(__fsub_rn(lg(j), m));
-    wave_sync_lds();
-    float acc = 0.0f;
-    if (lane < 16) {
-      // column `lane` of the 16-wide chunks, all loads first, then added in chunk order
-      float col[PP_MAX_EXPERTS / 16];
+static __device__ void select_one_token_wg(LG lg, int E, float tau, SelScratch* ss, unsigned long long* keys,
+                                           float* red, int tid, int nthreads) {
+  const int lane = tid & 63, wv = tid >> 6, nw = nthreads >> 6;
+  const int E16 = (E + 15) & ~15;
+  const float x = tid < E ? lg(tid) : -__builtin_huge_valf();
+  float m = wave_max(x);
+  if (lane == 0) red[wv] = m;
+  wg_lds_barrier();
+  m = red[0];
+  for (int w = 1; w < nw; ++w) m = fmaxf(m, red[w]);
+  const float e = tid < E ? pp_expf_u10(__fsub_rn(x, m)) : 0.0f;
+  if (tid < E16) ss->e[tid] = e;
+  wg_lds_barrier();
+  if (tid < 16) {
+    float col[PP_MAX_EXPERTS / 16];
 #pragma unroll
-      for (int c = 0; c < PP_MAX_EXPERTS / 16; ++c) col[c] = (16 * c + lane < E) ? ss->e[16 * c + lane] : 0.0f;
-      acc = col[0];
+    for (int c = 0; c < PP_MAX_EXPERTS / 16; ++c) col[c] = 16 * c < E16 ? ss->e[16 * c + tid] : 0.0f;
+    float acc = col[0];
 #pragma unroll
-      for (int c = 1; c < PP_MAX_EXPERTS / 16; ++c)
-        if (16 * c + lane < E) acc = __fadd_rn(acc, col[c]);
-    }
+    for (int c = 1; c < PP_MAX_EXPERTS / 16; ++c)
+      if (16 * c < E16) acc = __fadd_rn(acc, col[c]);
 #pragma unroll
-    for (int o = 8; o >= 1; o >>= 1) acc = __fadd_rn(acc, __shfl_xor(acc, o, PP_WAVE));
-    const float r = __fdiv_rn(1.0f, __shfl(acc, 0, PP_WAVE));
-    float pv[PP_MAX_EXPERTS / PP_WAVE];
-#pragma unroll
-    for (int i = 0; i < PP_MAX_EXPERTS / PP_WAVE; ++i) {
-      const int j = lane + i * PP_WAVE;
-      pv[i] = j < E ? __fmul_rn(ss->e[j], r) : 0.0f;
-    }
-    wave_sync_lds();
-#pragma unroll
-    for (int i = 0; i < PP_MAX_EXPERTS / PP_WAVE; ++i) {
-      const int j = lane + i * PP_WAVE;
-      if (j < E) ss->e[j] = pv[i];
-    }
+    for (int o = 8; o >= 1; o >>= 1) acc = __fadd_rn(acc, __shfl_xor(acc, o, 16));
+    if (tid == 0) red[0] = __fdiv_rn(1.0f, acc);
   }
-  __syncthreads();
-  for (int j = tid; j < E; j += nthreads) {
-    const float pj = ss->e[j];
-    const unsigned long long kj = sel_key(pj, j);
+  wg_lds_barrier();
+  const float pt = __fmul_rn(e, red[0]);
+  if (tid < E) {
+    ss->e[tid] = pt;
+    keys[tid] = sel_key(pt, tid);
+  } else if (tid < E16) {
+    keys[tid] = ~0ull;
+  }
+  wg_lds_barrier();
+  if (tid < E) {
+    const unsigned long long kt = keys[tid];
     int rank = 0;
-    for (int q0 = 0; q0 < E; q0 += 16) {
-      float pq[16];
+    for (int q0 = 0; q0 < E16; q0 += 16) {
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const float4 v4 = *(const float4*)&ss->e[q0 + 4 * u];
-        pq[4 * u] = v4.x; pq[4 * u + 1] = v4.y; pq[4 * u + 2] = v4.z; pq[4 * u + 3] = v4.w;
-      }
-#pragma unroll
-      for (int u = 0; u < 16; ++u) rank += (q0 + u < E && sel_key(pq[u], q0 + u) < kj) ? 1 : 0;
+      for (int u = 0; u < 16; ++u) rank += keys[q0 + u] < kt ? 1 : 0;
     }
-    ss->srt[rank] = pj;
-    ss->order[rank] = j;
+    ss->srt[rank] = pt;
+    ss->order[rank] = tid;
   }
-  __syncthreads();
+  wg_lds_barrier();
   if (tid < PP_WAVE) {
     constexpr int QPL = PP_MAX_EXPERTS / PP_WAVE;  // sorted positions per lane
     float v[QPL];
@@ -594,11 +592,11 @@ static __device__ void select_one_token_wg(LG lg, int E, float tau, SelScratch* 
     }
     int k;
     if (__all(exact)) {
-      double s[QPL], run = 0.0;
+      double sv[QPL], run = 0.0;
 #pragma unroll
       for (int i = 0; i < QPL; ++i) {
         run += (double)v[i];
-        s[i] = run;
+        sv[i] = run;
       }
       double incl = run;
 #pragma unroll
@@ -610,7 +608,7 @@ static __device__ void select_one_token_wg(LG lg, int E, float tau, SelScratch* 
       const float tau32 = tau;
       int c = 0;
 #pragma unroll
-      for (int i = 0; i < QPL; ++i) c += (lane * QPL + i < E && (float)(excl + s[i]) < tau32) ? 1 : 0;
+      for (int i = 0; i < QPL; ++i) c += (lane * QPL + i < E && (float)(excl + sv[i]) < tau32) ? 1 : 0;
 #pragma unroll
       for (int o = 32; o >= 1; o >>= 1) c += __shfl_xor(c, o, PP_WAVE);
       k = c > 0 ? c : 1;
@@ -627,5 +625,5 @@ static __device__ void select_one_token_wg(LG lg, int E, float tau, SelScratch* 
       }
     }
   }
-  __syncthreads();
+  wg_lds_barrier();
 }

@@ -46,9 +46,14 @@ def test_decode_c1_vs_fixture(pkg, c1, ti):
     z, w, x, m = c1
     tau = float(z["taus"][ti])
     m.tau = tau
+    epoch = None
     for t in range(x.shape[0]):
         out, st = _decode_one(pkg, m, x[t])
-        assert st["error"] == 0 and st["ready"] == 0 and st["done"] == 0 and st["router_ticket"] == 0
+        assert st["error"] == 0 and st["ready"] == 0 and st["done"] == 0
+        # the call epoch (accumulator set parity) advances by one per call
+        if epoch is not None:
+            assert st["router_ticket"] == epoch + 1
+        epoch = st["router_ticket"]
         lg = st["logits"].numpy()
         np.testing.assert_allclose(lg, z["logits"][t], rtol=1e-5, atol=1e-5)
         sel = oracle.select(lg[None], tau)
