@@ -368,6 +368,10 @@ def main():
         byt = k2 * 3 * H * G2 * 2 + 192 * H * 4 + H * 6
         extra["e192_g32_decode"] = {"us_per_layer": us, "k_mean": k2, "hbm_gbs": byt / (us * 1e-6) / 1e9,
                                     "weight_sets": NS}
+        del l192
+        # config 5: 26-layer decoder-shaped stack, 1024-token prompt + 128 greedy steps
+        torch.cuda.empty_cache()
+        extra["decoder_stack"] = pkg.decoder_stack.run(prompt_len=1024, steps=128, layers=26, tau=args.tau)
 
     # ---------------- CPU baseline: oracle dense masked layer, one token per call
     cpu = None

@@ -12,6 +12,7 @@ from . import ops
 from .tau_sparse_moe import TauSparseMoE
 from .model import (IntegratedOpenPanguMoEMLP, MoELayer, experts_masks_from_ids, load_cluster_ids,
                     physical_reorder_for_inference)
+from . import decoder_stack
 
 __all__ = ["TauSparseMoE", "IntegratedOpenPanguMoEMLP", "MoELayer", "experts_masks_from_ids", "load_cluster_ids",
-           "physical_reorder_for_inference", "ops", "build", "_lib"]
+           "physical_reorder_for_inference", "decoder_stack", "ops", "build", "_lib"]

@@ -1,0 +1,197 @@
+"""Decoder-shaped stack around the MoE-MLP path.
+
+openPangu-Embedded-1B-shaped and randomly initialised: 26 x (RMSNorm, causal
+attention with 12 heads of 128 and a KV cache, RMSNorm, MoE-MLP), token embedding and
+LM head over a 153,376-word vocabulary, bf16. Prefill a prompt, then greedy decode;
+the MoE-MLP is ``IntegratedOpenPanguMoEMLP`` (eval path through the MI355X kernels,
+the module tree of src/openpangu_moe.py:43-130), mirroring the reference's manual
+decode benchmark (src/evaluation_triton.py:403-460). ``run`` reports the time per
+decode step, the prefill time and the MoE-MLP share of both, measured with events on
+the current stream around each MoE-MLP call.
+
+Attention is plain torch with contiguous right operands (no transposed views in
+batched bf16 products); it is harness, not part of the hot path.
+"""
+from __future__ import annotations
+
+import math
+import types
+from typing import Dict, List
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import ops
+from .model import IntegratedOpenPanguMoEMLP, physical_reorder_for_inference
+
+VOCAB = 153376
+
+
+class RMSNorm(nn.Module):
+    def __init__(self, d: int, eps: float = 1e-6):
+        super().__init__()
+        self.weight = nn.Parameter(torch.ones(d))
+        self.eps = eps
+
+    def forward(self, x):
+        xf = x.float()
+        return (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.eps) * self.weight.float()).to(x.dtype)
+
+
+def rope(x: torch.Tensor, pos: torch.Tensor, base: float = 10000.0) -> torch.Tensor:
+    """Rotary position embedding on [B, heads, L, hd] (half-split form)."""
+    hd = x.shape[-1]
+    inv = 1.0 / (base ** (torch.arange(0, hd, 2, device=x.device, dtype=torch.float32) / hd))
+    ang = pos.float()[:, None] * inv[None, :]                       # [L, hd/2]
+    cos, sin = ang.cos()[None, None], ang.sin()[None, None]
+    x1, x2 = x.float()[..., : hd // 2], x.float()[..., hd // 2:]
+    return torch.cat([x1 * cos - x2 * sin, x1 * sin + x2 * cos], -1).to(x.dtype)
+
+
+class Attention(nn.Module):
+    def __init__(self, d: int, heads: int, max_len: int):
+        super().__init__()
+        self.h, self.hd = heads, d // heads
+        self.qkv = nn.Linear(d, 3 * d, bias=False)
+        self.o = nn.Linear(d, d, bias=False)
+        self.max_len = max_len
+        self.k_cache = None
+        self.v_cache = None
+        self.len = 0
+
+    def reset(self, B: int, device, dtype):
+        self.k_cache = torch.zeros(B, self.h, self.max_len, self.hd, device=device, dtype=dtype)
+        self.v_cache = torch.zeros(B, self.h, self.max_len, self.hd, device=device, dtype=dtype)
+        self.len = 0
+
+    def forward(self, x):
+        B, L, D = x.shape
+        q, k, v = self.qkv(x).view(B, L, 3, self.h, self.hd).permute(2, 0, 3, 1, 4)  # [B, h, L, hd] each
+        pos = torch.arange(self.len, self.len + L, device=x.device)
+        q, k = rope(q, pos), rope(k, pos)
+        self.k_cache[:, :, self.len:self.len + L] = k
+        self.v_cache[:, :, self.len:self.len + L] = v
+        T = self.len + L
+        kt = self.k_cache[:, :, :T].transpose(-1, -2).contiguous()     # [B, h, hd, T]
+        s = torch.matmul(q.contiguous(), kt).float() / math.sqrt(self.hd)  # [B, h, L, T]
+        if L > 1:
+            causal = torch.ones(L, T, device=x.device, dtype=torch.bool).tril(T - L)
+            s = s.masked_fill(~causal, float("-inf"))
+        p = torch.softmax(s, -1).to(x.dtype)
+        o = torch.matmul(p, self.v_cache[:, :, :T].contiguous())        # [B, h, L, hd]
+        self.len = T
+        return self.o(o.transpose(1, 2).reshape(B, L, D))
+
+
+class Block(nn.Module):
+    def __init__(self, cfg, args, max_len: int):
+        super().__init__()
+        self.input_layernorm = RMSNorm(cfg.hidden_size)
+        self.self_attn = Attention(cfg.hidden_size, cfg.num_attention_heads, max_len)
+        self.post_attention_layernorm = RMSNorm(cfg.hidden_size)
+        self.mlp = IntegratedOpenPanguMoEMLP(cfg, args)
+        self.moe_events: List = []
+
+    def forward(self, x):
+        x = x + self.self_attn(self.input_layernorm(x))
+        h = self.post_attention_layernorm(x)
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        m = self.mlp(h)
+        e1.record()
+        self.moe_events.append((e0, e1))
+        return x + m
+
+
+class DecoderStack(nn.Module):
+    def __init__(self, layers: int = 26, hidden: int = 1536, heads: int = 12, experts: int = 16,
+                 group: int = 384, tau: float = 0.70, vocab: int = VOCAB, max_len: int = 1152):
+        super().__init__()
+        self.cfg = types.SimpleNamespace(hidden_size=hidden, intermediate_size=experts * group,
+                                         num_attention_heads=heads)
+        self.args = types.SimpleNamespace(group_size=group, tau=tau)
+        self.embed_tokens = nn.Embedding(vocab, hidden)
+        self.layers = nn.ModuleList([Block(self.cfg, self.args, max_len) for _ in range(layers)])
+        self.norm = RMSNorm(hidden)
+        self.lm_head = nn.Linear(hidden, vocab, bias=False)
+
+    @torch.no_grad()
+    def init_random(self, seed: int = 0, std: float = 0.02):
+        dev = self.embed_tokens.weight.device
+        g = torch.Generator(device=dev)
+        g.manual_seed(seed)
+        for p in self.parameters():
+            if p.dim() >= 2:
+                p.copy_(torch.randn(p.shape, generator=g, device=p.device, dtype=torch.float32) * std)
+        for blk in self.layers:
+            mlp = blk.mlp
+            E = mlp.moelayer.experts
+            ids = torch.randperm(mlp.moelayer.dimension, generator=g, device=dev) % E
+            mlp.moelayer.experts_masks.copy_(F.one_hot(ids, E).t().to(mlp.moelayer.experts_masks.dtype))
+
+    def prepare_inference(self, tau: float):
+        physical_reorder_for_inference(self.layers, tau)
+
+    def forward(self, ids):
+        x = self.embed_tokens(ids)
+        for blk in self.layers:
+            x = blk(x)
+        return self.lm_head(self.norm(x[:, -1:]))
+
+
+@torch.no_grad()
+def run(prompt_len: int = 1024, steps: int = 128, layers: int = 26, tau: float = 0.70, seed: int = 0,
+        device: str = "cuda:0") -> Dict[str, float]:
+    """Prefill ``prompt_len`` random token ids, then ``steps`` greedy decode steps at
+    batch 1. Returns per-step and prefill times and the MoE-MLP share."""
+    dev = torch.device(device)
+    model = DecoderStack(layers=layers, max_len=prompt_len + steps).to(dev)
+    model.init_random(seed)
+    model = model.to(torch.bfloat16).eval()
+    for blk in model.layers:  # the masked layer and projections feed the reorder; keep the router fp32
+        blk.mlp.moelayer.float()
+    model.prepare_inference(tau)
+    for blk in model.layers:
+        blk.self_attn.reset(1, dev, torch.bfloat16)
+    g = torch.Generator(device="cpu")
+    g.manual_seed(seed + 1)
+    ids = torch.randint(0, VOCAB, (1, prompt_len), generator=g).to(dev)
+
+    def moe_ms():
+        torch.cuda.synchronize()
+        t = sum(e0.elapsed_time(e1) for blk in model.layers for (e0, e1) in blk.moe_events)
+        for blk in model.layers:
+            blk.moe_events.clear()
+        return t
+
+    # warm-up on a short prompt (kernels, allocator), then reset the caches
+    model(ids[:, :16])
+    moe_ms()
+    for blk in model.layers:
+        blk.self_attn.reset(1, dev, torch.bfloat16)
+    s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s0.record()
+    logits = model(ids)
+    s1.record()
+    torch.cuda.synchronize()
+    prefill_ms = s0.elapsed_time(s1)
+    prefill_moe = moe_ms()
+    nxt = logits.argmax(-1)
+    s0.record()
+    for _ in range(steps):
+        logits = model(nxt)
+        nxt = logits.argmax(-1)
+    s1.record()
+    torch.cuda.synchronize()
+    decode_ms = s0.elapsed_time(s1)
+    decode_moe = moe_ms()
+    return {
+        "layers": layers, "prompt": prompt_len, "steps": steps, "tau": tau,
+        "prefill_ms": prefill_ms, "prefill_moe_ms": prefill_moe, "prefill_moe_share": prefill_moe / prefill_ms,
+        "decode_ms_per_step": decode_ms / steps, "decode_moe_ms_per_step": decode_moe / steps,
+        "decode_moe_share": decode_moe / decode_ms,
+        "decode_moe_us_per_layer": decode_moe / steps / layers * 1000.0,
+        "note": "random-init bf16 weights, random prompt ids; events around each MoE-MLP call on the stream",
+    }

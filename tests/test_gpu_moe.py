@@ -312,3 +312,11 @@ def test_model_wrapper_reference_checkpoint_roundtrip(pkg):
     a = m(to_gpu(x[None])).float().cpu()
     b = m2(to_gpu(x[None])).float().cpu()
     assert torch.equal(a, b)
+
+
+def test_decoder_stack_runs(pkg):
+    """Decoder-shaped stack (config 5 harness) at a small size: prefill + greedy decode
+    through the model-side drop-in; the MoE-MLP share is a fraction of the step."""
+    r = pkg.decoder_stack.run(prompt_len=40, steps=3, layers=2, tau=0.7)
+    assert r["prefill_ms"] > 0 and r["decode_ms_per_step"] > 0
+    assert 0.0 < r["decode_moe_share"] < 1.0 and 0.0 < r["prefill_moe_share"] < 1.0
