@@ -150,8 +150,7 @@ __device__ void local_logits(const XT* __restrict__ x, int H, const float* __res
     for (int i = 0; i < 2; ++i)
       a2[i] = __fadd_rn(b5 ? part[i + 2] : part[i], __shfl_xor(b5 ? part[i] : part[i + 2], 32, PP_WAVE));
     float t = __fadd_rn(b4 ? a2[1] : a2[0], __shfl_xor(b4 ? a2[0] : a2[1], 16, PP_WAVE));
-#pragma unroll
-    for (int o = 8; o >= 1; o >>= 1) t = __fadd_rn(t, __shfl_xor(t, o, PP_WAVE));
+    t = row16_sum(t);
     const int e = e0 + 4 * wv + 2 * b5 + b4;
     if ((lane & 15) == 0 && e < E) lg_s[e] = bias ? __fadd_rn(t, bias[e]) : t;
   }
@@ -345,8 +344,8 @@ __global__ __launch_bounds__(DEC_THREADS) void decode_kernel(
       gs += dot8(g2[c], xr[c]);
       us += dot8(u2[c], xr[c]);
     }
-    gs = wave_sum(gs);
-    us = wave_sum(us);
+    gs = wave_sum_dpp(gs);
+    us = wave_sum_dpp(us);
     const float a = pp_silu(gs) * us * gwt;
 #pragma unroll
     for (int c = 0; c < CPL; ++c) axpy8(a, d2[c], oacc[c]);
@@ -461,9 +460,8 @@ __global__ __launch_bounds__(64 * NW) void decode16_kernel(
   constexpr int NT = 64 * NW;
   extern __shared__ __align__(16) float red[];  // [NW-1][H]
   __shared__ __align__(16) float lg_s[16];
-  __shared__ __align__(16) float ev_s[16];
+  __shared__ __align__(16) float pg_s[32];
   __shared__ __align__(16) float srt_s[16];
-  __shared__ int ord_s[16];
   __shared__ int flag_s;
   __shared__ int k_s;
   __shared__ int sel_ids_s[16];
@@ -520,68 +518,64 @@ __global__ __launch_bounds__(64 * NW) void decode16_kernel(
       t = __fadd_rn(t, __shfl_xor(t, 16, PP_WAVE));
       e = EPW * wv + b5;
     }
-#pragma unroll
-    for (int o = 8; o >= 1; o >>= 1) t = __fadd_rn(t, __shfl_xor(t, o, PP_WAVE));
+    t = row16_sum(t);
     if ((lane & 15) == 0 && (EPW == 4 || b4 == 0)) lg_s[e] = bias ? __fadd_rn(t, bias[e]) : t;
   }
   __syncthreads();
 
-  // ---- selection (wave 0), branch-free for E = 16 (same arithmetic as select_small)
+  // ---- selection (wave 0), same arithmetic as select_small. Lane (g, j) = 16 g + j
+  // serves expert j; the critical path is short dependent chains, so the four 16-lane
+  // groups split the work instead of repeating it:
+  // * one exp / one division for both outputs: group 1 evaluates the gate
+  //   1 / (exp(0 - x_j) + 1) while group 0 evaluates p_j = exp(x_j - max) * (1 / S);
+  //   max and S are the xor butterfly i^8, i^4, i^2, i^1 (torch's reduce_all order);
+  // * group g compares key_j with the keys of experts 4g .. 4g+3 (64-bit rank keys:
+  //   NaN first, then descending p, equal p by index = torch's stable descending sort)
+  //   and sums the p of those ranked before j; two xor steps combine the groups;
+  // * when every p is 0 or >= 2^-29 each partial sum (< 2) is a multiple of 2^-52 and
+  //   exact in double, so {p_q : rank_q <= rank_j} summed in any order equals the fp64
+  //   running sum at rank_j; otherwise (or for NaN) the sequential running sum.
   if (wv == 0) {
-    const int j = lane & 15;
+    const int j = lane & 15, grp = lane >> 4;
     const float xl = lg_s[j];
-    float m = xl;
-#pragma unroll
-    for (int o = 8; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, PP_WAVE));
-    const float e = pp_expf_u10(__fsub_rn(xl, m));
-    if (lane < 16) ev_s[lane] = e;
+    const float m = row16_max(xl);
+    const float e = pp_expf_u10(grp == 1 ? __fsub_rn(0.0f, xl) : __fsub_rn(xl, m));
+    const float S = row16_sum(e);
+    const float r = __fdiv_rn(1.0f, grp == 1 ? __fadd_rn(e, 1.0f) : S);
+    if (lane < 32) pg_s[lane] = grp == 1 ? r : __fmul_rn(e, r);  // [p_0..15 | gate_0..15]
     wave_sync_lds();
-    float ev[16];
+    const float p = pg_s[j];
+    const float4 p4 = *(const float4*)&pg_s[4 * grp];
+    const float pq[4] = {p4.x, p4.y, p4.z, p4.w};
+    const unsigned long long kj = sel_key(p, j);
+    int rank = 0, exact = 1;
+    double cum = 0.0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float4 v = *(const float4*)&ev_s[4 * i];
-      ev[4 * i] = v.x; ev[4 * i + 1] = v.y; ev[4 * i + 2] = v.z; ev[4 * i + 3] = v.w;
+      const bool before = sel_key(pq[i], 4 * grp + i) < kj;
+      rank += before ? 1 : 0;
+      cum += before ? (double)pq[i] : 0.0;
+      exact &= (int)(pq[i] == 0.0f) | (int)(pq[i] >= 0x1p-29f);  // NaN fails both
     }
-    float a8[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) a8[i] = __fadd_rn(ev[i], ev[i + 8]);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) a8[i] = __fadd_rn(a8[i], a8[i + 4]);
-#pragma unroll
-    for (int i = 0; i < 2; ++i) a8[i] = __fadd_rn(a8[i], a8[i + 2]);
-    const float r = __fdiv_rn(1.0f, __fadd_rn(a8[0], a8[1]));
-    const float p = __fmul_rn(e, r);
-    int rank = 0;
-#pragma unroll
-    for (int q = 0; q < 16; ++q) {
-      const float pq = __fmul_rn(ev[q], r);
-      rank += (kv_before(pq, p) || (pq == p && q < j)) ? 1 : 0;
-    }
-    if (lane < 16) {
-      srt_s[rank] = p;
-      ord_s[rank] = lane;
-    }
-    wave_sync_lds();
-    float sv[16];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float4 v = *(const float4*)&srt_s[4 * i];
-      sv[4 * i] = v.x; sv[4 * i + 1] = v.y; sv[4 * i + 2] = v.z; sv[4 * i + 3] = v.w;
-    }
-    // cum is non-decreasing, so the ranks with cum < tau are a prefix: count them
+    rank += __shfl_xor(rank, 16, PP_WAVE);
+    cum += __shfl_xor(cum, 16, PP_WAVE);
+    rank += __shfl_xor(rank, 32, PP_WAVE);
+    cum += __shfl_xor(cum, 32, PP_WAVE);
     const float tau32 = tau;
-    double a = 0.0;
-    int k = 0;
-#pragma unroll
-    for (int q = 0; q < 16; ++q) {
-      a += (double)sv[q];
-      k += ((float)a < tau32) ? 1 : 0;
+    int k;
+    bool sel;
+    if (__all(exact)) {
+      sel = rank == 0 || (float)(cum + (double)p) < tau32;
+      k = __popcll(__ballot(sel) & 0xffffull);
+    } else {
+      if (lane < 16) srt_s[rank] = p;
+      wave_sync_lds();
+      k = tau_cut([&](int q) { return srt_s[q]; }, 16, tau);
+      sel = rank < k;
     }
-    k = k > 0 ? k : 1;
-    if (lane < k) {
-      const int eid = ord_s[lane];
-      sel_ids_s[lane] = eid;
-      sel_g_s[lane] = pp_sigmoid(lg_s[eid]);
+    if (lane < 16 && sel) {
+      sel_ids_s[rank] = j;
+      sel_g_s[rank] = pg_s[16 + j];
     }
     if (lane == 0) k_s = k;
   }
@@ -647,8 +641,8 @@ __global__ __launch_bounds__(64 * NW) void decode16_kernel(
       gs += dot8(g2[c], xr[c]);
       us += dot8(u2[c], xr[c]);
     }
-    gs = wave_sum(gs);
-    us = wave_sum(us);
+    gs = wave_sum_dpp(gs);
+    us = wave_sum_dpp(us);
     const float av = pp_silu(gs) * us * gwt;
 #pragma unroll
     for (int c = 0; c < CPL; ++c) axpy8(av, d2[c], oacc[c]);

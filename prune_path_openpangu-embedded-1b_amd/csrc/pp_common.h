@@ -79,6 +79,46 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// DPP lane moves inside 16-lane rows: a VALU operand modifier, no LDS round trip
+// (__shfl_xor is a ds_bpermute, about a hundred cycles each).
+#define PP_DPP_XOR1 0xB1   // quad_perm [1,0,3,2]: lane i^1
+#define PP_DPP_XOR2 0x4E   // quad_perm [2,3,0,1]: lane i^2
+#define PP_DPP_ROR4 0x124  // row_ror:4: lane (i+4) mod 16 of the row
+#define PP_DPP_ROR8 0x128  // row_ror:8: lane (i+8) mod 16 of the row = i^8
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+// Sum over each 16-lane row, pairing i^8, i^4, i^2, i^1: bit-identical to four
+// __shfl_xor butterfly steps, and every lane of the row ends with the same bits. After
+// the i^8 step the row is 8-periodic (IEEE addition commutes), so lane (i+4) mod 16
+// holds the value of lane i^4.
+__device__ __forceinline__ float row16_sum(float v) {
+  v = __fadd_rn(v, dpp_mov<PP_DPP_ROR8>(v));
+  v = __fadd_rn(v, dpp_mov<PP_DPP_ROR4>(v));
+  v = __fadd_rn(v, dpp_mov<PP_DPP_XOR2>(v));
+  return __fadd_rn(v, dpp_mov<PP_DPP_XOR1>(v));
+}
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp_mov<PP_DPP_ROR8>(v));
+  v = fmaxf(v, dpp_mov<PP_DPP_ROR4>(v));
+  v = fmaxf(v, dpp_mov<PP_DPP_XOR2>(v));
+  return fmaxf(v, dpp_mov<PP_DPP_XOR1>(v));
+}
+// Whole-wave sum in a fixed order (rows by DPP, then the four row totals read as
+// scalars); the result is wave-uniform. Not the xor-butterfly order of wave_sum.
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v += dpp_mov<PP_DPP_XOR1>(v);
+  v += dpp_mov<PP_DPP_XOR2>(v);
+  v += dpp_mov<PP_DPP_ROR4>(v);
+  v += dpp_mov<PP_DPP_ROR8>(v);
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return (r0 + r1) + (r2 + r3);
+}
+
 // ---------------------------------------------------------------- torch-CPU exp / sigmoid
 // SLEEF expf_u10, FMA form (Shibata & Petrogalli, "SLEEF", IEEE TPDS 2020; the
 // routine torch's AVX512 Vectorized<float>::exp() calls). Every step is one IEEE
