@@ -36,7 +36,9 @@
 
 #define DEC_THREADS 256
 #define DEC_NCOPY 8
+#ifndef DEC16_NW
 #define DEC16_NW 8  // waves per workgroup in the E = 16 kernel
+#endif
 #define DEC_SPIN_LIMIT (1u << 22)
 #define DEC_LOCAL_ROUTER_FLOATS 32768  // Epad*H at or below this: every workgroup routes
 
@@ -86,6 +88,15 @@ __device__ __forceinline__ float dot8(const uint4 w, const float* x) {
     s = __builtin_fmaf(x[2 * i + 1], __uint_as_float(u[i] & 0xffff0000u), s);
   }
   return s;
+}
+// 8 bf16 weights . 8 bf16 x values (both packed in pairs), fp32 accumulation with the
+// bf16 dot-product instruction (products of bf16 values are exact in fp32)
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ float dot8_bf16(const uint4 w, const uint4 xb, float s) {
+  s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w.x), __builtin_bit_cast(bf16x2_t, xb.x), s, false);
+  s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w.y), __builtin_bit_cast(bf16x2_t, xb.y), s, false);
+  s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w.z), __builtin_bit_cast(bf16x2_t, xb.z), s, false);
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w.w), __builtin_bit_cast(bf16x2_t, xb.w), s, false);
 }
 __device__ __forceinline__ void axpy8(float a, const uint4 w, float* acc) {
   const uint32_t u[4] = {w.x, w.y, w.z, w.w};
@@ -450,6 +461,36 @@ __device__ __forceinline__ void load_x8<bf16_t>(const bf16_t* x, int ch, float* 
   }
 }
 
+// x chunk ch (4 values) as fp32
+template <typename XT>
+__device__ __forceinline__ float4 load_x4(const XT* x, int ch);
+template <>
+__device__ __forceinline__ float4 load_x4<float>(const float* x, int ch) {
+  return *(const float4*)(x + ch * 4);
+}
+template <>
+__device__ __forceinline__ float4 load_x4<bf16_t>(const bf16_t* x, int ch) {
+  const uint2 u = *(const uint2*)(x + ch * 4);
+  return make_float4(__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u), __uint_as_float(u.y << 16),
+                     __uint_as_float(u.y & 0xffff0000u));
+}
+
+// x chunk ch (8 values) as packed bf16 pairs, rounded to nearest even
+template <typename XT>
+__device__ __forceinline__ uint4 load_x8_bf16(const XT* x, int ch);
+template <>
+__device__ __forceinline__ uint4 load_x8_bf16<float>(const float* x, int ch) {
+  const float4 a = *(const float4*)(x + ch * 8), b = *(const float4*)(x + ch * 8 + 4);
+  const bf16x2_t p0 = {(__bf16)a.x, (__bf16)a.y}, p1 = {(__bf16)a.z, (__bf16)a.w};
+  const bf16x2_t p2 = {(__bf16)b.x, (__bf16)b.y}, p3 = {(__bf16)b.z, (__bf16)b.w};
+  return make_uint4(__builtin_bit_cast(uint32_t, p0), __builtin_bit_cast(uint32_t, p1),
+                    __builtin_bit_cast(uint32_t, p2), __builtin_bit_cast(uint32_t, p3));
+}
+template <>
+__device__ __forceinline__ uint4 load_x8_bf16<bf16_t>(const bf16_t* x, int ch) {
+  return *(const uint4*)(x + ch * 8);
+}
+
 template <typename XT, int CPL, int NW>
 __global__ __launch_bounds__(64 * NW) void decode16_kernel(
     const XT* __restrict__ x, const float* __restrict__ router, const float* __restrict__ bias, int G, float tau,
@@ -459,6 +500,7 @@ __global__ __launch_bounds__(64 * NW) void decode16_kernel(
   constexpr int HC = H / 8;
   constexpr int NT = 64 * NW;
   extern __shared__ __align__(16) float red[];  // [NW-1][H]
+  __shared__ __align__(16) float part_s[16 * NW];
   __shared__ __align__(16) float lg_s[16];
   __shared__ __align__(16) float pg_s[32];
   __shared__ __align__(16) float srt_s[16];
@@ -470,56 +512,46 @@ __global__ __launch_bounds__(64 * NW) void decode16_kernel(
   const int W = gridDim.x, b = blockIdx.x;
   const uint32_t epoch = ld_rlx(&st->router_ticket);  // accumulator set parity
 
-  // ---- logits: wave wv -> experts EPW*wv ..; lane -> x chunks lane + 64 c (8 values each)
-  constexpr int EPW = 16 / NW;  // experts per wave (4 or 2)
-  float xf[CPL][8];
+  // x for the stream as packed bf16 (round to nearest even), loaded now so the loads
+  // overlap the routing
+  uint4 xb[CPL];
 #pragma unroll
-  for (int c = 0; c < CPL; ++c) load_x8<XT>(x, lane + 64 * c, xf[c], false);
+  for (int c = 0; c < CPL; ++c) xb[c] = load_x8_bf16<XT>(x, lane + 64 * c);
+  const float bj = (bias != nullptr && wv == 0) ? bias[lane & 15] : 0.0f;
+
+  // ---- logits. Wave wv takes the slice [512 CPL wv / NW, 512 CPL (wv + 1) / NW) of
+  // x, CPL float4 chunks per lane: lanes form rows of LR = 128 / NW lanes, row rw takes
+  // experts rw, rw + NR, ... (NR = 64 / LR rows) and lane cl of the row the chunks
+  // cl + LR i. Loads per workgroup: the router once and x once. Rows add by DPP; wave 0
+  // adds the NW wave partials in wave order. Every workgroup uses the same order, so
+  // every workgroup gets the same logits.
+  static_assert(NW == 8 || NW == 16, "decode16_kernel: 8 or 16 waves");
+  constexpr int LR = 128 / NW, NR = 64 / LR, EPL = 16 / NR;
   {
-    float4 wr[EPW][2 * CPL];
+    const int rw = lane / LR, cl = lane % LR;
+    const int ch0 = (16 * CPL * 8 / NW) * wv + cl;  // float4 chunk index into x / a router row
+    float4 xv[CPL];
+    float4 wr[EPL][CPL];
 #pragma unroll
-    for (int j = 0; j < EPW; ++j)
+    for (int i = 0; i < CPL; ++i) xv[i] = load_x4<XT>(x, ch0 + LR * i);
 #pragma unroll
-      for (int c = 0; c < CPL; ++c) {
-        const float4* rp = (const float4*)(router + (EPW * wv + j) * H + (lane + 64 * c) * 8);
-        wr[j][2 * c] = rp[0];
-        wr[j][2 * c + 1] = rp[1];
-      }
-    float part[EPW];
+    for (int jj = 0; jj < EPL; ++jj)
 #pragma unroll
-    for (int j = 0; j < EPW; ++j) {
+      for (int i = 0; i < CPL; ++i)
+        wr[jj][i] = *(const float4*)(router + (rw + NR * jj) * H + 4 * (ch0 + LR * i));
+#pragma unroll
+    for (int jj = 0; jj < EPL; ++jj) {
       float sacc = 0.0f;
 #pragma unroll
-      for (int c = 0; c < CPL; ++c) {
-        sacc = __builtin_fmaf(xf[c][0], wr[j][2 * c].x, sacc);
-        sacc = __builtin_fmaf(xf[c][1], wr[j][2 * c].y, sacc);
-        sacc = __builtin_fmaf(xf[c][2], wr[j][2 * c].z, sacc);
-        sacc = __builtin_fmaf(xf[c][3], wr[j][2 * c].w, sacc);
-        sacc = __builtin_fmaf(xf[c][4], wr[j][2 * c + 1].x, sacc);
-        sacc = __builtin_fmaf(xf[c][5], wr[j][2 * c + 1].y, sacc);
-        sacc = __builtin_fmaf(xf[c][6], wr[j][2 * c + 1].z, sacc);
-        sacc = __builtin_fmaf(xf[c][7], wr[j][2 * c + 1].w, sacc);
+      for (int i = 0; i < CPL; ++i) {
+        sacc = __builtin_fmaf(xv[i].x, wr[jj][i].x, sacc);
+        sacc = __builtin_fmaf(xv[i].y, wr[jj][i].y, sacc);
+        sacc = __builtin_fmaf(xv[i].z, wr[jj][i].z, sacc);
+        sacc = __builtin_fmaf(xv[i].w, wr[jj][i].w, sacc);
       }
-      part[j] = sacc;
+      sacc = LR == 16 ? row16_sum(sacc) : row8_sum(sacc);
+      if (cl == 0) part_s[(rw + NR * jj) * NW + wv] = sacc;
     }
-    // butterfly over the wave: EPW values -> lane holds the total of value sel(lane)
-    const int b5 = (lane >> 5) & 1, b4 = (lane >> 4) & 1;
-    float t;
-    int e;
-    if (EPW == 4) {
-      float a2[2];
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-        a2[i] = __fadd_rn(b5 ? part[(i + 2) % EPW] : part[i % EPW], __shfl_xor(b5 ? part[i % EPW] : part[(i + 2) % EPW], 32, PP_WAVE));
-      t = __fadd_rn(b4 ? a2[1] : a2[0], __shfl_xor(b4 ? a2[0] : a2[1], 16, PP_WAVE));
-      e = EPW * wv + 2 * b5 + b4;
-    } else {
-      t = __fadd_rn(b5 ? part[1 % EPW] : part[0], __shfl_xor(b5 ? part[0] : part[1 % EPW], 32, PP_WAVE));
-      t = __fadd_rn(t, __shfl_xor(t, 16, PP_WAVE));
-      e = EPW * wv + b5;
-    }
-    t = row16_sum(t);
-    if ((lane & 15) == 0 && (EPW == 4 || b4 == 0)) lg_s[e] = bias ? __fadd_rn(t, bias[e]) : t;
   }
   __syncthreads();
 
@@ -537,7 +569,25 @@ __global__ __launch_bounds__(64 * NW) void decode16_kernel(
   //   running sum at rank_j; otherwise (or for NaN) the sequential running sum.
   if (wv == 0) {
     const int j = lane & 15, grp = lane >> 4;
-    const float xl = lg_s[j];
+    float xl;
+    {
+      float4 pv[NW / 4];
+#pragma unroll
+      for (int i = 0; i < NW / 4; ++i) pv[i] = *(const float4*)&part_s[j * NW + 4 * i];
+      xl = pv[0].x;
+      xl = __fadd_rn(xl, pv[0].y);
+      xl = __fadd_rn(xl, pv[0].z);
+      xl = __fadd_rn(xl, pv[0].w);
+#pragma unroll
+      for (int i = 1; i < NW / 4; ++i) {
+        xl = __fadd_rn(xl, pv[i].x);
+        xl = __fadd_rn(xl, pv[i].y);
+        xl = __fadd_rn(xl, pv[i].z);
+        xl = __fadd_rn(xl, pv[i].w);
+      }
+      if (bias != nullptr) xl = __fadd_rn(xl, bj);
+      if (lane < 16) lg_s[j] = xl;  // telemetry
+    }
     const float m = row16_max(xl);
     const float e = pp_expf_u10(grp == 1 ? __fsub_rn(0.0f, xl) : __fsub_rn(xl, m));
     const float S = row16_sum(e);
@@ -599,9 +649,6 @@ __global__ __launch_bounds__(64 * NW) void decode16_kernel(
   const int n = v1 - v0;
   int r = v0 + (n * wv) / NW;
   const int r_end = v0 + (n * (wv + 1)) / NW;
-  float xr[CPL][8];
-#pragma unroll
-  for (int c = 0; c < CPL; ++c) load_x8<XT>(x, lane + 64 * c, xr[c], true);
   float oacc[CPL][8];
 #pragma unroll
   for (int c = 0; c < CPL; ++c)
@@ -638,8 +685,8 @@ __global__ __launch_bounds__(64 * NW) void decode16_kernel(
     float gs = 0.0f, us = 0.0f;
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
-      gs += dot8(g2[c], xr[c]);
-      us += dot8(u2[c], xr[c]);
+      gs = dot8_bf16(g2[c], xb[c], gs);
+      us = dot8_bf16(u2[c], xb[c], us);
     }
     gs = wave_sum_dpp(gs);
     us = wave_sum_dpp(us);

@@ -99,6 +99,14 @@ __device__ __forceinline__ float row16_sum(float v) {
   v = __fadd_rn(v, dpp_mov<PP_DPP_XOR2>(v));
   return __fadd_rn(v, dpp_mov<PP_DPP_XOR1>(v));
 }
+// Sum over each 8-lane half row (quad steps, then the mirrored quad); a fixed order,
+// the same in every lane group, not the xor butterfly.
+#define PP_DPP_HALF_MIRROR 0x141  // row_half_mirror: lane 7 - i of the half row
+__device__ __forceinline__ float row8_sum(float v) {
+  v = __fadd_rn(v, dpp_mov<PP_DPP_XOR1>(v));
+  v = __fadd_rn(v, dpp_mov<PP_DPP_XOR2>(v));
+  return __fadd_rn(v, dpp_mov<PP_DPP_HALF_MIRROR>(v));
+}
 __device__ __forceinline__ float row16_max(float v) {
   v = fmaxf(v, dpp_mov<PP_DPP_ROR8>(v));
   v = fmaxf(v, dpp_mov<PP_DPP_ROR4>(v));
