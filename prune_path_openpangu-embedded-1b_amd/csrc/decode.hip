@@ -9,13 +9,13 @@
 // atomics.
 //
 // Routing. When the fp32 router is small (E <= 16 and 16*H*4 <= 128 KB, e.g. E=16 at
-// H=1536) every workgroup computes all logits (fixed reduction order, so every workgroup gets
-// the same bits) and runs the selection itself: no cross-workgroup wait at all.
-// Otherwise workgroups 0..R-1 compute the logits, the last of them (ticket) runs the
-// selection and publishes it, and every workgroup waits for the `ready` flag with a
-// bounded spin. Workgroups are dispatched in index order, so the producers are resident
-// before any waiter can take their slot; the bound only turns an impossible wait into
-// an error flag instead of a hang.
+// H=1536) every workgroup computes all logits (fixed reduction order, so every workgroup
+// gets the same bits) and runs the selection itself: no cross-workgroup wait at all.
+// Otherwise workgroup e < E computes logit e and publishes it in a 64-bit slot tagged
+// with the call epoch; every workgroup gathers the E slots (bounded spin on the tag) and
+// runs the selection on its own copy. Workgroups are dispatched in index order, so the
+// producers are resident before any waiter can take their slot; the bound only turns an
+// impossible wait into an error flag instead of a hang.
 //
 // Work split. The layer's weight bytes are k * G neuron records of 6*H bytes each
 // ({gate row, up row, down column}, see pack.hip). All workgroups share the k*G
@@ -23,9 +23,10 @@
 // record's loads are in flight while the current one is reduced), reduces the gate/up
 // dot products across the wave, applies silu(g)*u*gate in registers and accumulates
 // act * down into 8*CPL fp32 registers per lane. The workgroup's partial output goes to
-// one of DEC_NCOPY fp32 accumulators with float atomics; the last workgroup to finish
-// (ticket) folds the copies with atomic exchanges (which also clear them), writes the
-// bf16 output and resets the counters, so the next call needs no memset.
+// one of a few fp32 accumulator copies with float atomics; the last workgroup to finish
+// (ticket) folds the copies, writes the bf16 output, advances the call epoch and resets
+// the counters. Two accumulator sets alternate between calls, and each call clears the
+// set of the previous call early, off its critical path, so no call needs a memset.
 //
 // Cross-workgroup data (logits, selection, counters, accumulators) is only accessed
 // with agent-scope atomics, and ordering between them comes from waiting for
@@ -35,7 +36,8 @@
 #include "pp_common.h"
 
 #define DEC_THREADS 256
-#define DEC_NCOPY 8
+#define DEC_NCOPY 8   // accumulator copies per set (general kernel; the allocation)
+#define DEC16_NCOPY 4 // copies the E = 16 kernel uses (128 workgroups: 32 per address)
 #ifndef DEC16_NW
 #define DEC16_NW 8  // waves per workgroup in the E = 16 kernel
 #endif
@@ -70,11 +72,12 @@ __device__ __forceinline__ unsigned long long* dec_slots(float* acc, int H) {
   return (unsigned long long*)(acc + (size_t)2 * DEC_NCOPY * H);
 }
 // this workgroup's share of clearing the other set (the previous call's)
+// (the first ncopy copies of it: the ones the kernel uses)
 __device__ __forceinline__ void dec_clear_previous(float* acc, int H, uint32_t epoch, int b, int W, int tid,
-                                                   int nthreads) {
+                                                   int nthreads, int ncopy = DEC_NCOPY) {
   float* prev = dec_acc_set(acc, H, epoch + 1u);
   int lo, hi;
-  pp_split((uint32_t)(DEC_NCOPY * H), (uint32_t)W, (uint32_t)b, lo, hi);
+  pp_split((uint32_t)(ncopy * H), (uint32_t)W, (uint32_t)b, lo, hi);
   for (int i = lo + tid; i < hi; i += nthreads) st_rlx(prev + i, 0.0f);
 }
 
@@ -640,7 +643,7 @@ __global__ __launch_bounds__(64 * NW) void decode16_kernel(
     if (tid == 0) st_rlx(&st->k, k);
   }
 
-  dec_clear_previous(acc, H, epoch, b, W, tid, NT);
+  dec_clear_previous(acc, H, epoch, b, W, tid, NT, DEC16_NCOPY);
 
   // ---- stream the selected neuron records (as decode_kernel)
   const int T = k * G;
@@ -695,7 +698,7 @@ __global__ __launch_bounds__(64 * NW) void decode16_kernel(
     for (int c = 0; c < CPL; ++c) axpy8(av, d2[c], oacc[c]);
   }
 
-  // ---- workgroup reduction -> one of DEC_NCOPY fp32 accumulators
+  // ---- workgroup reduction -> one of DEC16_NCOPY fp32 accumulators
   // waves 1..NW-1 park partials in LDS, wave 0 adds its own into slot 0, then every
   // thread folds the slots in order for contiguous h and adds to the copy
   if (n > 0) {
@@ -717,7 +720,7 @@ __global__ __launch_bounds__(64 * NW) void decode16_kernel(
       }
     }
     __syncthreads();
-    float* accc = dec_acc_set(acc, H, epoch) + (b % DEC_NCOPY) * H;
+    float* accc = dec_acc_set(acc, H, epoch) + (b % DEC16_NCOPY) * H;
 #pragma unroll
     for (int i = 0; i < (H + NT - 1) / NT; ++i) {
       const int h = tid + NT * i;
@@ -737,11 +740,11 @@ __global__ __launch_bounds__(64 * NW) void decode16_kernel(
     // every load of the fold is issued before the first add (one round trip)
     constexpr int HPT = (H + NT - 1) / NT;
     const float* accs = dec_acc_set(acc, H, epoch);
-    float sv[HPT][DEC_NCOPY];
+    float sv[HPT][DEC16_NCOPY];
 #pragma unroll
     for (int i = 0; i < HPT; ++i)
 #pragma unroll
-      for (int c = 0; c < DEC_NCOPY; ++c) {
+      for (int c = 0; c < DEC16_NCOPY; ++c) {
         const int h = tid + NT * i;
         sv[i][c] = h < H ? ld_rlx(accs + c * H + h) : 0.0f;
       }
@@ -751,7 +754,7 @@ __global__ __launch_bounds__(64 * NW) void decode16_kernel(
       if (h < H) {
         float tot = 0.0f;
 #pragma unroll
-        for (int c = 0; c < DEC_NCOPY; ++c) tot += sv[i][c];
+        for (int c = 0; c < DEC16_NCOPY; ++c) tot += sv[i][c];
         out[h] = f32_to_bf16(tot);
       }
     }
