@@ -38,6 +38,7 @@
 #define DEC_THREADS 256
 #define DEC_NCOPY 8   // accumulator copies per set (general kernel; the allocation)
 #define DEC16_NCOPY 4 // copies the E = 16 kernel uses (128 workgroups: 32 per address)
+#define DEC16_SPEC(CPL) ((CPL) <= 4)  // speculative top-expert loads (register budget)
 #ifndef DEC16_NW
 #define DEC16_NW 8  // waves per workgroup in the E = 16 kernel
 #endif
@@ -511,6 +512,9 @@ __global__ __launch_bounds__(64 * NW) void decode16_kernel(
   __shared__ int k_s;
   __shared__ int sel_ids_s[16];
   __shared__ float sel_g_s[16];
+  __shared__ int main_ids_s[16];
+  __shared__ float main_g_s[16];
+  __shared__ int kmain_s, spec_s;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int W = gridDim.x, b = blockIdx.x;
   const uint32_t epoch = ld_rlx(&st->router_ticket);  // accumulator set parity
@@ -520,7 +524,7 @@ __global__ __launch_bounds__(64 * NW) void decode16_kernel(
   uint4 xb[CPL];
 #pragma unroll
   for (int c = 0; c < CPL; ++c) xb[c] = load_x8_bf16<XT>(x, lane + 64 * c);
-  const float bj = (bias != nullptr && wv == 0) ? bias[lane & 15] : 0.0f;
+  const float bias_j = bias != nullptr ? bias[lane & 15] : 0.0f;
 
   // ---- logits. Wave wv takes the slice [512 CPL wv / NW, 512 CPL (wv + 1) / NW) of
   // x, CPL float4 chunks per lane: lanes form rows of LR = 128 / NW lanes, row rw takes
@@ -558,6 +562,42 @@ __global__ __launch_bounds__(64 * NW) void decode16_kernel(
   }
   __syncthreads();
 
+  // ---- logit of expert j = lane & 15 in every wave: the NW wave partials in wave order
+  const int j = lane & 15;
+  float xl;
+  {
+    float4 pv[NW / 4];
+#pragma unroll
+    for (int i = 0; i < NW / 4; ++i) pv[i] = *(const float4*)&part_s[j * NW + 4 * i];
+    xl = pv[0].x;
+    xl = __fadd_rn(xl, pv[0].y);
+    xl = __fadd_rn(xl, pv[0].z);
+    xl = __fadd_rn(xl, pv[0].w);
+#pragma unroll
+    for (int i = 1; i < NW / 4; ++i) {
+      xl = __fadd_rn(xl, pv[i].x);
+      xl = __fadd_rn(xl, pv[i].y);
+      xl = __fadd_rn(xl, pv[i].z);
+      xl = __fadd_rn(xl, pv[i].w);
+    }
+    if (bias != nullptr) xl = __fadd_rn(xl, bias_j);
+  }
+  const float m = row16_max(xl);
+
+  // ---- speculative top expert. Rank 0 is always selected and is the expert with the
+  // largest logit unless probabilities tie (then the lowest index among equal p), so
+  // while wave 0 runs the selection, waves 1..7 start loading this workgroup's share of
+  // the records of e1 = the lowest index with the largest logit (at most one record per
+  // wave: G <= 7 W). After the selection barrier they are used if e1 was selected (then
+  // the main stream skips e1) and dropped otherwise; either way every selected record is
+  // used exactly once. No speculation for non-finite or NaN logits.
+  // (wave 0 evaluates e1 after its rank step, off its critical path)
+  auto top_expert = [&]() -> int {
+    const bool finite = __all(xl == xl) && __fsub_rn(m, m) == 0.0f;
+    if (!(DEC16_SPEC(CPL) && finite && G <= 7 * W)) return -1;
+    return __builtin_amdgcn_readfirstlane(row16_min_i(xl == m ? j : 16));
+  };
+  int e1 = -1;
   // ---- selection (wave 0), same arithmetic as select_small. Lane (g, j) = 16 g + j
   // serves expert j; the critical path is short dependent chains, so the four 16-lane
   // groups split the work instead of repeating it:
@@ -571,27 +611,8 @@ __global__ __launch_bounds__(64 * NW) void decode16_kernel(
   //   exact in double, so {p_q : rank_q <= rank_j} summed in any order equals the fp64
   //   running sum at rank_j; otherwise (or for NaN) the sequential running sum.
   if (wv == 0) {
-    const int j = lane & 15, grp = lane >> 4;
-    float xl;
-    {
-      float4 pv[NW / 4];
-#pragma unroll
-      for (int i = 0; i < NW / 4; ++i) pv[i] = *(const float4*)&part_s[j * NW + 4 * i];
-      xl = pv[0].x;
-      xl = __fadd_rn(xl, pv[0].y);
-      xl = __fadd_rn(xl, pv[0].z);
-      xl = __fadd_rn(xl, pv[0].w);
-#pragma unroll
-      for (int i = 1; i < NW / 4; ++i) {
-        xl = __fadd_rn(xl, pv[i].x);
-        xl = __fadd_rn(xl, pv[i].y);
-        xl = __fadd_rn(xl, pv[i].z);
-        xl = __fadd_rn(xl, pv[i].w);
-      }
-      if (bias != nullptr) xl = __fadd_rn(xl, bj);
-      if (lane < 16) lg_s[j] = xl;  // telemetry
-    }
-    const float m = row16_max(xl);
+    const int grp = lane >> 4;
+    if (lane < 16) lg_s[j] = xl;  // telemetry
     const float e = pp_expf_u10(grp == 1 ? __fsub_rn(0.0f, xl) : __fsub_rn(xl, m));
     const float S = row16_sum(e);
     const float r = __fdiv_rn(1.0f, grp == 1 ? __fadd_rn(e, 1.0f) : S);
@@ -626,13 +647,44 @@ __global__ __launch_bounds__(64 * NW) void decode16_kernel(
       k = tau_cut([&](int q) { return srt_s[q]; }, 16, tau);
       sel = rank < k;
     }
+    // full selection in rank order (telemetry), and the main stream's list: the same
+    // without e1 when e1 was selected (its records come from the speculative loads)
+    e1 = top_expert();
+    const bool e1_sel = e1 >= 0 && ((__ballot(sel) >> e1) & 1ull);
+    const int rank_e1 = e1 >= 0 ? __builtin_amdgcn_readlane(rank, e1) : 0;
     if (lane < 16 && sel) {
       sel_ids_s[rank] = j;
       sel_g_s[rank] = pg_s[16 + j];
+      if (!(e1_sel && j == e1)) {
+        const int mi = rank - ((e1_sel && rank > rank_e1) ? 1 : 0);
+        main_ids_s[mi] = j;
+        main_g_s[mi] = pg_s[16 + j];
+      }
     }
-    if (lane == 0) k_s = k;
+    if (lane == 0) {
+      k_s = k;
+      kmain_s = k - (e1_sel ? 1 : 0);
+      spec_s = e1_sel ? 1 : 0;
+    }
   }
-  __syncthreads();
+  int s0 = 0, s1 = 0;
+  if (wv != 0) {
+    e1 = top_expert();
+    if (e1 >= 0) pp_split((uint32_t)G, (uint32_t)W, (uint32_t)b, s0, s1);
+  }
+  const bool have_spec = wv >= 1 && e1 >= 0 && s0 + wv - 1 < s1;
+  uint4 sg[CPL], su[CPL], sd[CPL];
+  if (have_spec) {
+    const uint4* rec = (const uint4*)(rows + ((int64_t)e1 * G + s0 + wv - 1) * 3 * H);
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+      sg[c] = rec[lane + 64 * c];
+      su[c] = rec[HC + lane + 64 * c];
+      sd[c] = rec[2 * HC + lane + 64 * c];
+    }
+  }
+
+  wg_lds_barrier();  // LDS only: the speculative loads stay in flight
   const int k = k_s;
   if (b == 0) {  // telemetry for the caller
     if (tid < 16) st_rlx(&st->logits[tid], lg_s[tid]);
@@ -646,7 +698,8 @@ __global__ __launch_bounds__(64 * NW) void decode16_kernel(
   dec_clear_previous(acc, H, epoch, b, W, tid, NT, DEC16_NCOPY);
 
   // ---- stream the selected neuron records (as decode_kernel)
-  const int T = k * G;
+  const bool spec_used = spec_s != 0;
+  const int T = kmain_s * G;
   int v0, v1;
   pp_split((uint32_t)T, (uint32_t)W, (uint32_t)b, v0, v1);
   const int n = v1 - v0;
@@ -657,34 +710,8 @@ __global__ __launch_bounds__(64 * NW) void decode16_kernel(
   for (int c = 0; c < CPL; ++c)
 #pragma unroll
     for (int i = 0; i < 8; ++i) oacc[c][i] = 0.0f;
-  uint4 gq[CPL], uq[CPL], dq[CPL];
-  int s_cur = 0, g_cur = 0;
-  if (r < r_end) {
-    s_cur = (int)((uint32_t)r / (uint32_t)G);
-    g_cur = r - s_cur * G;
-    const uint4* rec = (const uint4*)(rows + ((int64_t)sel_ids_s[s_cur] * G + g_cur) * 3 * H);
-#pragma unroll
-    for (int c = 0; c < CPL; ++c) {
-      gq[c] = rec[lane + 64 * c];
-      uq[c] = rec[HC + lane + 64 * c];
-      dq[c] = rec[2 * HC + lane + 64 * c];
-    }
-  }
-  for (; r < r_end; ++r) {
-    uint4 g2[CPL], u2[CPL], d2[CPL];
-#pragma unroll
-    for (int c = 0; c < CPL; ++c) { g2[c] = gq[c]; u2[c] = uq[c]; d2[c] = dq[c]; }
-    const float gwt = sel_g_s[s_cur];
-    if (r + 1 < r_end) {
-      if (++g_cur == G) { g_cur = 0; ++s_cur; }
-      const uint4* rec = (const uint4*)(rows + ((int64_t)sel_ids_s[s_cur] * G + g_cur) * 3 * H);
-#pragma unroll
-      for (int c = 0; c < CPL; ++c) {
-        gq[c] = rec[lane + 64 * c];
-        uq[c] = rec[HC + lane + 64 * c];
-        dq[c] = rec[2 * HC + lane + 64 * c];
-      }
-    }
+  // one record: gate/up dots over the wave, silu(g) * u * gate, acc += act * down
+  auto process = [&](const uint4(&g2)[CPL], const uint4(&u2)[CPL], const uint4(&d2)[CPL], float gwt) {
     float gs = 0.0f, us = 0.0f;
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
@@ -696,12 +723,46 @@ __global__ __launch_bounds__(64 * NW) void decode16_kernel(
     const float av = pp_silu(gs) * us * gwt;
 #pragma unroll
     for (int c = 0; c < CPL; ++c) axpy8(av, d2[c], oacc[c]);
+  };
+  uint4 gq[CPL], uq[CPL], dq[CPL];
+  int s_cur = 0, g_cur = 0;
+  if (r < r_end) {
+    s_cur = (int)((uint32_t)r / (uint32_t)G);
+    g_cur = r - s_cur * G;
+    const uint4* rec = (const uint4*)(rows + ((int64_t)main_ids_s[s_cur] * G + g_cur) * 3 * H);
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+      gq[c] = rec[lane + 64 * c];
+      uq[c] = rec[HC + lane + 64 * c];
+      dq[c] = rec[2 * HC + lane + 64 * c];
+    }
+  }
+  // the speculative record (loaded before the selection) with e1's gate
+  if (have_spec && spec_used) process(sg, su, sd, pg_s[16 + e1]);
+  for (; r < r_end; ++r) {
+    uint4 g2[CPL], u2[CPL], d2[CPL];
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) { g2[c] = gq[c]; u2[c] = uq[c]; d2[c] = dq[c]; }
+    const float gwt = main_g_s[s_cur];
+    if (r + 1 < r_end) {
+      if (++g_cur == G) { g_cur = 0; ++s_cur; }
+      const uint4* rec = (const uint4*)(rows + ((int64_t)main_ids_s[s_cur] * G + g_cur) * 3 * H);
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) {
+        gq[c] = rec[lane + 64 * c];
+        uq[c] = rec[HC + lane + 64 * c];
+        dq[c] = rec[2 * HC + lane + 64 * c];
+      }
+    }
+    process(g2, u2, d2, gwt);
   }
 
   // ---- workgroup reduction -> one of DEC16_NCOPY fp32 accumulators
   // waves 1..NW-1 park partials in LDS, wave 0 adds its own into slot 0, then every
   // thread folds the slots in order for contiguous h and adds to the copy
-  if (n > 0) {
+  // (uniform over the workgroup: whether it has records of e1, from the same split)
+  const bool spec_wg = spec_used && ((uint32_t)G / (uint32_t)W > 0u || (uint32_t)b < (uint32_t)G % (uint32_t)W);
+  if (n > 0 || spec_wg) {
     if (wv > 0) {
 #pragma unroll
       for (int c = 0; c < CPL; ++c) {

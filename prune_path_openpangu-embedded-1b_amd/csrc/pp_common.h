@@ -113,6 +113,13 @@ __device__ __forceinline__ float row16_max(float v) {
   v = fmaxf(v, dpp_mov<PP_DPP_XOR2>(v));
   return fmaxf(v, dpp_mov<PP_DPP_XOR1>(v));
 }
+// Minimum over each 16-lane row (every lane of the row ends with it).
+__device__ __forceinline__ int row16_min_i(int v) {
+  v = min(v, __float_as_int(dpp_mov<PP_DPP_ROR8>(__int_as_float(v))));
+  v = min(v, __float_as_int(dpp_mov<PP_DPP_ROR4>(__int_as_float(v))));
+  v = min(v, __float_as_int(dpp_mov<PP_DPP_XOR2>(__int_as_float(v))));
+  return min(v, __float_as_int(dpp_mov<PP_DPP_XOR1>(__int_as_float(v))));
+}
 // Whole-wave sum in a fixed order (rows by DPP, then the four row totals read as
 // scalars); the result is wave-uniform. Not the xor-butterfly order of wave_sum.
 __device__ __forceinline__ float wave_sum_dpp(float v) {

@@ -320,3 +320,42 @@ def test_decoder_stack_runs(pkg):
     r = pkg.decoder_stack.run(prompt_len=40, steps=3, layers=2, tau=0.7)
     assert r["prefill_ms"] > 0 and r["decode_ms_per_step"] > 0
     assert 0.0 < r["decode_moe_share"] < 1.0 and 0.0 < r["prefill_moe_share"] < 1.0
+
+
+@pytest.mark.parametrize("tau,want", [(0.2, [1]), (0.7, [1, 3, 0, 2, 4, 5, 6])])
+def test_decode_top_expert_speculation(pkg, tau, want):
+    """E = 16 decode loads the records of the largest-logit expert before the selection
+    is known. With an identity router the logits are x[:16]: experts 1 and 3 get logits
+    one ulp apart at 1e-4 (the other 14 at -2), so exp(x - max) is exactly 1 for both,
+    their probabilities tie and rank 0 is expert 1 (lower index) although expert 3 has
+    the larger logit. tau=0.2 selects only expert 1 (the speculative loads of expert 3
+    must be dropped); tau=0.7 selects expert 3 at rank 1 (from the speculative loads) and
+    the rest from the main stream. Output vs the fp64 sparse reference on the oracle's
+    selection."""
+    E, H, G = 16, 1536, 384
+    w = np.zeros((E, H), np.float32)
+    w[np.arange(E), np.arange(E)] = 1.0
+    rp = pkg.ops.pack_router(to_gpu(w), layout="linear")
+    rng = np.random.default_rng(7)
+    I = E * G
+    wts = {"w_gate": rng.normal(0, 0.02, (I, H)).astype(np.float32),
+           "w_up": rng.normal(0, 0.02, (I, H)).astype(np.float32),
+           "w_down": rng.normal(0, 0.02, (H, I)).astype(np.float32),
+           "w_router": w, "expert_ids": np.repeat(np.arange(E), G).astype(np.int32)}
+    packed = pkg.ops.pack_experts(to_gpu(wts["w_gate"]), to_gpu(wts["w_up"]), to_gpu(wts["w_down"]), E, G,
+                                  layout="linear")
+    ws = pkg.ops.decode_workspace(H, E, torch.device("cuda:0"))
+    x = rng.normal(0, 1, H).astype(np.float32)
+    x[:E] = -2.0
+    x[3] = np.float32(1e-4)
+    x[1] = np.nextafter(x[3], np.float32(-np.inf))
+    for _ in range(2):  # both accumulator sets
+        out = pkg.ops.moe_decode(to_gpu(x), rp, None, E, G, tau, packed, ws)
+        st = pkg.ops.decode_state(ws, E)
+        assert st["error"] == 0
+        k = int(st["k"])
+        assert st["sel_ids"].numpy()[:k].tolist() == want
+        sel = oracle.select(st["logits"].numpy()[None], tau)
+        assert sel.ranked[0, :sel.count[0]].tolist() == want
+        sp = sparse_expected(x[None], wts, sel.gates)[0]
+        assert_close(out.float().cpu().numpy().reshape(-1), sp, what=f"speculation tau={tau}")
