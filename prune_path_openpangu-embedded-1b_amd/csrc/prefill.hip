@@ -481,6 +481,10 @@ __global__ __launch_bounds__(GM_THREADS, 2) void down_v2_kernel(
 }
 
 // ------------------------------------------------------------------ combine
+// Per (token, 8 columns): the token's pair ids are read first (one batch of independent
+// loads), then up to CB_BATCH y rows at once, summed in expert order: two memory round
+// trips per batch instead of two per pair.
+#define CB_BATCH 8
 __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ y,
                                                       const int32_t* __restrict__ token_pairs,
                                                       const int32_t* __restrict__ count, int64_t N, int H,
@@ -492,13 +496,30 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
     const int ch = (int)(i % HC);
     float4 s0 = make_float4(0.f, 0.f, 0.f, 0.f), s1 = s0;
     const int k = min(count[t], E);
-    for (int q = 0; q < k; ++q) {
-      const int p = token_pairs[t * E + q];
-      if (p < 0) break;  // fewer pairs than count: inconsistent caller data, never read out of range
-      const float4* src = (const float4*)(y + (int64_t)p * H + ch * 8);
-      const float4 a = src[0], b = src[1];
-      s0.x += a.x; s0.y += a.y; s0.z += a.z; s0.w += a.w;
-      s1.x += b.x; s1.y += b.y; s1.z += b.z; s1.w += b.w;
+    const int32_t* tp = token_pairs + t * E;
+    bool stop = false;
+    for (int q0 = 0; q0 < k && !stop; q0 += CB_BATCH) {
+      int p[CB_BATCH];
+#pragma unroll
+      for (int i2 = 0; i2 < CB_BATCH; ++i2) p[i2] = q0 + i2 < k ? tp[q0 + i2] : -1;
+      float4 a[CB_BATCH], b[CB_BATCH];
+#pragma unroll
+      for (int i2 = 0; i2 < CB_BATCH; ++i2) {
+        // a negative id (fewer pairs than count: inconsistent caller data) ends the sum;
+        // nothing is read out of range
+        if (p[i2] >= 0) {
+          const float4* src = (const float4*)(y + (int64_t)p[i2] * H + ch * 8);
+          a[i2] = src[0];
+          b[i2] = src[1];
+        }
+      }
+#pragma unroll
+      for (int i2 = 0; i2 < CB_BATCH; ++i2) {
+        if (q0 + i2 >= k) break;
+        if (p[i2] < 0) { stop = true; break; }
+        s0.x += a[i2].x; s0.y += a[i2].y; s0.z += a[i2].z; s0.w += a[i2].w;
+        s1.x += b[i2].x; s1.y += b[i2].y; s1.z += b[i2].z; s1.w += b[i2].w;
+      }
     }
     uint4 o;
     o.x = (uint32_t)f32_to_bf16(s0.x) | ((uint32_t)f32_to_bf16(s0.y) << 16);
