@@ -13,8 +13,9 @@
 //   combine_kernel out[t] = sum of y over the pairs of token t in expert order, fp32 ->
 //                  bf16 (deterministic, no atomics).
 // Both GEMMs are persistent over a device-side tile map (no host sync, no padding FLOPs
-// beyond the last partial tile of each expert), 256 threads = 4 waves, BK = 64, LDS
-// tiles double-buffered with a 16-byte row pad (conflict-free 16-byte fragment reads).
+// beyond the last partial tile of each expert), 256 threads = 4 waves, BK = 64:
+// gemm_v3_kernel for G % 64 == 0 (LDS-DMA pipeline, below), gateup_kernel /
+// down_kernel (register-staged, row-padded LDS tiles) otherwise.
 #include "pp_common.h"
 
 #define GM_THREADS 256
@@ -248,34 +249,48 @@ __global__ __launch_bounds__(GM_THREADS, 2) void down_kernel(
 }
 
 // ------------------------------------------------------------------ pipelined grouped GEMM
-// Tile 128 rows x 128 B-rows x BK=64 on v_mfma_f32_32x32x16_bf16, 4 waves as 2 x 2
+// Tile 128 rows x 128 B-rows x BK 64 on v_mfma_f32_32x32x16_bf16, 4 waves as 2 x 2
 // (wave tile 64 x 64), two workgroups per CU, persistent over (row tile, column tile)
 // items. Operands go straight from global memory into LDS (global_load_lds_dwordx4:
 // lane i of a wave writes bytes [16 i, 16 i + 16) of the wave's 1 KB block, no VGPR
-// staging), two 32 KB LDS stages: the DMA of K block kb+1 runs under the MFMAs of kb.
+// staging) through GP_STAGES LDS stages; the DMA runs GP_STAGES - 1 K blocks ahead and
+// does not stop at item boundaries -- the blocks of a workgroup's items form one
+// stream, so the next item's first blocks are in flight under the current item's last
+// MFMAs. Per-item data never stalls the stream: tile metadata comes through scalar
+// loads, and the gathered token ids and pair gates of item i+1 are DMA'd into an LDS
+// slot together with item i's first block, so building item i+1's row offsets is an
+// LDS read.
 //
-// A tile row holds 64 bf16 = 8 chunks of 16 bytes; chunk c of row r is stored at
-// position c ^ ((r >> 1) & 7). A fragment read (ds_read_b128) covers 32 consecutive
-// rows; any 16 of them then land in 16 distinct 16-byte slots of a 256-byte bank
-// window, and any 8 in 8 distinct slots of a 128-byte window.
+// A tile row holds BK bf16 = BK/8 chunks of 16 bytes; chunk c of row r is stored at
+// position c ^ gp_swz(r). A fragment read (ds_read_b128) covers 32 consecutive rows; any
+// 16 of them then land in 16 distinct 16-byte slots of a 256-byte bank window.
 //
 // Synchronisation is explicit: the compiler cannot tell that an LDS read does not
 // alias a DMA still in flight and would drain every prefetch before each read, and
 // __syncthreads() adds a release fence that does the same. So fragment reads are
 // inline ds_read_b128 whose results are fenced by s_waitcnt lgkmcnt tied to the
 // fragment registers, and the per-K-block barrier waits only for this wave's DMA of
-// the block about to be read.
-#define GV_STAGES 2
-#define GV_TILE_BYTES (128 * 64 * 2)               // one operand tile of one stage
-#define GV_STAGE_BYTES (2 * GV_TILE_BYTES)         // A + B
+// the block about to be read: every wave issues at least GP_DMA DMA instructions per
+// block (past the last block it re-fetches that block into the free stage, never
+// read), so "at most GP_DMA * (GP_STAGES - 2) of this wave's vector memory ops
+// outstanding" means its DMA of the block about to be read has landed (loads complete
+// in order; extra ops -- slot DMA, epilogue stores -- only make the wait stricter); the
+// barrier after it covers every wave and frees the stage written next.
+//
+// Measured alternatives (2048-token prefill, gate/up | down): the previous
+// two-stage kernel without the cross-item stream 54 | 34 us; one workgroup per CU with
+// four stages 81 | 50 (one wave per SIMD leaves the LDS and MFMA latencies exposed);
+// BK 32 with four stages 59 | 37 (twice the barriers); stream-K over (item, K block)
+// units with fp32 partials handed over through agent-scope stores 63 | 43 (the work is
+// balanced, but the per-block rate drops with all 512 workgroups streaming at once: the
+// GEMMs are bound by aggregate operand delivery, not by the second round); this
+// kernel 49 | 32.
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ void gl2lds(const void* src, unsigned char* lds_base) {
   __builtin_amdgcn_global_load_lds(src, (lds_void_t*)lds_base, 16, 0, 0);
 }
-
-__device__ __forceinline__ int gv_swz(int r) { return (r >> 1) & 7; }
 
 template <int IMM>
 __device__ __forceinline__ u32x4 gv_read(uint32_t lds_addr) {
@@ -311,72 +326,159 @@ struct GvItems {
   }
 };
 
-// One item = (tile t, column block nt). A rows: a_row(i) = element offset of the tile's
-// row i (i < 128, already clamped to a valid row); B rows: b_row(j) likewise (j < 128).
-// Accumulates the 128 x 128 product over K (multiple of 64) into acc[2][2] of each wave.
-template <typename AROW, typename BROW>
-__device__ __forceinline__ void gv_mainloop(unsigned char* smem, AROW a_row, BROW b_row, int K,
-                                            f32x16_t (&acc)[2][2]) {
+#define GP_BK 64         // K block (bf16 elements)
+#define GP_STAGES 2
+#define GP_WG_PER_CU 2
+#define GP_ROWB (GP_BK * 2)                     // bytes of one tile row in a stage
+#define GP_CH (GP_BK / 8)                       // 16-byte chunks per row
+#define GP_TILE (128 * GP_ROWB)                 // one operand tile of one stage
+#define GP_STAGE (2 * GP_TILE)
+#define GP_RPI (1024 / GP_ROWB)                 // rows per DMA instruction (a wave's 1 KB)
+#define GP_NI (128 / (4 * GP_RPI))              // DMA instructions per tile per wave
+#define GP_DMA (2 * GP_NI)                      // per wave per K block (A + B)
+#define GP_KS (GP_BK / 16)                      // MFMA k-steps per K block
+#define GP_SLOT_BYTES 1024                      // per item: 128 token ids + 128 pair gates
+#define GP_NSLOT 4
+#define GP_LDS_BYTES (GP_STAGES * GP_STAGE + GP_NSLOT * GP_SLOT_BYTES)
+// chunk c of row r is stored at position c ^ gp_swz(r): any 16 consecutive rows of a
+// fragment read land in 16 distinct 16-byte slots of a 256-byte bank window
+__device__ __forceinline__ int gp_swz(int r) { return GP_BK == 64 ? (r >> 1) & 7 : (r >> 2) & 3; }
+
+__device__ __forceinline__ void gl2lds4(const void* src, unsigned char* lds_base) {
+  __builtin_amdgcn_global_load_lds(src, (lds_void_t*)lds_base, 4, 0, 0);
+}
+
+template <int N>
+__device__ __forceinline__ void gp_wait_barrier() {
+  asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+// MODE 0: gate/up + SwiGLU (A = gathered x rows, B = gate/up rows of 64 neurons);
+// MODE 1: down (A = act rows, B = down_t rows of 128 hidden columns).
+template <int MODE>
+__global__ __launch_bounds__(GM_THREADS, GP_WG_PER_CU) void gemm_v3_kernel(
+    const bf16_t* __restrict__ abase, int H, int G, const bf16_t* __restrict__ bbase,
+    const int32_t* __restrict__ token_ids, const float* __restrict__ pair_gates,
+    const int32_t* __restrict__ tiles, const int32_t* __restrict__ meta, bf16_t* __restrict__ act,
+    float* __restrict__ y) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  unsigned char* slots = smem + GP_STAGES * GP_STAGE;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int wm = w >> 1, wn = w & 1;
-  // DMA assignment: instruction i covers rows 32 i + 8 w + lane/8, chunk position lane%8
-  int64_t aoff[4], boff[4];
+  const int n_ntile = MODE == 0 ? G / 64 : H / 128;
+  const int K = MODE == 0 ? H : G;
+  const int nkb = K / GP_BK;
+  const int n_items = meta[0] * n_ntile;
+  // this workgroup's items: it.first, it.first + it.step, ...; unit f = (local item
+  // f / nkb, K block f % nkb)
+  const GvItems it(n_items);
+  const int n_local_items = it.first < it.last ? (it.last - it.first + it.step - 1) / it.step : 0;
+  const int item0 = it.first, istep = it.step;
+  const int F = n_local_items * nkb;
+  if (F <= 0) return;
+  auto locate = [&](int f, int& li, int& kb) {
+    li = f / nkb;
+    kb = f - li * nkb;
+  };
+
+  // slot DMA of item li (wave 0): token ids and gates of the tile rows, row r >= rows
+  // reading row rows - 1 (in range; padding rows are never stored)
+  auto slot_dma = [&](int li) {
+    if (MODE != 0 || w != 0) return;
+    const int item = item0 + li * istep;
+    const int t = item / n_ntile;
+    const int p0 = tiles[t * 4 + 1], rows = tiles[t * 4 + 2];
+    unsigned char* sl = slots + (li & (GP_NSLOT - 1)) * GP_SLOT_BYTES;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = 32 * i + 8 * w + (lane >> 3);
-    const int pchunk = ((lane & 7) ^ gv_swz(r)) * 8;  // logical chunk stored at this lane's position
-    aoff[i] = a_row(r) + pchunk;
-    boff[i] = b_row(r) + pchunk;
-  }
-  // fragment read addresses per k-step: row (lane & 31) of the wave's 32-row blocks
-  const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void_t*)smem;
-  uint32_t offA[4], offB[4];
-#pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
-    const int r = lane & 31, c = ks * 2 + (lane >> 5);
-    const uint32_t o = (uint32_t)(r * 8 + (c ^ gv_swz(r))) * 16;
-    offA[ks] = lds0 + wm * 64 * 128 + o;
-    offB[ks] = lds0 + GV_TILE_BYTES + wn * 64 * 128 + o;
-  }
-  const int nkb = K / 64;
-  auto issue = [&](int kb, int st) {
-    unsigned char* sb = smem + st * GV_STAGE_BYTES;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int blk = (32 * i + 8 * w) * 128;  // wave's 1 KB block
-      gl2lds(a_row.base + aoff[i] + kb * 64, sb + blk);
-      gl2lds(b_row.base + boff[i] + kb * 64, sb + GV_TILE_BYTES + blk);
+    for (int h = 0; h < 2; ++h) {
+      const int r = min(64 * h + lane, rows - 1);
+      gl2lds4(token_ids + p0 + r, sl + 256 * h);
+      gl2lds4(pair_gates + p0 + r, sl + 512 + 256 * h);
     }
   };
+
+  // issue cursor: row offsets of the item whose blocks are being issued
+  int64_t aoff[GP_NI], boff[GP_NI];
+  auto setup_item = [&](int li) {
+    const int item = item0 + li * istep;
+    const int t = item / n_ntile, nt = item - t * n_ntile;
+    const int e = tiles[t * 4 + 0], p0 = tiles[t * 4 + 1], rows = tiles[t * 4 + 2];
+    const int32_t* tok = (const int32_t*)(slots + (li & (GP_NSLOT - 1)) * GP_SLOT_BYTES);
+#pragma unroll
+    for (int i = 0; i < GP_NI; ++i) {
+      const int r = (4 * i + w) * GP_RPI + lane / GP_CH;
+      const int pchunk = ((lane % GP_CH) ^ gp_swz(r)) * 8;
+      if (MODE == 0) {
+        aoff[i] = (int64_t)tok[r] * H + pchunk;
+        // B tile row r = wn_*64 + j*32 + q -> gate (j=0) / up (j=1) row of neuron nt*64 + wn_*32 + q
+        const int wn_ = r >> 6, j = (r >> 5) & 1, q = r & 31;
+        boff[i] = ((int64_t)(e * G + nt * 64 + wn_ * 32 + q) * 3 + j) * H + pchunk;
+      } else {
+        aoff[i] = (int64_t)(p0 + min(r, rows - 1)) * G + pchunk;
+        boff[i] = ((int64_t)e * H + nt * 128 + r) * G + pchunk;
+      }
+    }
+  };
+  auto issue = [&](int f) {
+    int li, kb;
+    locate(f < F ? f : F - 1, li, kb);  // past the end: the last block again, never read
+    if (f < F && kb == 0) {
+      setup_item(li);
+      // item li+1's slot is read nkb blocks later; items 0 and 1 get theirs in the
+      // prologue (the first item's blocks may all be in flight before its first wait)
+      if (li >= 1 && li + 1 < n_local_items) slot_dma(li + 1);
+    }
+    unsigned char* sb = smem + (f % GP_STAGES) * GP_STAGE;
+#pragma unroll
+    for (int i = 0; i < GP_NI; ++i) {
+      const int blk = (4 * i + w) * 1024;
+      gl2lds(abase + aoff[i] + kb * GP_BK, sb + blk);
+      gl2lds(bbase + boff[i] + kb * GP_BK, sb + GP_TILE + blk);
+    }
+  };
+
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void_t*)smem;
+  uint32_t offA[GP_KS], offB[GP_KS];
+#pragma unroll
+  for (int ks = 0; ks < GP_KS; ++ks) {
+    const int r = lane & 31, c = ks * 2 + (lane >> 5);
+    const uint32_t o = (uint32_t)(r * GP_CH + (c ^ gp_swz(r))) * 16;
+    offA[ks] = lds0 + wm * 64 * GP_ROWB + o;
+    offB[ks] = lds0 + GP_TILE + wn * 64 * GP_ROWB + o;
+  }
+
+  // prologue: the first two items' slots, then the first GP_STAGES - 1 blocks
+  slot_dma(0);
+  if (n_local_items > 1) slot_dma(1);
+  asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+#pragma unroll
+  for (int f = 0; f < GP_STAGES - 1; ++f) issue(f);
+
+  f32x16_t acc[2][2];
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int q = 0; q < 16; ++q) acc[i][j][q] = 0.0f;
-  issue(0, 0);
-  int st = 0;
-  for (int kb = 0; kb < nkb; ++kb) {
-    // this wave's DMA of block kb has landed, every wave's after the barrier; all
-    // waves are also done reading the other stage (block kb-1)
-    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    const uint32_t sbase = st * GV_STAGE_BYTES;
+
+  for (int f = 0; f < F; ++f) {
+    gp_wait_barrier<GP_DMA * (GP_STAGES - 2)>();
+    issue(f + GP_STAGES - 1);
+    const uint32_t sbase = (f % GP_STAGES) * GP_STAGE;
     u32x4 fa[2][2], fb[2][2];
     fa[0][0] = gv_read<0>(offA[0] + sbase);
-    fa[0][1] = gv_read<4096>(offA[0] + sbase);
+    fa[0][1] = gv_read<32 * GP_ROWB>(offA[0] + sbase);
     fb[0][0] = gv_read<0>(offB[0] + sbase);
-    fb[0][1] = gv_read<4096>(offB[0] + sbase);
-    // unconditional: past the end the last block is fetched again into the stage
-    // everyone finished before the barrier, and never read
-    issue(kb + 1 < nkb ? kb + 1 : nkb - 1, st ^ 1);
+    fb[0][1] = gv_read<32 * GP_ROWB>(offB[0] + sbase);
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
+    for (int ks = 0; ks < GP_KS; ++ks) {
       const int cur = ks & 1, nxt = cur ^ 1;
-      if (ks < 3) {
+      if (ks < GP_KS - 1) {
         fa[nxt][0] = gv_read<0>(offA[ks + 1] + sbase);
-        fa[nxt][1] = gv_read<4096>(offA[ks + 1] + sbase);
+        fa[nxt][1] = gv_read<32 * GP_ROWB>(offA[ks + 1] + sbase);
         fb[nxt][0] = gv_read<0>(offB[ks + 1] + sbase);
-        fb[nxt][1] = gv_read<4096>(offB[ks + 1] + sbase);
+        fb[nxt][1] = gv_read<32 * GP_ROWB>(offB[ks + 1] + sbase);
         gv_wait<4>(fa[cur][0], fa[cur][1], fb[cur][0], fb[cur][1]);
       } else {
         gv_wait<0>(fa[cur][0], fa[cur][1], fb[cur][0], fb[cur][1]);
@@ -386,98 +488,51 @@ __device__ __forceinline__ void gv_mainloop(unsigned char* smem, AROW a_row, BRO
 #pragma unroll
         for (int j = 0; j < 2; ++j) acc[i][j] = mfma32v(fa[cur][i], fb[cur][j], acc[i][j]);
     }
-    st ^= 1;
-  }
-  // the next item reuses both stages: drain the redundant tail DMA first
-  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
-
-struct GvRows {  // row source: base pointer + per-row element offset function
-  const bf16_t* base;
-};
-
-// gate/up with SwiGLU epilogue. B rows 0..63 = gate rows of neurons nb0..nb0+63,
-// rows 64..127 = up rows of the same neurons; wave (wm, wn) takes rows wm*64.. and
-// gate/up columns wn*32.. of each half, so lane-wise accG and accU line up.
-__global__ __launch_bounds__(GM_THREADS, 2) void gateup_v2_kernel(
-    const bf16_t* __restrict__ xb, int H, int G, const bf16_t* __restrict__ wrows,
-    const int32_t* __restrict__ token_ids, const float* __restrict__ pair_gates,
-    const int32_t* __restrict__ tiles, const int32_t* __restrict__ meta, bf16_t* __restrict__ act) {
-  extern __shared__ __align__(16) unsigned char smem[];
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int wm = w >> 1, wn = w & 1;
-  const int n_ntile = G / 64;
-  const GvItems it(meta[0] * n_ntile);
-  for (int item = it.first; item < it.last; item += it.step) {
-    const int t = item / n_ntile, nt = item % n_ntile;
-    const int e = tiles[t * 4 + 0], p0 = tiles[t * 4 + 1], rows = tiles[t * 4 + 2];
-    const int nb0 = nt * 64;
-    struct ARow { const bf16_t* base; const int32_t* tok; int p0, rows, H;
-      __device__ int64_t operator()(int r) const { return (int64_t)tok[p0 + (r < rows ? r : 0)] * H; } };
-    struct BRow { const bf16_t* base; int e, G, nb0, H;
-      __device__ int64_t operator()(int r) const {
-        const int part = r < 64 ? 0 : 1;
-        return ((int64_t)(e * G + nb0 + (r & 63)) * 3 + part) * H; } };
-    ARow ar{xb, token_ids, p0, rows, H};
-    BRow br{wrows, e, G, nb0, H};
-    f32x16_t acc[2][2];
-    // wave columns: gate block j=0 -> B rows wn*32.., up block j=1 -> B rows 64 + wn*32..
-    // gv_mainloop takes B rows wn*64 + j*32; remap so that j=0 is gate and j=1 is up
-    struct BRowPerm { const bf16_t* base; BRow inner;
-      __device__ int64_t operator()(int r) const {
-        // tile row r = wn*64 + j*32 + q  ->  gate/up row (j*64) + wn*32 + q
-        const int wn_ = r >> 6, j = (r >> 5) & 1, q = r & 31;
-        return inner(j * 64 + wn_ * 32 + q); } };
-    BRowPerm bp{wrows, br};
-    gv_mainloop(smem, ar, bp, H, acc);
-    const int neuron = nb0 + wn * 32 + (lane & 31);
+    int li, kb;
+    locate(f, li, kb);
+    if (kb != nkb - 1) continue;
+    const int item = item0 + li * istep;
+    // ---- epilogue of item li (lane laundered: its row indices are not worth registers
+    // across the main loop)
+    {
+      int ln = lane;
+      asm volatile("" : "+v"(ln));
+      const int t = item / n_ntile, nt = item - t * n_ntile;
+      const int p0 = tiles[t * 4 + 1], rows = tiles[t * 4 + 2];
+      if (MODE == 0) {
+        const float* gts = (const float*)(slots + (li & (GP_NSLOT - 1)) * GP_SLOT_BYTES + 512);
+        const int neuron = nt * 64 + wn * 32 + (ln & 31);
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < 2; ++i)
 #pragma unroll
-      for (int q = 0; q < 16; ++q) {
-        const int r = wm * 64 + i * 32 + mfma32_row(q, lane);
-        if (r < rows) {
-          const int p = p0 + r;
-          act[(int64_t)p * G + neuron] = f32_to_bf16(pp_silu(acc[i][0][q]) * acc[i][1][q] * pair_gates[p]);
-        }
+          for (int q = 0; q < 16; ++q) {
+            const int r = wm * 64 + i * 32 + mfma32_row(q, ln);
+            if (r < rows)
+              act[(int64_t)(p0 + r) * G + neuron] = f32_to_bf16(pp_silu(acc[i][0][q]) * acc[i][1][q] * gts[r]);
+          }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            const int h = nt * 128 + wn * 64 + j * 32 + (ln & 31);
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+              const int r = wm * 64 + i * 32 + mfma32_row(q, ln);
+              if (r < rows) y[(int64_t)(p0 + r) * H + h] = acc[i][j][q];
+            }
+          }
       }
     }
-  }
-}
-
-// down projection: A = act rows (pairs), B = down_t rows (hidden columns), K = G
-__global__ __launch_bounds__(GM_THREADS, 2) void down_v2_kernel(
-    const bf16_t* __restrict__ act, int H, int G, const bf16_t* __restrict__ down_t,
-    const int32_t* __restrict__ tiles, const int32_t* __restrict__ meta, float* __restrict__ y) {
-  extern __shared__ __align__(16) unsigned char smem[];
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int wm = w >> 1, wn = w & 1;
-  const int n_ntile = H / 128;
-  const GvItems it(meta[0] * n_ntile);
-  for (int item = it.first; item < it.last; item += it.step) {
-    const int t = item / n_ntile, nt = item % n_ntile;
-    const int e = tiles[t * 4 + 0], p0 = tiles[t * 4 + 1], rows = tiles[t * 4 + 2];
-    const int h0 = nt * 128;
-    struct ARow { const bf16_t* base; int p0, rows, G;
-      __device__ int64_t operator()(int r) const { return (int64_t)(p0 + (r < rows ? r : 0)) * G; } };
-    struct BRow { const bf16_t* base; int e, H, h0, G;
-      __device__ int64_t operator()(int r) const { return ((int64_t)e * H + h0 + r) * G; } };
-    ARow ar{act, p0, rows, G};
-    BRow br{down_t, e, H, h0, G};
-    f32x16_t acc[2][2];
-    gv_mainloop(smem, ar, br, G, acc);
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int h = h0 + wn * 64 + j * 32 + (lane & 31);
+      for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int q = 0; q < 16; ++q) {
-          const int r = wm * 64 + i * 32 + mfma32_row(q, lane);
-          if (r < rows) y[(int64_t)(p0 + r) * H + h] = acc[i][j][q];
-        }
-      }
+        for (int q = 0; q < 16; ++q) acc[i][j][q] = 0.0f;
   }
+  // the redundant tail DMAs must land before the workgroup's LDS is released
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
 // ------------------------------------------------------------------ combine
@@ -537,8 +592,8 @@ static int gemm_grid(int64_t items) {
   return (int)(g < 1 ? 1 : g);
 }
 
-static int gemm_grid_v2(int64_t items) {  // two workgroups per CU, a multiple of 8 (XCD order)
-  int64_t g = 2 * (int64_t)pp_device_cus();
+static int gemm_grid_v3(int64_t items) {  // GP_WG_PER_CU workgroups per CU, a multiple of 8 (XCD order)
+  int64_t g = (int64_t)GP_WG_PER_CU * pp_device_cus();
   if (items < g) g = items;
   g = (g + 7) / 8 * 8;
   return (int)(g < 8 ? 8 : g);
@@ -549,9 +604,9 @@ static int gateup_launch(const bf16_t* xb, int H, int G, const bf16_t* wrows, in
                          bf16_t* act, hipStream_t st) {
   (void)E;
   if (G % 64 == 0) {
-    int grid = gemm_grid_v2(max_tiles * (G / 64));
-    gateup_v2_kernel<<<grid, GM_THREADS, GV_STAGES * GV_STAGE_BYTES, st>>>(xb, H, G, wrows, token_ids, pair_gates,
-                                                                          tiles, meta, act);
+    int grid = gemm_grid_v3(max_tiles * (G / 64));
+    gemm_v3_kernel<0><<<grid, GM_THREADS, GP_LDS_BYTES, st>>>(xb, H, G, wrows, token_ids, pair_gates, tiles, meta,
+                                                              act, nullptr);
   } else {
     int grid = gemm_grid(max_tiles * (G / 32));
     gateup_kernel<4, 1, 1><<<grid, GM_THREADS, 0, st>>>(xb, H, G, wrows, token_ids, pair_gates, tiles, meta, act);
@@ -562,8 +617,9 @@ static int gateup_launch(const bf16_t* xb, int H, int G, const bf16_t* wrows, in
 static int down_launch(const bf16_t* act, int H, int G, const bf16_t* down_t, const int32_t* tiles,
                        const int32_t* meta, int64_t max_tiles, float* y, hipStream_t st) {
   if (G % 64 == 0) {
-    int grid = gemm_grid_v2(max_tiles * (H / 128));
-    down_v2_kernel<<<grid, GM_THREADS, GV_STAGES * GV_STAGE_BYTES, st>>>(act, H, G, down_t, tiles, meta, y);
+    int grid = gemm_grid_v3(max_tiles * (H / 128));
+    gemm_v3_kernel<1><<<grid, GM_THREADS, GP_LDS_BYTES, st>>>(act, H, G, down_t, nullptr, nullptr, tiles, meta,
+                                                              nullptr, y);
   } else {
     int grid = gemm_grid(max_tiles * (H / 128));
     down_kernel<<<grid, GM_THREADS, 0, st>>>(act, H, G, down_t, tiles, meta, y);
