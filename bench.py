@@ -61,6 +61,8 @@ def parse():
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="run 5 plain elementwise passes (torch.neg, fp32) over this many MiB first "
                          "(counter calibration for --pmc)")
+    ap.add_argument("--calibrate-only", action="store_true",
+                    help="run only the --calibrate-copy-mib pass (a profiler run of its own)")
     ap.add_argument("--pmc-summary", default=None,
                     help="summarise rocprofv3 --pmc csv output under this directory and exit")
     return ap.parse_args()
@@ -133,6 +135,8 @@ def main():
         print(f"calibration: 5 x torch.neg over {args.calibrate_copy_mib} MiB fp32 "
               f"(reads {n * 4} B, writes {n * 4} B per dispatch)", file=sys.stderr)
         del src, dst
+    if args.calibrate_only:
+        return
 
     # ---------------- layers (random init, packed once; reference-layout copies not kept)
     layers = []
