@@ -107,6 +107,7 @@ int pp_route_logits(const float* logits, int64_t n_tokens, int E, float tau,
  *   tiles       int32 [pp_max_tiles(N,E,tile_m)][4]: {expert, first pair, rows, 0}
  *   meta        int32 [4]: {number of tiles, number of pairs P, 0, 0}
  * workspace: pp_bucket_workspace_bytes(N, E) bytes of device scratch.
+ * mask must be 4-byte aligned (it is read as 32-bit words); PP_ERR_INVALID otherwise.
  * ------------------------------------------------------------------------- */
 size_t pp_bucket_workspace_bytes(int64_t n_tokens, int E);
 /* Row-tile height the grouped GEMMs (pp_expert_gateup / pp_expert_down) expect

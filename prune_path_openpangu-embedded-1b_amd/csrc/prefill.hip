@@ -675,13 +675,18 @@ extern "C" int pp_combine(const float* y_f32, const int32_t* token_pairs, const 
 // ------------------------------------------------------------------ whole prefill
 int pp_route_impl(const void* x, int x_dtype, const float* logits_in, int64_t N, int H, const float* router,
                   const float* bias, int E, float tau, float* logits_out, float* probs_out, float* gates_out,
-                  uint8_t* mask_out, int32_t* count_out, bf16_t* xbf_out, hipStream_t st);
+                  uint8_t* mask_out, int32_t* count_out, bf16_t* xbf_out, hipStream_t st, int32_t* blkcnt_out);
+int pp_bucket_from_counts(const uint8_t* mask, const float* gates, int64_t N, int E, int tile_m,
+                          const int32_t* blkcnt, int cb, int32_t* offsets, int32_t* token_ids, float* pair_gates,
+                          int32_t* token_pairs, int32_t* tiles, int32_t* meta, hipStream_t st);
+bool pp_bucket_counts16_fit(int64_t N, int E);
 int pp_bucket_impl(const uint8_t* mask, const float* gates, int64_t N, int E, int tile_m, int32_t* offsets,
                    int32_t* token_ids, float* pair_gates, int32_t* token_pairs, int32_t* tiles, int32_t* meta,
                    void* workspace, hipStream_t st);
 
 struct PrefillWs {
-  size_t gates, mask, count, offsets, token_ids, pair_gates, token_pairs, tiles, meta, bws, xbf, act, y, total;
+  size_t gates, mask, count, offsets, token_ids, pair_gates, token_pairs, tiles, meta, bws, blk16, xbf, act, y,
+      total;
 };
 
 static PrefillWs prefill_layout(int64_t N, int H, int E, int G) {
@@ -704,6 +709,7 @@ static PrefillWs prefill_layout(int64_t N, int H, int E, int G) {
   L.tiles = take((size_t)mt * 16);
   L.meta = take(16);
   L.bws = take(pp_bucket_workspace_bytes(N, E));
+  L.blk16 = take((size_t)((N + 15) / 16) * 16 * 4);  // route16's per-16-token expert counts
   L.xbf = take((size_t)N * H * 2);
   L.act = take((size_t)P * G * 2);
   L.y = take((size_t)P * H * 4);
@@ -742,12 +748,19 @@ extern "C" int pp_moe_prefill(const void* x, int x_dtype, int64_t n_tokens, int 
   bf16_t* act = (bf16_t*)(ws + L.act);
   float* y = (float*)(ws + L.y);
   const int64_t mt = pp_max_tiles(n_tokens, E, GM_BM);
+  // E = 16: the router kernel also counts selections per 16-token block, and the
+  // bucketing is one kernel from those counts (no counting or scan pass)
+  int32_t* blk16 = (E == 16 && pp_bucket_counts16_fit(n_tokens, E)) ? (int32_t*)(ws + L.blk16) : nullptr;
   if ((rc = pp_route_impl(x, x_dtype, nullptr, n_tokens, H, router_packed, bias, E, tau, nullptr, nullptr, gates,
-                          mask, count, x_dtype == PP_DTYPE_BF16 ? nullptr : xbf, st)))
+                          mask, count, x_dtype == PP_DTYPE_BF16 ? nullptr : xbf, st, blk16)))
     return rc;
-  if ((rc = pp_bucket_impl(mask, gates, n_tokens, E, GM_BM, offsets, token_ids, pair_gates, token_pairs, tiles, meta,
-                           ws + L.bws, st)))
-    return rc;
+  if (blk16)
+    rc = pp_bucket_from_counts(mask, gates, n_tokens, E, GM_BM, blk16, 16, offsets, token_ids, pair_gates,
+                               token_pairs, tiles, meta, st);
+  else
+    rc = pp_bucket_impl(mask, gates, n_tokens, E, GM_BM, offsets, token_ids, pair_gates, token_pairs, tiles, meta,
+                        ws + L.bws, st);
+  if (rc) return rc;
   if ((rc = gateup_launch(xbf, H, G, (const bf16_t*)packed, E, token_ids, pair_gates, tiles, meta, mt, act, st)))
     return rc;
   const bf16_t* down_t = (const bf16_t*)packed + (int64_t)E * G * 3 * H;

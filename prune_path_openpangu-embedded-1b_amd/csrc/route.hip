@@ -151,66 +151,12 @@ __device__ __forceinline__ void rt16_load(const XT* __restrict__ x, const float*
   }
 }
 
-template <typename XT>
-__global__ __launch_bounds__(64 * RT16_WAVES) void route16_kernel(
-    const XT* __restrict__ x, int64_t N, int H, const float* __restrict__ router, const float* __restrict__ bias,
-    float tau, float* __restrict__ logits_out, float* __restrict__ probs_out, float* __restrict__ gates_out,
-    uint8_t* __restrict__ mask_out, int32_t* __restrict__ count_out, bf16_t* __restrict__ xbf_out) {
-  __shared__ __align__(16) float part[RT16_WAVES][16][16];
-  __shared__ __align__(16) float lg_s[16][16];
-  __shared__ __align__(16) float ev_s[16][16];
-  __shared__ __align__(16) float srt_s[16][16];
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int64_t tok0 = (int64_t)blockIdx.x * 16;
-  {
-    const int r = lane & 15, g = lane >> 4;
-    const int64_t t = tok0 + r;
-    const bool valid = t < N;
-    const int nkb_w = H / (16 * RT16_WAVES);  // 16-wide K blocks per wave
-    const int kbase = w * nkb_w;
-    f32x4_t acc[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[j] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
-    float4 xa[RT16_CHUNK], wa[RT16_CHUNK], xn[RT16_CHUNK], wn[RT16_CHUNK];
-    rt16_load<XT>(x, router, t, valid, H, kbase, nkb_w, r, g, xa, wa);
-    for (int c0 = 0; c0 < nkb_w; c0 += RT16_CHUNK) {
-      const int left = nkb_w - c0 - RT16_CHUNK;
-      if (left > 0) rt16_load<XT>(x, router, t, valid, H, kbase + c0 + RT16_CHUNK, left, r, g, xn, wn);
-#pragma unroll
-      for (int i = 0; i < RT16_CHUNK; ++i) {
-        if (c0 + i < nkb_w) {
-          acc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[i].x, wa[i].x, acc[0], 0, 0, 0);
-          acc[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[i].y, wa[i].y, acc[1], 0, 0, 0);
-          acc[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[i].z, wa[i].z, acc[2], 0, 0, 0);
-          acc[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[i].w, wa[i].w, acc[3], 0, 0, 0);
-          if (xbf_out && valid) {
-            uint2 pk;
-            pk.x = (uint32_t)f32_to_bf16(xa[i].x) | ((uint32_t)f32_to_bf16(xa[i].y) << 16);
-            pk.y = (uint32_t)f32_to_bf16(xa[i].z) | ((uint32_t)f32_to_bf16(xa[i].w) << 16);
-            *(uint2*)(xbf_out + t * H + (kbase + c0 + i) * 16 + 4 * g) = pk;
-          }
-        }
-      }
-#pragma unroll
-      for (int i = 0; i < RT16_CHUNK; ++i) { xa[i] = xn[i]; wa[i] = wn[i]; }
-    }
-    // lane l, element q: token 4 (l / 16) + q, expert l % 16
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-      part[w][4 * g + q][r] = __fadd_rn(__fadd_rn(__fadd_rn(acc[0][q], acc[1][q]), acc[2][q]), acc[3][q]);
-  }
-  __syncthreads();
-  if (tid < 256) {
-    const int rr = tid >> 4, e = tid & 15;
-    float l = part[0][rr][e];
-#pragma unroll
-    for (int ww = 1; ww < RT16_WAVES; ++ww) l = __fadd_rn(l, part[ww][rr][e]);
-    if (bias) l = __fadd_rn(l, bias[e]);
-    lg_s[rr][e] = l;
-  }
-  __syncthreads();
-  if (w >= 4) return;
-  // ---- selection: wave w, group q4 = lane / 16 -> token 4 w + q4, lane j = expert
+// ---- selection: wave w, group q4 = lane / 16 -> token 4 w + q4, lane j = expert
+__device__ __forceinline__ void route16_select(const float (*lg_s)[16], float (*ev_s)[16], float (*srt_s)[16],
+                                               int* cnt_s, int64_t tok0, int64_t N, float tau, int lane, int w,
+                                               float* __restrict__ logits_out, float* __restrict__ probs_out,
+                                               float* __restrict__ gates_out, uint8_t* __restrict__ mask_out,
+                                               int32_t* __restrict__ count_out) {
   const int rr = 4 * w + (lane >> 4), j = lane & 15;
   const int64_t t = tok0 + rr;
   const float xl = lg_s[rr][j];
@@ -267,13 +213,85 @@ __global__ __launch_bounds__(64 * RT16_WAVES) void route16_kernel(
     if (gates_out) gates_out[t * 16 + j] = s ? pp_sigmoid(xl) : 0.0f;
     if (mask_out) mask_out[t * 16 + j] = (uint8_t)s;
     if (count_out && j == 0) count_out[t] = k;
+    if (s) atomicAdd(&cnt_s[j], 1);
   }
 }
 
+template <typename XT>
+__global__ __launch_bounds__(64 * RT16_WAVES) void route16_kernel(
+    const XT* __restrict__ x, int64_t N, int H, const float* __restrict__ router, const float* __restrict__ bias,
+    float tau, float* __restrict__ logits_out, float* __restrict__ probs_out, float* __restrict__ gates_out,
+    uint8_t* __restrict__ mask_out, int32_t* __restrict__ count_out, bf16_t* __restrict__ xbf_out,
+    int32_t* __restrict__ blkcnt_out) {
+  __shared__ __align__(16) float part[RT16_WAVES][16][16];
+  __shared__ __align__(16) float lg_s[16][16];
+  __shared__ __align__(16) float ev_s[16][16];
+  __shared__ __align__(16) float srt_s[16][16];
+  __shared__ int cnt_s[16];  // selections per expert over this workgroup's 16 tokens
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int64_t tok0 = (int64_t)blockIdx.x * 16;
+  if (tid < 16) cnt_s[tid] = 0;
+  {
+    const int r = lane & 15, g = lane >> 4;
+    const int64_t t = tok0 + r;
+    const bool valid = t < N;
+    const int nkb_w = H / (16 * RT16_WAVES);  // 16-wide K blocks per wave
+    const int kbase = w * nkb_w;
+    f32x4_t acc[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[j] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+    float4 xa[RT16_CHUNK], wa[RT16_CHUNK], xn[RT16_CHUNK], wn[RT16_CHUNK];
+    rt16_load<XT>(x, router, t, valid, H, kbase, nkb_w, r, g, xa, wa);
+    for (int c0 = 0; c0 < nkb_w; c0 += RT16_CHUNK) {
+      const int left = nkb_w - c0 - RT16_CHUNK;
+      if (left > 0) rt16_load<XT>(x, router, t, valid, H, kbase + c0 + RT16_CHUNK, left, r, g, xn, wn);
+#pragma unroll
+      for (int i = 0; i < RT16_CHUNK; ++i) {
+        if (c0 + i < nkb_w) {
+          acc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[i].x, wa[i].x, acc[0], 0, 0, 0);
+          acc[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[i].y, wa[i].y, acc[1], 0, 0, 0);
+          acc[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[i].z, wa[i].z, acc[2], 0, 0, 0);
+          acc[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[i].w, wa[i].w, acc[3], 0, 0, 0);
+          if (xbf_out && valid) {
+            uint2 pk;
+            pk.x = (uint32_t)f32_to_bf16(xa[i].x) | ((uint32_t)f32_to_bf16(xa[i].y) << 16);
+            pk.y = (uint32_t)f32_to_bf16(xa[i].z) | ((uint32_t)f32_to_bf16(xa[i].w) << 16);
+            *(uint2*)(xbf_out + t * H + (kbase + c0 + i) * 16 + 4 * g) = pk;
+          }
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < RT16_CHUNK; ++i) { xa[i] = xn[i]; wa[i] = wn[i]; }
+    }
+    // lane l, element q: token 4 (l / 16) + q, expert l % 16
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      part[w][4 * g + q][r] = __fadd_rn(__fadd_rn(__fadd_rn(acc[0][q], acc[1][q]), acc[2][q]), acc[3][q]);
+  }
+  __syncthreads();
+  if (tid < 256) {
+    const int rr = tid >> 4, e = tid & 15;
+    float l = part[0][rr][e];
+#pragma unroll
+    for (int ww = 1; ww < RT16_WAVES; ++ww) l = __fadd_rn(l, part[ww][rr][e]);
+    if (bias) l = __fadd_rn(l, bias[e]);
+    lg_s[rr][e] = l;
+  }
+  __syncthreads();
+  if (w < 4) route16_select(lg_s, ev_s, srt_s, cnt_s, tok0, N, tau, lane, w, logits_out, probs_out, gates_out,
+                            mask_out, count_out);
+  if (blkcnt_out) {  // per-block expert counts for the bucketing (blocks of 16 tokens)
+    __syncthreads();
+    if (tid < 16) blkcnt_out[(int64_t)blockIdx.x * 16 + tid] = cnt_s[tid];
+  }
+}
+
+// blkcnt_out (E = 16 path only, else untouched): per 16-token block, per expert, the
+// number of selections -- the bucketing's block counts, so it needs no counting pass.
 int pp_route_impl(const void* x, int x_dtype, const float* logits_in, int64_t N, int H,
                   const float* router, const float* bias, int E, float tau, float* logits_out,
                   float* probs_out, float* gates_out, uint8_t* mask_out, int32_t* count_out,
-                  bf16_t* xbf_out, hipStream_t st) {
+                  bf16_t* xbf_out, hipStream_t st, int32_t* blkcnt_out) {
   if (N == 0) return PP_OK;
   const int grid = (int)((N + ROUTE_TOK - 1) / ROUTE_TOK);
   const size_t smem = 0;
@@ -282,11 +300,12 @@ int pp_route_impl(const void* x, int x_dtype, const float* logits_in, int64_t N,
     const int g16 = (int)((N + 15) / 16);
     if (x_dtype == PP_DTYPE_F32)
       route16_kernel<float><<<g16, 64 * RT16_WAVES, 0, st>>>((const float*)x, N, H, router, bias, tau, logits_out,
-                                                            probs_out, gates_out, mask_out, count_out, xbf_out);
+                                                            probs_out, gates_out, mask_out, count_out, xbf_out,
+                                                            blkcnt_out);
     else
       route16_kernel<bf16_t><<<g16, 64 * RT16_WAVES, 0, st>>>((const bf16_t*)x, N, H, router, bias, tau,
                                                              logits_out, probs_out, gates_out, mask_out,
-                                                             count_out, xbf_out);
+                                                             count_out, xbf_out, blkcnt_out);
     return pp_check_launch("route16_kernel");
   }
   if (logits_in) {
@@ -314,7 +333,7 @@ extern "C" int pp_route(const void* x, int x_dtype, int64_t n_tokens, int H, con
   PP_REQUIRE(n_tokens == 0 || (x && router_packed), PP_ERR_INVALID, "pp_route: null x/router");
   PP_REQUIRE(x_dtype == PP_DTYPE_F32 || x_dtype == PP_DTYPE_BF16, PP_ERR_INVALID, "pp_route: x_dtype %d", x_dtype);
   return pp_route_impl(x, x_dtype, nullptr, n_tokens, H, router_packed, bias, E, tau, logits_out,
-                       probs_out, gates_out, mask_out, count_out, nullptr, (hipStream_t)stream);
+                       probs_out, gates_out, mask_out, count_out, nullptr, (hipStream_t)stream, nullptr);
 }
 
 extern "C" int pp_route_logits(const float* logits, int64_t n_tokens, int E, float tau, float* probs_out,
@@ -323,7 +342,7 @@ extern "C" int pp_route_logits(const float* logits, int64_t n_tokens, int E, flo
   PP_REQUIRE(n_tokens >= 0, PP_ERR_INVALID, "pp_route_logits: n_tokens < 0");
   PP_REQUIRE(n_tokens == 0 || logits, PP_ERR_INVALID, "pp_route_logits: null logits");
   return pp_route_impl(nullptr, PP_DTYPE_F32, logits, n_tokens, 128, nullptr, nullptr, E, tau, nullptr,
-                       probs_out, gates_out, mask_out, count_out, nullptr, (hipStream_t)stream);
+                       probs_out, gates_out, mask_out, count_out, nullptr, (hipStream_t)stream, nullptr);
 }
 
 // ------------------------------------------------------------------ bucketing
@@ -344,16 +363,37 @@ extern "C" int pp_route_logits(const float* logits, int64_t n_tokens, int E, flo
 
 __device__ __forceinline__ void bucket_block_words(const uint8_t* __restrict__ mask, int64_t N, int E, int64_t t0,
                                                    unsigned long long* tokw, unsigned long long (*expw)[BKT_QW]) {
+  // the block's mask bytes as 32-bit words (the block starts at byte t0 * E, a multiple
+  // of 64 E, so words are aligned); the first words are loaded before the LDS clearing
+  // and its barrier, and every word of a batch before the first LDS update
+  const int64_t nt = min((int64_t)BKT_TOK, N - t0);
+  const int nb = (int)nt * E, nw = (nb + 3) >> 2;
+  const uint32_t* mw = (const uint32_t*)(mask + t0 * E);
+  uint32_t v[4];
+  auto load4 = [&](int w0) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int wi = w0 + q * BKT_THREADS + threadIdx.x;
+      v[q] = wi < nw ? mw[wi] : 0u;
+    }
+  };
+  load4(0);
   for (int e = threadIdx.x; e < E; e += BKT_THREADS) tokw[e] = 0ull;
   for (int l = threadIdx.x; l < BKT_TOK * BKT_QW; l += BKT_THREADS) expw[l / BKT_QW][l % BKT_QW] = 0ull;
   __syncthreads();
-  const int pairs = BKT_TOK * E;
-  for (int i = threadIdx.x; i < pairs; i += BKT_THREADS) {
-    const int l = i / E, e = i - l * E;
-    const int64_t t = t0 + l;
-    if (t < N && mask[t * E + e]) {
-      atomicOr(&tokw[e], 1ull << l);
-      atomicOr(&expw[l][e >> 6], 1ull << (e & 63));
+  for (int w0 = 0; w0 < nw; w0 += 4 * BKT_THREADS) {
+    if (w0) load4(w0);
+    // rolled on purpose: the instruction cache is cold at launch, code size is latency
+#pragma unroll 1
+    for (int k = 0; k < 16; ++k) {
+      const int q = k >> 2, by = k & 3;
+      const int i = 4 * (w0 + q * BKT_THREADS + threadIdx.x) + by;
+      const uint32_t vq = q == 0 ? v[0] : q == 1 ? v[1] : q == 2 ? v[2] : v[3];
+      if (i < nb && ((vq >> (8 * by)) & 0xffu)) {
+        const int l = i / E, e = i - l * E;
+        atomicOr(&tokw[e], 1ull << l);
+        atomicOr(&expw[l][e >> 6], 1ull << (e & 63));
+      }
     }
   }
   __syncthreads();
@@ -367,14 +407,70 @@ __global__ __launch_bounds__(BKT_THREADS) void bucket_count_kernel(const uint8_t
   for (int e = threadIdx.x; e < E; e += BKT_THREADS) blkcnt[(int64_t)blockIdx.x * E + e] = __popcll(tokw[e]);
 }
 
+// Exclusive prefixes over experts of the pair totals (CSR offsets) and of their
+// row-tile counts (tile-map offsets); thread e < E holds expert e's total, the others
+// pass 0. One shuffle scan per wave (only as many steps as E needs), earlier waves'
+// sums through LDS. Fills off_s / toff_s [E + 1]; every thread of the block calls it;
+// ends on a barrier. blockDim.x == BKT_THREADS, E <= BKT_THREADS.
+__device__ __forceinline__ void bucket_expert_scan(int tot, int E, int tile_m, int* off_s, int* toff_s) {
+  __shared__ int wsum_s[2][BKT_THREADS / 64];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int nt = (tot + tile_m - 1) / tile_m;
+  int ip = tot, it = nt;
+  const int span = min(E, 64);
+  for (int d = 1; d < span; d <<= 1) {
+    const int vp = __shfl_up(ip, d), vt = __shfl_up(it, d);
+    if (lane >= d) {
+      ip += vp;
+      it += vt;
+    }
+  }
+  if (E > 64) {  // several waves hold experts
+    if (lane == 63) {
+      wsum_s[0][w] = ip;
+      wsum_s[1][w] = it;
+    }
+    __syncthreads();
+    for (int v = 0; v < w; ++v) {
+      ip += wsum_s[0][v];
+      it += wsum_s[1][v];
+    }
+  }
+  if (tid < E) {
+    off_s[tid] = ip - tot;
+    toff_s[tid] = it - nt;
+  }
+  if (tid == E - 1) {
+    off_s[E] = ip;
+    toff_s[E] = it;
+  }
+  __syncthreads();
+}
+
+// Row-tile map from the scanned offsets: tile i of expert e is {e, first pair, rows,
+// 0}; BKT_THREADS / E threads per expert take its tiles in turn.
+__device__ __forceinline__ void bucket_write_tiles(int E, int tile_m, const int* off_s, const int* toff_s,
+                                                   int32_t* __restrict__ tiles) {
+  const int G = BKT_THREADS / E;  // >= 1
+  if ((int)threadIdx.x < G * E) {
+    const int g = threadIdx.x / E, e = threadIdx.x - g * E;
+    const int o = off_s[e], ne = off_s[e + 1] - o, t0 = toff_s[e], nt = toff_s[e + 1] - t0;
+    for (int i = g; i < nt; i += G) {
+      int32_t* tp = tiles + (int64_t)(t0 + i) * 4;
+      tp[0] = e;
+      tp[1] = o + i * tile_m;
+      tp[2] = min(tile_m, ne - i * tile_m);
+      tp[3] = 0;
+    }
+  }
+}
+
 // One workgroup: expert totals, CSR offsets, per-block write offsets, GEMM tile map.
 __global__ __launch_bounds__(256) void bucket_scan_kernel(const int32_t* __restrict__ blkcnt, int nblk,
                                                           int E, int tile_m, int32_t* __restrict__ blkoff,
                                                           int32_t* __restrict__ offsets,
                                                           int32_t* __restrict__ tiles,
                                                           int32_t* __restrict__ meta) {
-  __shared__ int tot[PP_MAX_EXPERTS];
-  __shared__ int ntl[PP_MAX_EXPERTS];
   __shared__ int off_s[PP_MAX_EXPERTS + 1];
   __shared__ int toff_s[PP_MAX_EXPERTS + 1];
   __shared__ int cnt_s[BKT_SCAN_CHUNK];
@@ -391,28 +487,15 @@ __global__ __launch_bounds__(256) void bucket_scan_kernel(const int32_t* __restr
     if (e < E)
       for (int b = 0; b < nb; ++b) s += cnt_s[b * E + e];
   }
-  if (e < E) {
-    tot[e] = s;
-    ntl[e] = (s + tile_m - 1) / tile_m;
-  }
-  __syncthreads();
+  bucket_expert_scan(e < E ? s : 0, E, tile_m, off_s, toff_s);
   if (threadIdx.x == 0) {
-    int o = 0, to = 0;
-    for (int j = 0; j < E; ++j) {
-      off_s[j] = o;
-      toff_s[j] = to;
-      o += tot[j];
-      to += ntl[j];
-    }
-    off_s[E] = o;
-    toff_s[E] = to;
-    meta[0] = to;
-    meta[1] = o;
+    meta[0] = toff_s[E];
+    meta[1] = off_s[E];
     meta[2] = 0;
     meta[3] = 0;
   }
-  __syncthreads();
   for (int j = threadIdx.x; j <= E; j += 256) offsets[j] = off_s[j];
+  bucket_write_tiles(E, tile_m, off_s, toff_s, tiles);
   int run = e < E ? off_s[e] : 0;
   for (int b0 = 0; b0 < nblk; b0 += cb) {
     const int nb = min(cb, nblk - b0);
@@ -428,16 +511,6 @@ __global__ __launch_bounds__(256) void bucket_scan_kernel(const int32_t* __restr
     __syncthreads();
     for (int i = threadIdx.x; i < nb * E; i += 256) blkoff[(int64_t)b0 * E + i] = cnt_s[i];
   }
-  for (int j = 0; j < E; ++j) {  // tile i of expert j
-    const int n = tot[j];
-    for (int i = threadIdx.x; i < ntl[j]; i += 256) {
-      int32_t* tp = tiles + (int64_t)(toff_s[j] + i) * 4;
-      tp[0] = j;
-      tp[1] = off_s[j] + i * tile_m;
-      tp[2] = min(tile_m, n - i * tile_m);
-      tp[3] = 0;
-    }
-  }
 }
 
 __device__ __forceinline__ int popc_below(const unsigned long long* w, int bit) {
@@ -448,6 +521,74 @@ __device__ __forceinline__ int popc_below(const unsigned long long* w, int bit) 
   return c;
 }
 
+// Placement of the pairs of block blockIdx.x once its selection words are in LDS: four
+// consecutive pairs per thread step (their gates as one 16-byte load when aligned).
+// The gates of pairs 4i .. 4i+3 of the block (zeros past the block's end).
+__device__ __forceinline__ float4 bucket_gate4(const float* __restrict__ gates, int64_t t0, int E, int nb, int i0) {
+  float4 g = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (i0 + 4 <= nb) {
+    g = *(const float4*)(gates + t0 * E + i0);
+  } else {
+    if (i0 + 0 < nb) g.x = gates[t0 * E + i0 + 0];
+    if (i0 + 1 < nb) g.y = gates[t0 * E + i0 + 1];
+    if (i0 + 2 < nb) g.z = gates[t0 * E + i0 + 2];
+  }
+  return g;
+}
+
+// g_first: this thread's first gate quad (pairs 4 tid ..), loaded by the caller early.
+__device__ __forceinline__ void bucket_scatter_pairs(const float* __restrict__ gates, int64_t N, int E,
+                                                     const int* base_s, int32_t* __restrict__ token_ids,
+                                                     float* __restrict__ pair_gates,
+                                                     int32_t* __restrict__ token_pairs,
+                                                     const unsigned long long* tokw,
+                                                     const unsigned long long (*expw)[BKT_QW], float4 g_first) {
+  const int64_t t0 = (int64_t)blockIdx.x * BKT_TOK;
+  const int64_t nt = min((int64_t)BKT_TOK, N - t0);
+  const int nb = (int)nt * E;
+  for (int i0 = 4 * threadIdx.x; i0 < nb; i0 += 4 * BKT_THREADS) {
+    float4 g = g_first;
+    if (i0 != 4 * (int)threadIdx.x && gates && pair_gates) g = bucket_gate4(gates, t0, E, nb, i0);
+#pragma unroll 1
+    for (int by = 0; by < 4; ++by) {
+      const int i = i0 + by;
+      if (i >= nb) break;
+      const int l = i / E, e = i - l * E;
+      const int64_t t = t0 + l;
+      const unsigned long long* ew = expw[l];
+      const bool sel = (ew[e >> 6] >> (e & 63)) & 1ull;
+      const int below = popc_below(ew, e);  // selected experts of this token below e
+      if (sel) {
+        const int pos = base_s[e] + (l ? __popcll(tokw[e] & (~0ull >> (64 - l))) : 0);
+        token_ids[pos] = (int32_t)t;
+        if (pair_gates) pair_gates[pos] = by == 0 ? g.x : by == 1 ? g.y : by == 2 ? g.z : g.w;
+        if (token_pairs) token_pairs[t * E + below] = pos;
+      } else if (token_pairs) {
+        int cnt = 0;
+        for (int q = 0; q < BKT_QW; ++q) cnt += __popcll(ew[q]);
+        token_pairs[t * E + cnt + (e - below)] = -1;  // unselected experts fill the tail in order
+      }
+    }
+  }
+}
+
+// Block blockIdx.x of BKT_TOK tokens: pair (l, e) -> position base_s[e] + (tokens of
+// the block below l that selected e); base_s is read after the barrier inside
+// bucket_block_words.
+__device__ __forceinline__ void bucket_scatter_block(const uint8_t* __restrict__ mask,
+                                                     const float* __restrict__ gates, int64_t N, int E,
+                                                     const int* base_s, int32_t* __restrict__ token_ids,
+                                                     float* __restrict__ pair_gates,
+                                                     int32_t* __restrict__ token_pairs, unsigned long long* tokw,
+                                                     unsigned long long (*expw)[BKT_QW]) {
+  const int64_t t0 = (int64_t)blockIdx.x * BKT_TOK;
+  const int nb = (int)min((int64_t)BKT_TOK, N - t0) * E;
+  const float4 g_first = (gates && pair_gates) ? bucket_gate4(gates, t0, E, nb, 4 * threadIdx.x)
+                                               : make_float4(0.f, 0.f, 0.f, 0.f);
+  bucket_block_words(mask, N, E, t0, tokw, expw);
+  bucket_scatter_pairs(gates, N, E, base_s, token_ids, pair_gates, token_pairs, tokw, expw, g_first);
+}
+
 __global__ __launch_bounds__(BKT_THREADS) void bucket_scatter_kernel(
     const uint8_t* __restrict__ mask, const float* __restrict__ gates, int64_t N, int E,
     const int32_t* __restrict__ blkoff, int32_t* __restrict__ token_ids, float* __restrict__ pair_gates,
@@ -455,28 +596,91 @@ __global__ __launch_bounds__(BKT_THREADS) void bucket_scatter_kernel(
   __shared__ unsigned long long tokw[PP_MAX_EXPERTS];
   __shared__ unsigned long long expw[BKT_TOK][BKT_QW];
   __shared__ int base_s[PP_MAX_EXPERTS];
-  const int64_t t0 = (int64_t)blockIdx.x * BKT_TOK;
   for (int e = threadIdx.x; e < E; e += BKT_THREADS) base_s[e] = blkoff[(int64_t)blockIdx.x * E + e];
-  bucket_block_words(mask, N, E, t0, tokw, expw);
-  const int pairs = BKT_TOK * E;
-  for (int i = threadIdx.x; i < pairs; i += BKT_THREADS) {
-    const int l = i / E, e = i - l * E;
-    const int64_t t = t0 + l;
-    if (t >= N) break;  // pairs of later tokens are later too
-    const unsigned long long* ew = expw[l];
-    const bool sel = (ew[e >> 6] >> (e & 63)) & 1ull;
-    const int below = popc_below(ew, e);  // selected experts of this token below e
-    if (sel) {
-      const int pos = base_s[e] + (l ? __popcll(tokw[e] & (~0ull >> (64 - l))) : 0);
-      token_ids[pos] = (int32_t)t;
-      if (pair_gates) pair_gates[pos] = gates ? gates[t * E + e] : 0.0f;
-      if (token_pairs) token_pairs[t * E + below] = pos;
-    } else if (token_pairs) {
-      int cnt = 0;
-      for (int q = 0; q < BKT_QW; ++q) cnt += __popcll(ew[q]);
-      token_pairs[t * E + cnt + (e - below)] = -1;  // unselected experts fill the tail in order
+  bucket_scatter_block(mask, gates, N, E, base_s, token_ids, pair_gates, token_pairs, tokw, expw);
+}
+
+// Scan and scatter in one kernel when the block-count table is small (nblk_c * E <=
+// BKT_PLACE_INTS): every workgroup stages the whole table (counts per block of cb
+// tokens, cb dividing BKT_TOK) in LDS and computes the expert totals, the CSR offsets
+// and its own blocks' bases itself -- a few KB of L2 reads per workgroup instead of a
+// serial scan kernel between counting and scattering. Workgroup 0 also writes the CSR
+// offsets, the tile map and meta, as bucket_scan_kernel does. Same layout bit for bit.
+#define BKT_PLACE_INTS 8192
+__global__ __launch_bounds__(BKT_THREADS) void bucket_place_kernel(
+    const uint8_t* __restrict__ mask, const float* __restrict__ gates, int64_t N, int E,
+    const int32_t* __restrict__ blkcnt, int cb, int nblk_c, int tile_m, int32_t* __restrict__ offsets,
+    int32_t* __restrict__ token_ids, float* __restrict__ pair_gates, int32_t* __restrict__ token_pairs,
+    int32_t* __restrict__ tiles, int32_t* __restrict__ meta) {
+  __shared__ int cnt_s[BKT_PLACE_INTS];
+  __shared__ int part_tot[BKT_THREADS], part_pre[BKT_THREADS];
+  __shared__ int base_s[PP_MAX_EXPERTS];
+  __shared__ int off_s[PP_MAX_EXPERTS + 1], toff_s[PP_MAX_EXPERTS + 1];
+  __shared__ unsigned long long tokw[PP_MAX_EXPERTS];
+  __shared__ unsigned long long expw[BKT_TOK][BKT_QW];
+  const int tid = threadIdx.x;
+  const int n = nblk_c * E;
+  // independent loads first: the start of the count table, this thread's first gate
+  // quad; the mask words follow inside bucket_block_words, all in one round trip
+  int cv[8];
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const int i = tid + q * BKT_THREADS;
+    cv[q] = i < n ? blkcnt[i] : 0;
+  }
+  const int64_t t0 = (int64_t)blockIdx.x * BKT_TOK;
+  const bool has_tokens = t0 < N;
+  const int nb = has_tokens ? (int)min((int64_t)BKT_TOK, N - t0) * E : 0;
+  const float4 g_first = (has_tokens && gates && pair_gates) ? bucket_gate4(gates, t0, E, nb, 4 * tid)
+                                                             : make_float4(0.f, 0.f, 0.f, 0.f);
+  if (has_tokens) bucket_block_words(mask, N, E, t0, tokw, expw);  // has barriers
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const int i = tid + q * BKT_THREADS;
+    if (i < n) cnt_s[i] = cv[q];
+  }
+  for (int i = tid + 8 * BKT_THREADS; i < n; i += BKT_THREADS) cnt_s[i] = blkcnt[i];
+  __syncthreads();
+  // thread (g, e): column e of blocks g, g + G, ...; totals and the prefix before this
+  // workgroup's first count block
+  const int G = BKT_THREADS / E;  // >= 1 (E <= 256)
+  const int c_first = (int)(((int64_t)blockIdx.x * BKT_TOK) / cb);
+  if (tid < G * E) {
+    const int g = tid / E, e = tid - g * E;
+    int tot = 0, pre = 0;
+#pragma unroll 4
+    for (int c = g; c < nblk_c; c += G) {
+      const int v = cnt_s[c * E + e];
+      tot += v;
+      pre += c < c_first ? v : 0;
+    }
+    part_tot[tid] = tot;
+    part_pre[tid] = pre;
+  }
+  __syncthreads();
+  int tot = 0, pre = 0;  // expert tid's column total and prefix
+  if (tid < E) {
+#pragma unroll 4
+    for (int g = 0; g < G; ++g) {
+      tot += part_tot[g * E + tid];
+      pre += part_pre[g * E + tid];
     }
   }
+  bucket_expert_scan(tot, E, tile_m, off_s, toff_s);  // ends on a barrier
+  if (tid < E) base_s[tid] = off_s[tid] + pre;
+  if (blockIdx.x == 0) {
+    for (int e = tid; e <= E; e += BKT_THREADS) offsets[e] = off_s[e];
+    if (tid == 0) {
+      meta[0] = toff_s[E];
+      meta[1] = off_s[E];
+      meta[2] = 0;
+      meta[3] = 0;
+    }
+    bucket_write_tiles(E, tile_m, off_s, toff_s, tiles);
+  }
+  if (!has_tokens) return;  // N == 0: only the offsets / tile map
+  __syncthreads();         // base_s
+  bucket_scatter_pairs(gates, N, E, base_s, token_ids, pair_gates, token_pairs, tokw, expw, g_first);
 }
 
 extern "C" size_t pp_bucket_workspace_bytes(int64_t n_tokens, int E) {
@@ -493,6 +697,22 @@ extern "C" int64_t pp_max_tiles(int64_t n_tokens, int E, int tile_m) {
   return (n_tokens * E) / tile_m + E;
 }
 
+// Bucketing from block counts already made (cb tokens per count block, cb | BKT_TOK):
+// one place kernel when the count table is small, else the scan + scatter pair (the
+// scatter needs BKT_TOK-token block bases, summed from the cb-token counts by the scan
+// only when cb == BKT_TOK -- callers with finer counts use the place path only).
+static bool bucket_place_fits(int64_t nblk_c, int E) { return nblk_c * E <= BKT_PLACE_INTS; }
+
+int pp_bucket_from_counts(const uint8_t* mask, const float* gates, int64_t N, int E, int tile_m,
+                          const int32_t* blkcnt, int cb, int32_t* offsets, int32_t* token_ids, float* pair_gates,
+                          int32_t* token_pairs, int32_t* tiles, int32_t* meta, hipStream_t st) {
+  const int64_t nblk_c = (N + cb - 1) / cb;
+  const int64_t nblk = (N + BKT_TOK - 1) / BKT_TOK;
+  bucket_place_kernel<<<(unsigned)(nblk > 0 ? nblk : 1), BKT_THREADS, 0, st>>>(
+      mask, gates, N, E, blkcnt, cb, (int)nblk_c, tile_m, offsets, token_ids, pair_gates, token_pairs, tiles, meta);
+  return pp_check_launch("pp_bucket");
+}
+
 int pp_bucket_impl(const uint8_t* mask, const float* gates, int64_t N, int E, int tile_m,
                    int32_t* offsets, int32_t* token_ids, float* pair_gates, int32_t* token_pairs,
                    int32_t* tiles, int32_t* meta, void* workspace, hipStream_t st) {
@@ -500,12 +720,18 @@ int pp_bucket_impl(const uint8_t* mask, const float* gates, int64_t N, int E, in
   int32_t* blkcnt = (int32_t*)workspace;
   int32_t* blkoff = blkcnt + (nblk < 1 ? 1 : nblk) * E;
   if (nblk > 0) bucket_count_kernel<<<(unsigned)nblk, BKT_THREADS, 0, st>>>(mask, N, E, blkcnt);
+  if (bucket_place_fits(nblk, E))
+    return pp_bucket_from_counts(mask, gates, N, E, tile_m, blkcnt, BKT_TOK, offsets, token_ids, pair_gates,
+                                 token_pairs, tiles, meta, st);
   bucket_scan_kernel<<<1, 256, 0, st>>>(blkcnt, (int)nblk, E, tile_m, blkoff, offsets, tiles, meta);
   if (nblk > 0)
     bucket_scatter_kernel<<<(unsigned)nblk, BKT_THREADS, 0, st>>>(mask, gates, N, E, blkoff, token_ids, pair_gates,
                                                           token_pairs);
   return pp_check_launch("pp_bucket");
 }
+
+// Whether pp_bucket_from_counts can take route16's 16-token counts for N tokens.
+bool pp_bucket_counts16_fit(int64_t N, int E) { return bucket_place_fits((N + 15) / 16, E); }
 
 extern "C" int pp_bucket(const uint8_t* mask, const float* gates, int64_t n_tokens, int E, int tile_m,
                          int32_t* offsets, int32_t* token_ids, float* pair_gates, int32_t* token_pairs,
@@ -516,6 +742,8 @@ extern "C" int pp_bucket(const uint8_t* mask, const float* gates, int64_t n_toke
   PP_REQUIRE(tile_m >= 1, PP_ERR_INVALID, "pp_bucket: tile_m %d", tile_m);
   PP_REQUIRE(offsets && tiles && meta && workspace, PP_ERR_INVALID, "pp_bucket: null output/workspace");
   PP_REQUIRE(n_tokens == 0 || (mask && token_ids), PP_ERR_INVALID, "pp_bucket: null mask/token_ids");
+  PP_REQUIRE(((uintptr_t)mask & 3) == 0 && ((uintptr_t)gates & 3) == 0, PP_ERR_INVALID,
+             "pp_bucket: mask must be 4-byte aligned (read as 32-bit words)");
   return pp_bucket_impl(mask, gates, n_tokens, E, tile_m, offsets, token_ids, pair_gates, token_pairs, tiles,
                         meta, workspace, (hipStream_t)stream);
 }

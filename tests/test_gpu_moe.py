@@ -136,7 +136,8 @@ def _layer(seed, H=1536, E=16, G=384):
 
 
 @pytest.mark.parametrize("N,tau,zipf", [(2, 0.7, False), (37, 0.7, False), (16, 0.95, True),
-                                        (64, 0.95, True), (300, 0.7, False), (2048, 0.7, False)])
+                                        (64, 0.95, True), (300, 0.7, False), (2048, 0.7, False),
+                                        (8200, 0.7, False)])
 def test_prefill_shapes_vs_oracle(pkg, N, tau, zipf):
     w = _layer(100 + N)
     bias = gi.zipf_bias(16) if zipf else None
