@@ -277,14 +277,23 @@ __global__ __launch_bounds__(GM_THREADS, 2) void down_kernel(
 // in order; extra ops -- slot DMA, epilogue stores -- only make the wait stricter); the
 // barrier after it covers every wave and frees the stage written next.
 //
-// Measured alternatives (2048-token prefill, gate/up | down): the previous
-// two-stage kernel without the cross-item stream 54 | 34 us; one workgroup per CU with
-// four stages 81 | 50 (one wave per SIMD leaves the LDS and MFMA latencies exposed);
-// BK 32 with four stages 59 | 37 (twice the barriers); stream-K over (item, K block)
-// units with fp32 partials handed over through agent-scope stores 63 | 43 (the work is
-// balanced, but the per-block rate drops with all 512 workgroups streaming at once: the
-// GEMMs are bound by aggregate operand delivery, not by the second round); this
-// kernel 49 | 32.
+// Where the time goes (2048-token prefill, timestamps per workgroup): a K block takes
+// 1.07 us with two workgroups per CU -- 0.20 loop skeleton, 0.58 with only the MFMAs,
+// 0.36 with only the fragment reads, 0.73 without the DMA -- and the same with every
+// operand forced L2-resident, so the CU's own pipeline (DMA issue and landing, LDS,
+// MFMA, barrier), not HBM or L2, sets the rate: about 1.85 128x128x64 blocks per us per
+// CU. gate/up has ~630 items for 512 workgroups: the median workgroup is done at 34 us,
+// the 118 with a second item at 52. down: 28 | 33 us, of which ~13 us is the 77 MB fp32
+// y epilogue (HBM write rate).
+// Measured alternatives (gate/up | down): the two-stage kernel without the cross-item
+// stream 54 | 34 us; one workgroup per CU with four stages 81 | 50 (one wave per SIMD
+// leaves the LDS and MFMA latencies exposed); BK 32 with four stages 59 | 37; BK 32,
+// three stages, three workgroups per CU (every item in one round) 53 | 35 (the per-CU
+// rate drops to ~1.5 blocks/us); stream-K -- equal (item, K block) ranges per
+// workgroup, an item cut between two workgroups joined through an agent-scope ticket
+// and fp32 partial sums -- 58 | 47 (a K block slows to 1.25-1.35 us once workgroups
+// sharing a row tile or an expert's weights no longer walk K in step, and each join
+// costs 2.6-3 us of memory-side round trips); this kernel 49 | 32.
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
