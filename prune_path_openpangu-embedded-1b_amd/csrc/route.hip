@@ -127,27 +127,66 @@ __global__ __launch_bounds__(256) void route_kernel(
 }
 
 // ------------------------------------------------------------------ E = 16 fast path
-// 16 tokens x 16 experts per workgroup of 8 waves. Wave w owns the contiguous K slice
-// [w H/8, (w+1) H/8) and issues all of its x and router loads before the first MFMA
-// (RT16_CHUNK 16-wide K blocks at a time, the next chunk in flight under the current
-// one); the four float4 components feed four independent MFMA chains, added in
-// component order, then the eight wave partials are added in wave order through LDS
-// (fixed order: deterministic logits). Selection: four tokens per wave at once, one
-// per 16-lane group, branch-free, same arithmetic as select_small<16> (torch's sort is
-// stable for E <= 16, so rank = number of (greater, or equal with smaller index)).
+// 16 tokens x 16 experts per workgroup of 8 waves. x and the router pass through LDS in
+// K chunks of RT16_KC (four stages, DMA three chunks ahead), loaded as whole rows -- one
+// 1 KB row (or two 512-byte bf16 rows) per instruction, so a load touches a few cache
+// lines instead of sixteen: the per-CU address path, not bandwidth, bounded loads that
+// took sixteen rows x 64 bytes per instruction. 16-byte chunk c of LDS row r sits at
+// position c ^ r, so the sixteen rows of a fragment read land in distinct bank slots.
+// Wave w takes the 32-wide K block w of every chunk; lane (t = l % 16, g = l / 16) holds
+// x[t][k + 8g + j] and W[expert l % 16][k + 8g + j], j = 0..7, one fp32 MFMA per j
+// (chain j % 4), then the four chains are added in order and the eight wave partials in
+// wave order through LDS (fixed order: deterministic logits). Selection: four tokens per
+// wave at once, one per 16-lane group, branch-free, same arithmetic as select_small<16>
+// (torch's sort is stable for E <= 16, so rank = number of (greater, or equal with
+// smaller index)).
 #define RT16_WAVES 8
-#define RT16_CHUNK 8
-
+#define RT16_KC 256
+#define RT16_STAGES 4
+#define RT16_RROW (RT16_KC * 4)  // router row bytes in a stage
 template <typename XT>
-__device__ __forceinline__ void rt16_load(const XT* __restrict__ x, const float* __restrict__ router, int64_t t,
-                                          bool valid, int H, int kb0, int nkb, int r, int g, float4 (&xa)[RT16_CHUNK],
-                                          float4 (&wa)[RT16_CHUNK]) {
+struct Rt16 {
+  static constexpr int XROW = RT16_KC * (int)sizeof(XT);  // x row bytes in a stage
+  static constexpr int STAGE = 16 * (XROW + RT16_RROW);
+  static constexpr int DMA = sizeof(XT) == 4 ? 4 : 3;     // DMA instructions per wave per stage
+};
+typedef __attribute__((address_space(3))) void rt_lds_t;
+
+__device__ __forceinline__ void rt16_dma(const void* src, unsigned char* lds) {
+  __builtin_amdgcn_global_load_lds(src, (rt_lds_t*)lds, 16, 0, 0);
+}
+
+template <int N>
+__device__ __forceinline__ void rt16_wait_barrier() {
+  asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+// DMA of K chunk k0 .. k0 + kw into stage st: x rows of the workgroup's 16 tokens (rows
+// past N repeat row N - 1), then the 16 router rows. Chunks past kw load chunk 0 (in
+// range, never read).
+template <typename XT>
+__device__ __forceinline__ void rt16_issue(const XT* __restrict__ x, const float* __restrict__ router, int64_t N,
+                                           int H, int64_t tok0, int k0, int kw, unsigned char* st, int w, int lane) {
+  if (sizeof(XT) == 4) {
 #pragma unroll
-  for (int i = 0; i < RT16_CHUNK; ++i) {
-    const int kk = (kb0 + i) * 16 + 4 * g;
-    const bool in = i < nkb;
-    xa[i] = (in && valid) ? load_x4<XT>(x, t * H + kk) : make_float4(0.f, 0.f, 0.f, 0.f);
-    wa[i] = in ? *(const float4*)(router + (int64_t)r * H + kk) : make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int h = 0; h < 2; ++h) {  // x rows 2w, 2w + 1: 64 chunks of 4 floats
+      const int r = 2 * w + h;
+      const int c = lane ^ r;
+      const int64_t t = min(tok0 + r, N - 1);
+      rt16_dma(x + t * H + k0 + 4 * (c < kw / 4 ? c : 0), st + r * Rt16<XT>::XROW);
+    }
+  } else {  // x rows 2w (lanes 0..31), 2w + 1 (lanes 32..63): 32 chunks of 8 bf16
+    const int r = 2 * w + (lane >> 5);
+    const int c = (lane & 31) ^ r;
+    const int64_t t = min(tok0 + r, N - 1);
+    rt16_dma(x + t * H + k0 + 8 * (c < kw / 8 ? c : 0), st + 2 * w * Rt16<XT>::XROW);
+  }
+  unsigned char* rs = st + 16 * Rt16<XT>::XROW;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {  // router rows 2w, 2w + 1
+    const int e = 2 * w + h;
+    const int c = lane ^ e;
+    rt16_dma(router + (int64_t)e * H + k0 + 4 * (c < kw / 4 ? c : 0), rs + e * RT16_RROW);
   }
 }
 
@@ -232,41 +271,77 @@ __global__ __launch_bounds__(64 * RT16_WAVES) void route16_kernel(
   const int64_t tok0 = (int64_t)blockIdx.x * 16;
   if (tid < 16) cnt_s[tid] = 0;
   {
-    const int r = lane & 15, g = lane >> 4;
-    const int64_t t = tok0 + r;
-    const bool valid = t < N;
-    const int nkb_w = H / (16 * RT16_WAVES);  // 16-wide K blocks per wave
-    const int kbase = w * nkb_w;
+    __shared__ __align__(16) unsigned char stg[RT16_STAGES * Rt16<XT>::STAGE];
+    const int t_l = lane & 15, g = lane >> 4;
+    const int nst = (H + RT16_KC - 1) / RT16_KC;
+    auto chunk_w = [&](int sidx) { return min(RT16_KC, H - sidx * RT16_KC); };
     f32x4_t acc[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[j] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
-    float4 xa[RT16_CHUNK], wa[RT16_CHUNK], xn[RT16_CHUNK], wn[RT16_CHUNK];
-    rt16_load<XT>(x, router, t, valid, H, kbase, nkb_w, r, g, xa, wa);
-    for (int c0 = 0; c0 < nkb_w; c0 += RT16_CHUNK) {
-      const int left = nkb_w - c0 - RT16_CHUNK;
-      if (left > 0) rt16_load<XT>(x, router, t, valid, H, kbase + c0 + RT16_CHUNK, left, r, g, xn, wn);
 #pragma unroll
-      for (int i = 0; i < RT16_CHUNK; ++i) {
-        if (c0 + i < nkb_w) {
-          acc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[i].x, wa[i].x, acc[0], 0, 0, 0);
-          acc[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[i].y, wa[i].y, acc[1], 0, 0, 0);
-          acc[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[i].z, wa[i].z, acc[2], 0, 0, 0);
-          acc[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[i].w, wa[i].w, acc[3], 0, 0, 0);
-          if (xbf_out && valid) {
-            uint2 pk;
-            pk.x = (uint32_t)f32_to_bf16(xa[i].x) | ((uint32_t)f32_to_bf16(xa[i].y) << 16);
-            pk.y = (uint32_t)f32_to_bf16(xa[i].z) | ((uint32_t)f32_to_bf16(xa[i].w) << 16);
-            *(uint2*)(xbf_out + t * H + (kbase + c0 + i) * 16 + 4 * g) = pk;
-          }
+    for (int sidx = 0; sidx < RT16_STAGES - 1; ++sidx)
+      if (sidx < nst)
+        rt16_issue<XT>(x, router, N, H, tok0, sidx * RT16_KC, chunk_w(sidx), stg + sidx * Rt16<XT>::STAGE, w, lane);
+    for (int sidx = 0; sidx < nst; ++sidx) {
+      // chunk sidx has landed when at most the DMA of the chunks issued after it is
+      // outstanding (loads complete in order; the x stores in between only make it stricter)
+      if (sidx + 2 < nst) rt16_wait_barrier<2 * Rt16<XT>::DMA>();
+      else if (sidx + 1 < nst) rt16_wait_barrier<Rt16<XT>::DMA>();
+      else rt16_wait_barrier<0>();
+      unsigned char* st = stg + (sidx % RT16_STAGES) * Rt16<XT>::STAGE;
+      const int kw = chunk_w(sidx);
+      // x as bf16 for the grouped GEMMs (fp32 x only): thread -> row tid / 32, 8 values
+      if (sizeof(XT) == 4 && xbf_out) {
+        const int r = tid >> 5, k8 = (tid & 31) * 8;
+        const int64_t t = tok0 + r;
+        if (t < N && k8 < kw) {
+          const float4 v0 = *(const float4*)(st + r * Rt16<XT>::XROW + (((k8 >> 2) ^ r) << 4));
+          const float4 v1 = *(const float4*)(st + r * Rt16<XT>::XROW + ((((k8 >> 2) + 1) ^ r) << 4));
+          uint4 pk;
+          pk.x = (uint32_t)f32_to_bf16(v0.x) | ((uint32_t)f32_to_bf16(v0.y) << 16);
+          pk.y = (uint32_t)f32_to_bf16(v0.z) | ((uint32_t)f32_to_bf16(v0.w) << 16);
+          pk.z = (uint32_t)f32_to_bf16(v1.x) | ((uint32_t)f32_to_bf16(v1.y) << 16);
+          pk.w = (uint32_t)f32_to_bf16(v1.z) | ((uint32_t)f32_to_bf16(v1.w) << 16);
+          *(uint4*)(xbf_out + t * H + sidx * RT16_KC + k8) = pk;
         }
       }
+      if (sidx + RT16_STAGES - 1 < nst)
+        rt16_issue<XT>(x, router, N, H, tok0, (sidx + RT16_STAGES - 1) * RT16_KC, chunk_w(sidx + RT16_STAGES - 1),
+                       stg + ((sidx + RT16_STAGES - 1) % RT16_STAGES) * Rt16<XT>::STAGE, w, lane);
+      if (32 * w < kw) {  // this wave's K block of the chunk
+        float xv[8], wv8[8];
+        if (sizeof(XT) == 4) {
+          const int c0 = 8 * w + 2 * g;
+          const float4 a0 = *(const float4*)(st + t_l * Rt16<XT>::XROW + ((c0 ^ t_l) << 4));
+          const float4 a1 = *(const float4*)(st + t_l * Rt16<XT>::XROW + (((c0 + 1) ^ t_l) << 4));
+          xv[0] = a0.x; xv[1] = a0.y; xv[2] = a0.z; xv[3] = a0.w;
+          xv[4] = a1.x; xv[5] = a1.y; xv[6] = a1.z; xv[7] = a1.w;
+        } else {
+          const int c = 4 * w + g;
+          const uint4 u = *(const uint4*)(st + t_l * Rt16<XT>::XROW + ((c ^ t_l) << 4));
+          const uint32_t uw[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
-      for (int i = 0; i < RT16_CHUNK; ++i) { xa[i] = xn[i]; wa[i] = wn[i]; }
+          for (int i = 0; i < 4; ++i) {
+            xv[2 * i] = __uint_as_float(uw[i] << 16);
+            xv[2 * i + 1] = __uint_as_float(uw[i] & 0xffff0000u);
+          }
+        }
+        {
+          const unsigned char* rs = st + 16 * Rt16<XT>::XROW + t_l * RT16_RROW;  // expert row l % 16
+          const int c0 = 8 * w + 2 * g;
+          const float4 b0 = *(const float4*)(rs + ((c0 ^ t_l) << 4));
+          const float4 b1 = *(const float4*)(rs + (((c0 + 1) ^ t_l) << 4));
+          wv8[0] = b0.x; wv8[1] = b0.y; wv8[2] = b0.z; wv8[3] = b0.w;
+          wv8[4] = b1.x; wv8[5] = b1.y; wv8[6] = b1.z; wv8[7] = b1.w;
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[j & 3] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[j], wv8[j], acc[j & 3], 0, 0, 0);
+      }
     }
     // lane l, element q: token 4 (l / 16) + q, expert l % 16
 #pragma unroll
     for (int q = 0; q < 4; ++q)
-      part[w][4 * g + q][r] = __fadd_rn(__fadd_rn(__fadd_rn(acc[0][q], acc[1][q]), acc[2][q]), acc[3][q]);
+      part[w][4 * g + q][t_l] = __fadd_rn(__fadd_rn(__fadd_rn(acc[0][q], acc[1][q]), acc[2][q]), acc[3][q]);
   }
   __syncthreads();
   if (tid < 256) {
