@@ -293,7 +293,10 @@ __global__ __launch_bounds__(GM_THREADS, 2) void down_kernel(
 // workgroup, an item cut between two workgroups joined through an agent-scope ticket
 // and fp32 partial sums -- 58 | 47 (a K block slows to 1.25-1.35 us once workgroups
 // sharing a row tile or an expert's weights no longer walk K in step, and each join
-// costs 2.6-3 us of memory-side round trips); this kernel 49 | 32. Small batches (16 /
+// costs 2.6-3 us of memory-side round trips); 128 x 256 tiles, eight waves (2 x 4, the
+// same 64 x 64 wave tile), three stages, one workgroup per CU 61 | 32 (one barrier
+// keeps all eight waves in step, so the two waves of a SIMD no longer overlap each
+// other's waits, and 315 items leave 59 CUs with two); this kernel 49 | 32. Small batches (16 /
 // 64 tokens, ~100 items): four stages with the CU to itself 26.9 | 10.3 us against 26.4
 // | 9.5 -- the weights stream from HBM into LDS, so the bytes in flight per CU are capped
 // by LDS, ~5 MB over the chip where HBM needs ~16 MB; register-streamed loads (as in
