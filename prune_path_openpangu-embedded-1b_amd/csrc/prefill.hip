@@ -551,6 +551,182 @@ __global__ __launch_bounds__(GM_THREADS, GP_WG_PER_CU) void gemm_v3_kernel(
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
+// ------------------------------------------------------------------ short tiles
+// Small batches (N <= GS_MAX_N tokens): 32-row tiles (bucketed with tile_m = GS_TM),
+// items of 64 neurons (gate/up) or 128 hidden columns (down) as above. At such sizes
+// the 128-row kernel streams the weights at the rate its LDS stages allow in flight (two
+// 32 KB stages per workgroup, ~100 workgroups): a 20 KB stage (4 KB of A rows, 16 KB of
+// B rows) lets GS_STAGES - 1 blocks -- 96 KB of weights -- be in flight per CU. Four
+// waves split N: wave w computes B rows 32 w .. 32 w + 31 over the whole K, one 32x32x16
+// MFMA per k-step. gate/up: the B blocks are gate and up of neurons 0..31, then of
+// 32..63, so the up waves (1, 3) hand their accumulators to the gate waves (0, 2)
+// through LDS for the SwiGLU epilogue. Same DMA / slot / wait scheme as gemm_v3_kernel.
+#define GS_MAX_N 64
+#define GS_TM 32
+#define GS_STAGES 7
+#define GS_TILE_A (GS_TM * GP_ROWB)
+#define GS_TILE_B (128 * GP_ROWB)
+#define GS_STAGE (GS_TILE_A + GS_TILE_B)
+#define GS_SLOT_BYTES 256  // 32 token ids, then 32 pair gates
+#define GS_XCHG_BYTES (2 * 16 * 64 * 4)
+#define GS_LDS_BYTES (GS_STAGES * GS_STAGE + GP_NSLOT * GS_SLOT_BYTES + GS_XCHG_BYTES)
+#define GS_DMA 5  // DMA instructions per wave per K block: one A, four B
+
+template <int N>
+__device__ __forceinline__ void gv_wait2(u32x4& a, u32x4& b) {
+  asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(a), "+v"(b) : "n"(N));
+}
+
+template <int MODE>
+__global__ __launch_bounds__(GM_THREADS, 1) void gemm_s_kernel(
+    const bf16_t* __restrict__ abase, int H, int G, const bf16_t* __restrict__ bbase,
+    const int32_t* __restrict__ token_ids, const float* __restrict__ pair_gates,
+    const int32_t* __restrict__ tiles, const int32_t* __restrict__ meta, bf16_t* __restrict__ act,
+    float* __restrict__ y) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  unsigned char* slots = smem + GS_STAGES * GS_STAGE;
+  float* xchg = (float*)(slots + GP_NSLOT * GS_SLOT_BYTES);
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int n_ntile = MODE == 0 ? G / 64 : H / 128;
+  const int K = MODE == 0 ? H : G;
+  const int nkb = K / GP_BK;
+  const int n_items = meta[0] * n_ntile;
+  const GvItems it(n_items);
+  const int n_local_items = it.first < it.last ? (it.last - it.first + it.step - 1) / it.step : 0;
+  const int item0 = it.first, istep = it.step;
+  const int F = n_local_items * nkb;
+  if (F <= 0) return;
+  auto locate = [&](int f, int& li, int& kb) {
+    li = f / nkb;
+    kb = f - li * nkb;
+  };
+  // slot of item li (wave 0, one 4-byte DMA per lane): token ids, then pair gates of the
+  // tile rows, row r >= rows reading row rows - 1
+  auto slot_dma = [&](int li) {
+    if (MODE != 0 || w != 0) return;
+    const int item = item0 + li * istep;
+    const int t = item / n_ntile;
+    const int p0 = tiles[t * 4 + 1], rows = tiles[t * 4 + 2];
+    const int r = min(lane & 31, rows - 1);
+    gl2lds4(lane < 32 ? (const void*)(token_ids + p0 + r) : (const void*)(pair_gates + p0 + r),
+            slots + (li & (GP_NSLOT - 1)) * GS_SLOT_BYTES);
+  };
+  int64_t aoff, boff[4];
+  auto setup_item = [&](int li) {
+    const int item = item0 + li * istep;
+    const int t = item / n_ntile, nt = item - t * n_ntile;
+    const int e = tiles[t * 4 + 0], p0 = tiles[t * 4 + 1], rows = tiles[t * 4 + 2];
+    const int32_t* tok = (const int32_t*)(slots + (li & (GP_NSLOT - 1)) * GS_SLOT_BYTES);
+    {
+      const int r = w * GP_RPI + lane / GP_CH;  // A row 0..31
+      const int pchunk = ((lane % GP_CH) ^ gp_swz(r)) * 8;
+      aoff = MODE == 0 ? (int64_t)tok[r] * H + pchunk : (int64_t)(p0 + min(r, rows - 1)) * G + pchunk;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = (4 * i + w) * GP_RPI + lane / GP_CH;  // B row 0..127
+      const int pchunk = ((lane % GP_CH) ^ gp_swz(r)) * 8;
+      if (MODE == 0) {
+        const int wn_ = r >> 6, j = (r >> 5) & 1, q = r & 31;
+        boff[i] = ((int64_t)(e * G + nt * 64 + wn_ * 32 + q) * 3 + j) * H + pchunk;
+      } else {
+        boff[i] = ((int64_t)e * H + nt * 128 + r) * G + pchunk;
+      }
+    }
+  };
+  auto issue = [&](int f) {
+    int li, kb;
+    locate(f < F ? f : F - 1, li, kb);  // past the end: the last block again, never read
+    if (f < F && kb == 0) {
+      setup_item(li);
+      if (li >= 1 && li + 1 < n_local_items) slot_dma(li + 1);
+    }
+    unsigned char* sb = smem + (f % GS_STAGES) * GS_STAGE;
+    gl2lds(abase + aoff + kb * GP_BK, sb + w * 1024);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) gl2lds(bbase + boff[i] + kb * GP_BK, sb + GS_TILE_A + (4 * i + w) * 1024);
+  };
+
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void_t*)smem;
+  uint32_t offA[GP_KS], offB[GP_KS];
+#pragma unroll
+  for (int ks = 0; ks < GP_KS; ++ks) {
+    const int r = lane & 31, c = ks * 2 + (lane >> 5);
+    const uint32_t o = (uint32_t)(r * GP_CH + (c ^ gp_swz(r))) * 16;  // gp_swz(32 w + r) == gp_swz(r)
+    offA[ks] = lds0 + o;
+    offB[ks] = lds0 + GS_TILE_A + w * 32 * GP_ROWB + o;
+  }
+
+  slot_dma(0);
+  if (n_local_items > 1) slot_dma(1);
+  asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+#pragma unroll
+  for (int f = 0; f < GS_STAGES - 1; ++f) issue(f);
+
+  f32x16_t acc;
+#pragma unroll
+  for (int q = 0; q < 16; ++q) acc[q] = 0.0f;
+  for (int f = 0; f < F; ++f) {
+    gp_wait_barrier<GS_DMA * (GS_STAGES - 2)>();
+    issue(f + GS_STAGES - 1);
+    const uint32_t sbase = (f % GS_STAGES) * GS_STAGE;
+    u32x4 fa[2], fb[2];
+    fa[0] = gv_read<0>(offA[0] + sbase);
+    fb[0] = gv_read<0>(offB[0] + sbase);
+#pragma unroll
+    for (int ks = 0; ks < GP_KS; ++ks) {
+      const int cur = ks & 1, nxt = cur ^ 1;
+      if (ks < GP_KS - 1) {
+        fa[nxt] = gv_read<0>(offA[ks + 1] + sbase);
+        fb[nxt] = gv_read<0>(offB[ks + 1] + sbase);
+        gv_wait2<2>(fa[cur], fb[cur]);
+      } else {
+        gv_wait2<0>(fa[cur], fb[cur]);
+      }
+      acc = mfma32v(fa[cur], fb[cur], acc);
+    }
+    int li, kb;
+    locate(f, li, kb);
+    if (kb != nkb - 1) continue;
+    {
+      int ln = lane;
+      asm volatile("" : "+v"(ln));
+      const int item = item0 + li * istep;
+      const int t = item / n_ntile, nt = item - t * n_ntile;
+      const int p0 = tiles[t * 4 + 1], rows = tiles[t * 4 + 2];
+      if (MODE == 0) {
+        float* xw = xchg + (w >> 1) * 16 * 64;
+        if (w & 1) {
+#pragma unroll
+          for (int q = 0; q < 16; ++q) xw[q * 64 + ln] = acc[q];
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // LDS only: the DMA stays in flight
+        if (!(w & 1)) {
+          const float* gts = (const float*)(slots + (li & (GP_NSLOT - 1)) * GS_SLOT_BYTES + 128);
+          const int neuron = nt * 64 + (w >> 1) * 32 + (ln & 31);
+#pragma unroll
+          for (int q = 0; q < 16; ++q) {
+            const int r = mfma32_row(q, ln);
+            if (r < rows)
+              act[(int64_t)(p0 + r) * G + neuron] = f32_to_bf16(pp_silu(acc[q]) * xw[q * 64 + ln] * gts[r]);
+          }
+        }
+      } else {
+        const int h = nt * 128 + w * 32 + (ln & 31);
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+          const int r = mfma32_row(q, ln);
+          if (r < rows) y[(int64_t)(p0 + r) * H + h] = acc[q];
+        }
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < 16; ++q) acc[q] = 0.0f;
+  }
+  // the redundant tail DMAs must land before the workgroup's LDS is released
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+
 // ------------------------------------------------------------------ combine
 // Per (token, 8 columns): the token's pair ids are read first (one batch of independent
 // loads), then up to CB_BATCH y rows at once, summed in expert order: two memory round
@@ -615,11 +791,27 @@ static int gemm_grid_v3(int64_t items) {  // GP_WG_PER_CU workgroups per CU, a m
   return (int)(g < 8 ? 8 : g);
 }
 
+// Short tiles (gemm_s_kernel) for small batches inside pp_moe_prefill: the tile map is
+// then built with tile_m = GS_TM. Needs six K blocks per gate/up item (the next item's
+// slot lands GS_STAGES - 1 blocks ahead).
+static bool prefill_short_tiles(int64_t N, int H, int G) {
+  return N <= GS_MAX_N && G % 64 == 0 && H / GP_BK >= GS_STAGES - 1;
+}
+static int gemm_s_grid(int64_t items) {  // one workgroup per CU, a multiple of 8 (XCD order)
+  int64_t g = pp_device_cus();
+  if (items < g) g = items;
+  g = (g + 7) / 8 * 8;
+  return (int)(g < 8 ? 8 : g);
+}
+
 static int gateup_launch(const bf16_t* xb, int H, int G, const bf16_t* wrows, int E, const int32_t* token_ids,
                          const float* pair_gates, const int32_t* tiles, const int32_t* meta, int64_t max_tiles,
-                         bf16_t* act, hipStream_t st) {
+                         bf16_t* act, hipStream_t st, bool short_tiles = false) {
   (void)E;
-  if (G % 64 == 0) {
+  if (short_tiles) {
+    gemm_s_kernel<0><<<gemm_s_grid(max_tiles * (G / 64)), GM_THREADS, GS_LDS_BYTES, st>>>(
+        xb, H, G, wrows, token_ids, pair_gates, tiles, meta, act, nullptr);
+  } else if (G % 64 == 0) {
     int grid = gemm_grid_v3(max_tiles * (G / 64));
     gemm_v3_kernel<0><<<grid, GM_THREADS, GP_LDS_BYTES, st>>>(xb, H, G, wrows, token_ids, pair_gates, tiles, meta,
                                                               act, nullptr);
@@ -631,8 +823,11 @@ static int gateup_launch(const bf16_t* xb, int H, int G, const bf16_t* wrows, in
 }
 
 static int down_launch(const bf16_t* act, int H, int G, const bf16_t* down_t, const int32_t* tiles,
-                       const int32_t* meta, int64_t max_tiles, float* y, hipStream_t st) {
-  if (G % 64 == 0) {
+                       const int32_t* meta, int64_t max_tiles, float* y, hipStream_t st, bool short_tiles = false) {
+  if (short_tiles) {
+    gemm_s_kernel<1><<<gemm_s_grid(max_tiles * (H / 128)), GM_THREADS, GS_LDS_BYTES, st>>>(
+        act, H, G, down_t, nullptr, nullptr, tiles, meta, nullptr, y);
+  } else if (G % 64 == 0) {
     int grid = gemm_grid_v3(max_tiles * (H / 128));
     gemm_v3_kernel<1><<<grid, GM_THREADS, GP_LDS_BYTES, st>>>(act, H, G, down_t, nullptr, nullptr, tiles, meta,
                                                               nullptr, y);
@@ -714,7 +909,7 @@ static PrefillWs prefill_layout(int64_t N, int H, int E, int G) {
     return at;
   };
   const int64_t P = N * E;
-  const int64_t mt = pp_max_tiles(N, E, GM_BM);
+  const int64_t mt = pp_max_tiles(N, E, prefill_short_tiles(N, H, G) ? GS_TM : GM_BM);
   L.gates = take((size_t)P * 4);
   L.mask = take((size_t)P);
   L.count = take((size_t)N * 4);
@@ -763,7 +958,9 @@ extern "C" int pp_moe_prefill(const void* x, int x_dtype, int64_t n_tokens, int 
   bf16_t* xbf = x_dtype == PP_DTYPE_BF16 ? (bf16_t*)x : (bf16_t*)(ws + L.xbf);
   bf16_t* act = (bf16_t*)(ws + L.act);
   float* y = (float*)(ws + L.y);
-  const int64_t mt = pp_max_tiles(n_tokens, E, GM_BM);
+  const bool short_tiles = prefill_short_tiles(n_tokens, H, G);
+  const int tile_m = short_tiles ? GS_TM : GM_BM;
+  const int64_t mt = pp_max_tiles(n_tokens, E, tile_m);
   // E = 16: the router kernel also counts selections per 16-token block, and the
   // bucketing is one kernel from those counts (no counting or scan pass)
   int32_t* blk16 = (E == 16 && pp_bucket_counts16_fit(n_tokens, E)) ? (int32_t*)(ws + L.blk16) : nullptr;
@@ -771,15 +968,16 @@ extern "C" int pp_moe_prefill(const void* x, int x_dtype, int64_t n_tokens, int 
                           mask, count, x_dtype == PP_DTYPE_BF16 ? nullptr : xbf, st, blk16)))
     return rc;
   if (blk16)
-    rc = pp_bucket_from_counts(mask, gates, n_tokens, E, GM_BM, blk16, 16, offsets, token_ids, pair_gates,
+    rc = pp_bucket_from_counts(mask, gates, n_tokens, E, tile_m, blk16, 16, offsets, token_ids, pair_gates,
                                token_pairs, tiles, meta, st);
   else
-    rc = pp_bucket_impl(mask, gates, n_tokens, E, GM_BM, offsets, token_ids, pair_gates, token_pairs, tiles, meta,
+    rc = pp_bucket_impl(mask, gates, n_tokens, E, tile_m, offsets, token_ids, pair_gates, token_pairs, tiles, meta,
                         ws + L.bws, st);
   if (rc) return rc;
-  if ((rc = gateup_launch(xbf, H, G, (const bf16_t*)packed, E, token_ids, pair_gates, tiles, meta, mt, act, st)))
+  if ((rc = gateup_launch(xbf, H, G, (const bf16_t*)packed, E, token_ids, pair_gates, tiles, meta, mt, act, st,
+                          short_tiles)))
     return rc;
   const bf16_t* down_t = (const bf16_t*)packed + (int64_t)E * G * 3 * H;
-  if ((rc = down_launch(act, H, G, down_t, tiles, meta, mt, y, st))) return rc;
+  if ((rc = down_launch(act, H, G, down_t, tiles, meta, mt, y, st, short_tiles))) return rc;
   return combine_launch(y, token_pairs, count, n_tokens, H, E, (bf16_t*)out_bf16, st);
 }
