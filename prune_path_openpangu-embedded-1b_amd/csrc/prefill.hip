@@ -369,6 +369,118 @@ __device__ __forceinline__ void gp_wait_barrier() {
   asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(N) : "memory");
 }
 
+// ---- split items: the K blocks of an item shared by several workgroups
+// Schedule of both pipelined GEMMs (GpSched): rank q = XCD-major workgroup index (an
+// XCD's ranks are consecutive); full rounds of whole items first -- item r * grid + q in
+// round r, so the workgroups sharing a row tile or an expert's weights walk K in step --
+// then, with a split workspace, the tail items (n_items % grid) each cut into nparts K
+// ranges, one range per workgroup; the workgroups holding the parts of a tail item join
+// their fp32 partial sums (gp_join). Without a workspace: whole items, grid-strided.
+// Split workspace: sync words [0] (reserved), [1, 1 + grid) tickets (one per tail item),
+// then partial-sum slots of NF floats per thread, one slot per part (at most grid). The
+// tickets are zero at launch and every launch leaves them zero.
+#define GP_MIN_PART_BLOCKS 4  // a part shorter than this does not repay its join (measured)
+__device__ __forceinline__ void gp_st(uint32_t* p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+struct GpSched {
+  int n_whole;       // whole local items
+  int first, step;   // whole local item li is first + li * step
+  int part_item;     // the tail item of this workgroup's part (-1: none)
+  int kb_lo, kb_hi;  // its K blocks
+  int unit, nparts;  // part index = unit % nparts
+  int tail0;         // first tail item
+  __device__ GpSched(int n_items, int nkb, bool can_split) {
+    const int g = gridDim.x, per = g >> 3;
+    const int rank = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
+    const int rounds = n_items / g, tail = n_items - rounds * g;
+    nparts = (can_split && tail > 0) ? max(1, min(nkb / GP_MIN_PART_BLOCKS, g / tail)) : 1;
+    part_item = -1;
+    kb_lo = kb_hi = 0;
+    unit = rank;
+    tail0 = rounds * g;
+    if (nparts > 1) {
+      n_whole = rounds;
+      first = rank;
+      step = g;
+      if (rank < tail * nparts) {
+        const int ti = rank / nparts, pi = rank - ti * nparts;
+        part_item = tail0 + ti;
+        kb_lo = pi * nkb / nparts;
+        kb_hi = (pi + 1) * nkb / nparts;
+      }
+    } else {
+      const GvItems it(n_items);
+      n_whole = it.first < it.last ? (it.last - it.first + it.step - 1) / it.step : 0;
+      first = it.first;
+      step = it.step;
+    }
+  }
+  __device__ int n_local() const { return n_whole + (part_item >= 0 ? 1 : 0); }
+  __device__ int item(int li) const { return li < n_whole ? first + li * step : part_item; }
+  __device__ int units(int nkb) const { return n_whole * nkb + (kb_hi - kb_lo); }
+  // local unit f -> (local item, K block)
+  __device__ void locate(int f, int nkb, int& li, int& kb) const {
+    if (f < n_whole * nkb) {
+      li = f / nkb;
+      kb = f - li * nkb;
+    } else {
+      li = n_whole;
+      kb = kb_lo + (f - n_whole * nkb);
+    }
+  }
+};
+
+// Join of a tail item's parts; every thread calls it, at the part's last K block. Every
+// part stores its partial sums (agent-scope stores), waits until they are performed,
+// then takes an agent-scope ticket: the part drawing the last ticket knows every other
+// part's sums are in memory -- nobody waits for anybody -- adds the parts in part order
+// (a fixed order: the same bits whichever part draws the last ticket), returns true and
+// clears the ticket; the others return false. A(i) / SET(i, v): float i of the thread's
+// NF accumulators. (Flags polled by the last part instead cost ~20 us at 2048 tokens:
+// ~150 pollers on a few cache lines slow the very stores they wait for.)
+template <int NF, typename Get, typename Set>
+__device__ __forceinline__ bool gp_join(Get&& A, Set&& SET, const GpSched& sc, float* part, uint32_t* sync,
+                                        int* role_s) {
+  const int tid = threadIdx.x, nt = blockDim.x;
+  const int ti = sc.part_item - sc.tail0, p = sc.unit % sc.nparts, u0 = sc.unit - p;
+  uint32_t* tick = sync + 1 + ti;
+  {
+    unsigned long long* mine = (unsigned long long*)(part + (size_t)sc.unit * NF * nt) + tid;
+#pragma unroll
+    for (int c = 0; c < NF / 2; ++c) {
+      const unsigned long long v =
+          (unsigned long long)__float_as_uint(A(2 * c)) | ((unsigned long long)__float_as_uint(A(2 * c + 1)) << 32);
+      __hip_atomic_store(mine + c * nt, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");  // every thread's stores performed
+  if (tid == 0) *role_s = (int)__hip_atomic_fetch_add(tick, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  if (*role_s != sc.nparts - 1) return false;
+  float tot[NF];
+  for (int q = 0; q < sc.nparts; ++q) {
+    if (q == p) {
+#pragma unroll
+      for (int i = 0; i < NF; ++i) tot[i] = q == 0 ? A(i) : tot[i] + A(i);
+    } else {
+      const unsigned long long* src = (const unsigned long long*)(part + (size_t)(u0 + q) * NF * nt) + tid;
+#pragma unroll
+      for (int c = 0; c < NF / 2; ++c) {
+        const unsigned long long v = __hip_atomic_load(src + c * nt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const float lo = __uint_as_float((uint32_t)v), hi = __uint_as_float((uint32_t)(v >> 32));
+        tot[2 * c] = q == 0 ? lo : tot[2 * c] + lo;
+        tot[2 * c + 1] = q == 0 ? hi : tot[2 * c + 1] + hi;
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < NF; ++i) SET(i, tot[i]);
+  if (tid == 0) gp_st(tick, 0u);
+  return true;
+}
+
 // MODE 0: gate/up + SwiGLU (A = gathered x rows, B = gate/up rows of 64 neurons);
 // MODE 1: down (A = act rows, B = down_t rows of 128 hidden columns).
 template <int MODE>
@@ -385,23 +497,17 @@ __global__ __launch_bounds__(GM_THREADS, GP_WG_PER_CU) void gemm_v3_kernel(
   const int K = MODE == 0 ? H : G;
   const int nkb = K / GP_BK;
   const int n_items = meta[0] * n_ntile;
-  // this workgroup's items: it.first, it.first + it.step, ...; unit f = (local item
-  // f / nkb, K block f % nkb)
-  const GvItems it(n_items);
-  const int n_local_items = it.first < it.last ? (it.last - it.first + it.step - 1) / it.step : 0;
-  const int item0 = it.first, istep = it.step;
-  const int F = n_local_items * nkb;
+  const GpSched sc(n_items, nkb, false);  // whole items (a split costs this loop more than it saves)
+  const int n_local_items = sc.n_local();
+  const int F = sc.units(nkb);
   if (F <= 0) return;
-  auto locate = [&](int f, int& li, int& kb) {
-    li = f / nkb;
-    kb = f - li * nkb;
-  };
+  auto locate = [&](int f, int& li, int& kb) { sc.locate(f, nkb, li, kb); };
 
   // slot DMA of item li (wave 0): token ids and gates of the tile rows, row r >= rows
   // reading row rows - 1 (in range; padding rows are never stored)
   auto slot_dma = [&](int li) {
     if (MODE != 0 || w != 0) return;
-    const int item = item0 + li * istep;
+    const int item = sc.item(li);
     const int t = item / n_ntile;
     const int p0 = tiles[t * 4 + 1], rows = tiles[t * 4 + 2];
     unsigned char* sl = slots + (li & (GP_NSLOT - 1)) * GP_SLOT_BYTES;
@@ -416,7 +522,7 @@ __global__ __launch_bounds__(GM_THREADS, GP_WG_PER_CU) void gemm_v3_kernel(
   // issue cursor: row offsets of the item whose blocks are being issued
   int64_t aoff[GP_NI], boff[GP_NI];
   auto setup_item = [&](int li) {
-    const int item = item0 + li * istep;
+    const int item = sc.item(li);
     const int t = item / n_ntile, nt = item - t * n_ntile;
     const int e = tiles[t * 4 + 0], p0 = tiles[t * 4 + 1], rows = tiles[t * 4 + 2];
     const int32_t* tok = (const int32_t*)(slots + (li & (GP_NSLOT - 1)) * GP_SLOT_BYTES);
@@ -438,7 +544,7 @@ __global__ __launch_bounds__(GM_THREADS, GP_WG_PER_CU) void gemm_v3_kernel(
   auto issue = [&](int f) {
     int li, kb;
     locate(f < F ? f : F - 1, li, kb);  // past the end: the last block again, never read
-    if (f < F && kb == 0) {
+    if (f < F && (kb == 0 || f == sc.n_whole * nkb)) {  // an item's first block (a part's: kb_lo)
       setup_item(li);
       // item li+1's slot is read nkb blocks later; items 0 and 1 get theirs in the
       // prologue (the first item's blocks may all be in flight before its first wait)
@@ -507,7 +613,7 @@ __global__ __launch_bounds__(GM_THREADS, GP_WG_PER_CU) void gemm_v3_kernel(
     int li, kb;
     locate(f, li, kb);
     if (kb != nkb - 1) continue;
-    const int item = item0 + li * istep;
+    const int item = sc.item(li);
     // ---- epilogue of item li (lane laundered: its row indices are not worth registers
     // across the main loop)
     {
@@ -582,8 +688,9 @@ __global__ __launch_bounds__(GM_THREADS, 1) void gemm_s_kernel(
     const bf16_t* __restrict__ abase, int H, int G, const bf16_t* __restrict__ bbase,
     const int32_t* __restrict__ token_ids, const float* __restrict__ pair_gates,
     const int32_t* __restrict__ tiles, const int32_t* __restrict__ meta, bf16_t* __restrict__ act,
-    float* __restrict__ y) {
+    float* __restrict__ y, float* __restrict__ part, uint32_t* __restrict__ sync) {
   extern __shared__ __align__(16) unsigned char smem[];
+  __shared__ int role_s;
   unsigned char* slots = smem + GS_STAGES * GS_STAGE;
   float* xchg = (float*)(slots + GP_NSLOT * GS_SLOT_BYTES);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -591,20 +698,16 @@ __global__ __launch_bounds__(GM_THREADS, 1) void gemm_s_kernel(
   const int K = MODE == 0 ? H : G;
   const int nkb = K / GP_BK;
   const int n_items = meta[0] * n_ntile;
-  const GvItems it(n_items);
-  const int n_local_items = it.first < it.last ? (it.last - it.first + it.step - 1) / it.step : 0;
-  const int item0 = it.first, istep = it.step;
-  const int F = n_local_items * nkb;
+  const GpSched sc(n_items, nkb, MODE == 0 && part != nullptr);  // down items are too short to split
+  const int n_local_items = sc.n_local();
+  const int F = sc.units(nkb);
   if (F <= 0) return;
-  auto locate = [&](int f, int& li, int& kb) {
-    li = f / nkb;
-    kb = f - li * nkb;
-  };
+  auto locate = [&](int f, int& li, int& kb) { sc.locate(f, nkb, li, kb); };
   // slot of item li (wave 0, one 4-byte DMA per lane): token ids, then pair gates of the
   // tile rows, row r >= rows reading row rows - 1
   auto slot_dma = [&](int li) {
     if (MODE != 0 || w != 0) return;
-    const int item = item0 + li * istep;
+    const int item = sc.item(li);
     const int t = item / n_ntile;
     const int p0 = tiles[t * 4 + 1], rows = tiles[t * 4 + 2];
     const int r = min(lane & 31, rows - 1);
@@ -613,7 +716,7 @@ __global__ __launch_bounds__(GM_THREADS, 1) void gemm_s_kernel(
   };
   int64_t aoff, boff[4];
   auto setup_item = [&](int li) {
-    const int item = item0 + li * istep;
+    const int item = sc.item(li);
     const int t = item / n_ntile, nt = item - t * n_ntile;
     const int e = tiles[t * 4 + 0], p0 = tiles[t * 4 + 1], rows = tiles[t * 4 + 2];
     const int32_t* tok = (const int32_t*)(slots + (li & (GP_NSLOT - 1)) * GS_SLOT_BYTES);
@@ -637,7 +740,7 @@ __global__ __launch_bounds__(GM_THREADS, 1) void gemm_s_kernel(
   auto issue = [&](int f) {
     int li, kb;
     locate(f < F ? f : F - 1, li, kb);  // past the end: the last block again, never read
-    if (f < F && kb == 0) {
+    if (f < F && (kb == 0 || f == sc.n_whole * nkb)) {  // an item's first block (a part's: kb_lo)
       setup_item(li);
       if (li >= 1 && li + 1 < n_local_items) slot_dma(li + 1);
     }
@@ -687,11 +790,17 @@ __global__ __launch_bounds__(GM_THREADS, 1) void gemm_s_kernel(
     }
     int li, kb;
     locate(f, li, kb);
-    if (kb != nkb - 1) continue;
+    if (kb != nkb - 1 && f != F - 1) continue;
+    if (MODE == 0 && li == sc.n_whole && sc.nparts > 1 &&
+        !gp_join<16>([&](int i) { return acc[i]; }, [&](int i, float v) { acc[i] = v; }, sc, part, sync, &role_s)) {
+#pragma unroll
+      for (int q = 0; q < 16; ++q) acc[q] = 0.0f;
+      continue;
+    }
     {
       int ln = lane;
       asm volatile("" : "+v"(ln));
-      const int item = item0 + li * istep;
+      const int item = sc.item(li);
       const int t = item / n_ntile, nt = item - t * n_ntile;
       const int p0 = tiles[t * 4 + 1], rows = tiles[t * 4 + 2];
       if (MODE == 0) {
@@ -797,20 +906,33 @@ static int gemm_grid_v3(int64_t items) {  // GP_WG_PER_CU workgroups per CU, a m
 static bool prefill_short_tiles(int64_t N, int H, int G) {
   return N <= GS_MAX_N && G % 64 == 0 && H / GP_BK >= GS_STAGES - 1;
 }
-static int gemm_s_grid(int64_t items) {  // one workgroup per CU, a multiple of 8 (XCD order)
-  int64_t g = pp_device_cus();
-  if (items < g) g = items;
-  g = (g + 7) / 8 * 8;
-  return (int)(g < 8 ? 8 : g);
+static int gemm_s_grid() {  // one workgroup per CU, a multiple of 8 (XCD order); spare ones take item parts
+  const int g = (pp_device_cus() + 7) / 8 * 8;
+  return g < 8 ? 8 : g;
+}
+
+// Split workspace of the short-tile GEMMs (layout at GpSched): sync words, then one
+// slot of 16 floats per thread (a workgroup's accumulators) per workgroup of their grid.
+static int64_t gemm_split_slots() { return gemm_s_grid(); }
+static size_t gemm_sync_bytes() { return (size_t)((1 + gemm_split_slots()) * 4 + 255) / 256 * 256; }
+static size_t gemm_split_bytes() {
+  return gemm_sync_bytes() + (size_t)gemm_split_slots() * 16 * GM_THREADS * sizeof(float);
+}
+static void gemm_split_ptrs(void* gws, uint32_t** sync, float** part) {
+  *sync = gws ? (uint32_t*)gws : nullptr;
+  *part = gws ? (float*)((char*)gws + gemm_sync_bytes()) : nullptr;
 }
 
 static int gateup_launch(const bf16_t* xb, int H, int G, const bf16_t* wrows, int E, const int32_t* token_ids,
                          const float* pair_gates, const int32_t* tiles, const int32_t* meta, int64_t max_tiles,
-                         bf16_t* act, hipStream_t st, bool short_tiles = false) {
+                         bf16_t* act, void* gws, hipStream_t st, bool short_tiles = false) {
   (void)E;
+  uint32_t* sync;
+  float* part;
+  gemm_split_ptrs(gws, &sync, &part);
   if (short_tiles) {
-    gemm_s_kernel<0><<<gemm_s_grid(max_tiles * (G / 64)), GM_THREADS, GS_LDS_BYTES, st>>>(
-        xb, H, G, wrows, token_ids, pair_gates, tiles, meta, act, nullptr);
+    gemm_s_kernel<0><<<gemm_s_grid(), GM_THREADS, GS_LDS_BYTES, st>>>(xb, H, G, wrows, token_ids, pair_gates, tiles,
+                                                                      meta, act, nullptr, part, sync);
   } else if (G % 64 == 0) {
     int grid = gemm_grid_v3(max_tiles * (G / 64));
     gemm_v3_kernel<0><<<grid, GM_THREADS, GP_LDS_BYTES, st>>>(xb, H, G, wrows, token_ids, pair_gates, tiles, meta,
@@ -823,10 +945,14 @@ static int gateup_launch(const bf16_t* xb, int H, int G, const bf16_t* wrows, in
 }
 
 static int down_launch(const bf16_t* act, int H, int G, const bf16_t* down_t, const int32_t* tiles,
-                       const int32_t* meta, int64_t max_tiles, float* y, hipStream_t st, bool short_tiles = false) {
+                       const int32_t* meta, int64_t max_tiles, float* y, void* gws, hipStream_t st,
+                       bool short_tiles = false) {
+  uint32_t* sync;
+  float* part;
+  gemm_split_ptrs(gws, &sync, &part);
   if (short_tiles) {
-    gemm_s_kernel<1><<<gemm_s_grid(max_tiles * (H / 128)), GM_THREADS, GS_LDS_BYTES, st>>>(
-        act, H, G, down_t, nullptr, nullptr, tiles, meta, nullptr, y);
+    gemm_s_kernel<1><<<gemm_s_grid(), GM_THREADS, GS_LDS_BYTES, st>>>(act, H, G, down_t, nullptr, nullptr, tiles,
+                                                                      meta, nullptr, y, part, sync);
   } else if (G % 64 == 0) {
     int grid = gemm_grid_v3(max_tiles * (H / 128));
     gemm_v3_kernel<1><<<grid, GM_THREADS, GP_LDS_BYTES, st>>>(act, H, G, down_t, nullptr, nullptr, tiles, meta,
@@ -858,7 +984,7 @@ extern "C" int pp_expert_gateup(const void* x_bf16, int H, int G, const void* pa
   PP_REQUIRE(max_tiles >= 0, PP_ERR_INVALID, "pp_expert_gateup: max_tiles < 0");
   if (max_tiles == 0) return PP_OK;
   return gateup_launch((const bf16_t*)x_bf16, H, G, (const bf16_t*)packed, E, token_ids, pair_gates, tiles, meta,
-                       max_tiles, (bf16_t*)act_bf16, (hipStream_t)stream);
+                       max_tiles, (bf16_t*)act_bf16, nullptr, (hipStream_t)stream);
 }
 
 extern "C" int pp_expert_down(const void* act_bf16, int H, int G, const void* packed, int E, const int32_t* tiles,
@@ -869,7 +995,7 @@ extern "C" int pp_expert_down(const void* act_bf16, int H, int G, const void* pa
   PP_REQUIRE(max_tiles >= 0, PP_ERR_INVALID, "pp_expert_down: max_tiles < 0");
   if (max_tiles == 0) return PP_OK;
   const bf16_t* down_t = (const bf16_t*)packed + (int64_t)E * G * 3 * H;
-  return down_launch((const bf16_t*)act_bf16, H, G, down_t, tiles, meta, max_tiles, (float*)y_f32,
+  return down_launch((const bf16_t*)act_bf16, H, G, down_t, tiles, meta, max_tiles, (float*)y_f32, nullptr,
                      (hipStream_t)stream);
 }
 
@@ -889,15 +1015,16 @@ int pp_route_impl(const void* x, int x_dtype, const float* logits_in, int64_t N,
                   uint8_t* mask_out, int32_t* count_out, bf16_t* xbf_out, hipStream_t st, int32_t* blkcnt_out);
 int pp_bucket_from_counts(const uint8_t* mask, const float* gates, int64_t N, int E, int tile_m,
                           const int32_t* blkcnt, int cb, int32_t* offsets, int32_t* token_ids, float* pair_gates,
-                          int32_t* token_pairs, int32_t* tiles, int32_t* meta, hipStream_t st);
+                          int32_t* token_pairs, int32_t* tiles, int32_t* meta, hipStream_t st, uint32_t* zero,
+                          int nzero);
 bool pp_bucket_counts16_fit(int64_t N, int E);
 int pp_bucket_impl(const uint8_t* mask, const float* gates, int64_t N, int E, int tile_m, int32_t* offsets,
                    int32_t* token_ids, float* pair_gates, int32_t* token_pairs, int32_t* tiles, int32_t* meta,
-                   void* workspace, hipStream_t st);
+                   void* workspace, hipStream_t st, uint32_t* zero, int nzero);
 
 struct PrefillWs {
   size_t gates, mask, count, offsets, token_ids, pair_gates, token_pairs, tiles, meta, bws, blk16, xbf, act, y,
-      total;
+      gws, total;
 };
 
 static PrefillWs prefill_layout(int64_t N, int H, int E, int G) {
@@ -924,6 +1051,7 @@ static PrefillWs prefill_layout(int64_t N, int H, int E, int G) {
   L.xbf = take((size_t)N * H * 2);
   L.act = take((size_t)P * G * 2);
   L.y = take((size_t)P * H * 4);
+  L.gws = prefill_short_tiles(N, H, G) ? take(gemm_split_bytes()) : 0;
   L.total = o;
   return L;
 }
@@ -961,6 +1089,9 @@ extern "C" int pp_moe_prefill(const void* x, int x_dtype, int64_t n_tokens, int 
   const bool short_tiles = prefill_short_tiles(n_tokens, H, G);
   const int tile_m = short_tiles ? GS_TM : GM_BM;
   const int64_t mt = pp_max_tiles(n_tokens, E, tile_m);
+  // the GEMMs' split workspace: its sync words are cleared by this call's bucketing kernel
+  void* gws = short_tiles ? (void*)(ws + L.gws) : nullptr;
+  const int nzero = gws ? (int)(1 + gemm_split_slots()) : 0;
   // E = 16: the router kernel also counts selections per 16-token block, and the
   // bucketing is one kernel from those counts (no counting or scan pass)
   int32_t* blk16 = (E == 16 && pp_bucket_counts16_fit(n_tokens, E)) ? (int32_t*)(ws + L.blk16) : nullptr;
@@ -969,15 +1100,15 @@ extern "C" int pp_moe_prefill(const void* x, int x_dtype, int64_t n_tokens, int 
     return rc;
   if (blk16)
     rc = pp_bucket_from_counts(mask, gates, n_tokens, E, tile_m, blk16, 16, offsets, token_ids, pair_gates,
-                               token_pairs, tiles, meta, st);
+                               token_pairs, tiles, meta, st, (uint32_t*)gws, nzero);
   else
     rc = pp_bucket_impl(mask, gates, n_tokens, E, tile_m, offsets, token_ids, pair_gates, token_pairs, tiles, meta,
-                        ws + L.bws, st);
+                        ws + L.bws, st, (uint32_t*)gws, nzero);
   if (rc) return rc;
-  if ((rc = gateup_launch(xbf, H, G, (const bf16_t*)packed, E, token_ids, pair_gates, tiles, meta, mt, act, st,
-                          short_tiles)))
+  if ((rc = gateup_launch(xbf, H, G, (const bf16_t*)packed, E, token_ids, pair_gates, tiles, meta, mt, act, gws,
+                          st, short_tiles)))
     return rc;
   const bf16_t* down_t = (const bf16_t*)packed + (int64_t)E * G * 3 * H;
-  if ((rc = down_launch(act, H, G, down_t, tiles, meta, mt, y, st, short_tiles))) return rc;
+  if ((rc = down_launch(act, H, G, down_t, tiles, meta, mt, y, gws, st, short_tiles))) return rc;
   return combine_launch(y, token_pairs, count, n_tokens, H, E, (bf16_t*)out_bf16, st);
 }

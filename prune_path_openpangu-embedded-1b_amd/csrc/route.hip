@@ -545,8 +545,10 @@ __global__ __launch_bounds__(256) void bucket_scan_kernel(const int32_t* __restr
                                                           int E, int tile_m, int32_t* __restrict__ blkoff,
                                                           int32_t* __restrict__ offsets,
                                                           int32_t* __restrict__ tiles,
-                                                          int32_t* __restrict__ meta) {
+                                                          int32_t* __restrict__ meta,
+                                                          uint32_t* __restrict__ zero, int nzero) {
   __shared__ int off_s[PP_MAX_EXPERTS + 1];
+  for (int i = threadIdx.x; i < nzero; i += 256) zero[i] = 0u;
   __shared__ int toff_s[PP_MAX_EXPERTS + 1];
   __shared__ int cnt_s[BKT_SCAN_CHUNK];
   const int e = threadIdx.x;
@@ -686,7 +688,7 @@ __global__ __launch_bounds__(BKT_THREADS) void bucket_place_kernel(
     const uint8_t* __restrict__ mask, const float* __restrict__ gates, int64_t N, int E,
     const int32_t* __restrict__ blkcnt, int cb, int nblk_c, int tile_m, int32_t* __restrict__ offsets,
     int32_t* __restrict__ token_ids, float* __restrict__ pair_gates, int32_t* __restrict__ token_pairs,
-    int32_t* __restrict__ tiles, int32_t* __restrict__ meta) {
+    int32_t* __restrict__ tiles, int32_t* __restrict__ meta, uint32_t* __restrict__ zero, int nzero) {
   __shared__ int cnt_s[BKT_PLACE_INTS];
   __shared__ int part_tot[BKT_THREADS], part_pre[BKT_THREADS];
   __shared__ int base_s[PP_MAX_EXPERTS];
@@ -744,6 +746,7 @@ __global__ __launch_bounds__(BKT_THREADS) void bucket_place_kernel(
   bucket_expert_scan(tot, E, tile_m, off_s, toff_s);  // ends on a barrier
   if (tid < E) base_s[tid] = off_s[tid] + pre;
   if (blockIdx.x == 0) {
+    for (int i = tid; i < nzero; i += BKT_THREADS) zero[i] = 0u;
     for (int e = tid; e <= E; e += BKT_THREADS) offsets[e] = off_s[e];
     if (tid == 0) {
       meta[0] = toff_s[E];
@@ -772,6 +775,8 @@ extern "C" int64_t pp_max_tiles(int64_t n_tokens, int E, int tile_m) {
   return (n_tokens * E) / tile_m + E;
 }
 
+// zero[0 .. nzero) (may be null): words the caller needs cleared before its next kernel
+// (the prefill GEMMs' split sync words); workgroup 0 of the place / scan kernel clears them.
 // Bucketing from block counts already made (cb tokens per count block, cb | BKT_TOK):
 // one place kernel when the count table is small, else the scan + scatter pair (the
 // scatter needs BKT_TOK-token block bases, summed from the cb-token counts by the scan
@@ -780,25 +785,28 @@ static bool bucket_place_fits(int64_t nblk_c, int E) { return nblk_c * E <= BKT_
 
 int pp_bucket_from_counts(const uint8_t* mask, const float* gates, int64_t N, int E, int tile_m,
                           const int32_t* blkcnt, int cb, int32_t* offsets, int32_t* token_ids, float* pair_gates,
-                          int32_t* token_pairs, int32_t* tiles, int32_t* meta, hipStream_t st) {
+                          int32_t* token_pairs, int32_t* tiles, int32_t* meta, hipStream_t st, uint32_t* zero,
+                          int nzero) {
   const int64_t nblk_c = (N + cb - 1) / cb;
   const int64_t nblk = (N + BKT_TOK - 1) / BKT_TOK;
   bucket_place_kernel<<<(unsigned)(nblk > 0 ? nblk : 1), BKT_THREADS, 0, st>>>(
-      mask, gates, N, E, blkcnt, cb, (int)nblk_c, tile_m, offsets, token_ids, pair_gates, token_pairs, tiles, meta);
+      mask, gates, N, E, blkcnt, cb, (int)nblk_c, tile_m, offsets, token_ids, pair_gates, token_pairs, tiles, meta,
+      zero, zero ? nzero : 0);
   return pp_check_launch("pp_bucket");
 }
 
 int pp_bucket_impl(const uint8_t* mask, const float* gates, int64_t N, int E, int tile_m,
                    int32_t* offsets, int32_t* token_ids, float* pair_gates, int32_t* token_pairs,
-                   int32_t* tiles, int32_t* meta, void* workspace, hipStream_t st) {
+                   int32_t* tiles, int32_t* meta, void* workspace, hipStream_t st, uint32_t* zero, int nzero) {
   int64_t nblk = (N + BKT_TOK - 1) / BKT_TOK;
   int32_t* blkcnt = (int32_t*)workspace;
   int32_t* blkoff = blkcnt + (nblk < 1 ? 1 : nblk) * E;
   if (nblk > 0) bucket_count_kernel<<<(unsigned)nblk, BKT_THREADS, 0, st>>>(mask, N, E, blkcnt);
   if (bucket_place_fits(nblk, E))
     return pp_bucket_from_counts(mask, gates, N, E, tile_m, blkcnt, BKT_TOK, offsets, token_ids, pair_gates,
-                                 token_pairs, tiles, meta, st);
-  bucket_scan_kernel<<<1, 256, 0, st>>>(blkcnt, (int)nblk, E, tile_m, blkoff, offsets, tiles, meta);
+                                 token_pairs, tiles, meta, st, zero, nzero);
+  bucket_scan_kernel<<<1, 256, 0, st>>>(blkcnt, (int)nblk, E, tile_m, blkoff, offsets, tiles, meta, zero,
+                                        zero ? nzero : 0);
   if (nblk > 0)
     bucket_scatter_kernel<<<(unsigned)nblk, BKT_THREADS, 0, st>>>(mask, gates, N, E, blkoff, token_ids, pair_gates,
                                                           token_pairs);
@@ -820,5 +828,5 @@ extern "C" int pp_bucket(const uint8_t* mask, const float* gates, int64_t n_toke
   PP_REQUIRE(((uintptr_t)mask & 3) == 0 && ((uintptr_t)gates & 3) == 0, PP_ERR_INVALID,
              "pp_bucket: mask must be 4-byte aligned (read as 32-bit words)");
   return pp_bucket_impl(mask, gates, n_tokens, E, tile_m, offsets, token_ids, pair_gates, token_pairs, tiles,
-                        meta, workspace, (hipStream_t)stream);
+                        meta, workspace, (hipStream_t)stream, nullptr, 0);
 }
