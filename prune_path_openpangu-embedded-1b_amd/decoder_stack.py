@@ -5,12 +5,16 @@ attention with 12 heads of 128 and a KV cache, RMSNorm, MoE-MLP), token embeddin
 LM head over a 153,376-word vocabulary, bf16. Prefill a prompt, then greedy decode;
 the MoE-MLP is ``IntegratedOpenPanguMoEMLP`` (eval path through the MI355X kernels,
 the module tree of src/openpangu_moe.py:43-130), mirroring the reference's manual
-decode benchmark (src/evaluation_triton.py:403-460). ``run`` reports the time per
-decode step, the prefill time and the MoE-MLP share of both, measured with events on
-the current stream around each MoE-MLP call.
+decode benchmark (src/evaluation_triton.py:403-460). ``run`` reports the prefill time
+(eager, events around each MoE-MLP call) and the decode step: one whole greedy step
+(26 layers, LM head, argmax, next position) captured in a HIP graph with static shapes
+-- the KV cache at its full length, the position a device tensor, a causal mask over
+the cache -- replayed ``steps`` times, once with and once without the MoE-MLP, so the
+MoE share is device time rather than host dispatch.
 
-Attention is plain torch with contiguous right operands (no transposed views in
-batched bf16 products); it is harness, not part of the hot path.
+Attention is plain torch with contiguous right operands (the K cache is kept
+transposed, so no transposed view enters a batched bf16 product); it is harness, not
+part of the hot path.
 """
 from __future__ import annotations
 
@@ -56,24 +60,25 @@ class Attention(nn.Module):
         self.qkv = nn.Linear(d, 3 * d, bias=False)
         self.o = nn.Linear(d, d, bias=False)
         self.max_len = max_len
-        self.k_cache = None
-        self.v_cache = None
+        self.kt_cache = None  # [B, h, hd, max_len]: K kept transposed
+        self.v_cache = None   # [B, h, max_len, hd]
         self.len = 0
 
     def reset(self, B: int, device, dtype):
-        self.k_cache = torch.zeros(B, self.h, self.max_len, self.hd, device=device, dtype=dtype)
+        self.kt_cache = torch.zeros(B, self.h, self.hd, self.max_len, device=device, dtype=dtype)
         self.v_cache = torch.zeros(B, self.h, self.max_len, self.hd, device=device, dtype=dtype)
         self.len = 0
 
     def forward(self, x):
+        """Eager: L new tokens at host position ``self.len``."""
         B, L, D = x.shape
         q, k, v = self.qkv(x).view(B, L, 3, self.h, self.hd).permute(2, 0, 3, 1, 4)  # [B, h, L, hd] each
         pos = torch.arange(self.len, self.len + L, device=x.device)
         q, k = rope(q, pos), rope(k, pos)
-        self.k_cache[:, :, self.len:self.len + L] = k
+        self.kt_cache[:, :, :, self.len:self.len + L] = k.transpose(-1, -2)
         self.v_cache[:, :, self.len:self.len + L] = v
         T = self.len + L
-        kt = self.k_cache[:, :, :T].transpose(-1, -2).contiguous()     # [B, h, hd, T]
+        kt = self.kt_cache[:, :, :, :T].contiguous()                    # [B, h, hd, T]
         s = torch.matmul(q.contiguous(), kt).float() / math.sqrt(self.hd)  # [B, h, L, T]
         if L > 1:
             causal = torch.ones(L, T, device=x.device, dtype=torch.bool).tril(T - L)
@@ -81,6 +86,20 @@ class Attention(nn.Module):
         p = torch.softmax(s, -1).to(x.dtype)
         o = torch.matmul(p, self.v_cache[:, :, :T].contiguous())        # [B, h, L, hd]
         self.len = T
+        return self.o(o.transpose(1, 2).reshape(B, L, D))
+
+    def forward_static(self, x, pos_t, mask):
+        """One token at device position ``pos_t`` ([1] int64), attending over the whole
+        cache with ``mask`` ([max_len]: 0 up to pos_t, -inf after): static shapes, so a
+        step can be captured in a graph."""
+        B, L, D = x.shape
+        q, k, v = self.qkv(x).view(B, L, 3, self.h, self.hd).permute(2, 0, 3, 1, 4)  # [B, h, 1, hd]
+        q, k = rope(q, pos_t), rope(k, pos_t)
+        self.kt_cache.index_copy_(3, pos_t, k.transpose(-1, -2).contiguous())
+        self.v_cache.index_copy_(2, pos_t, v.contiguous())
+        s = torch.matmul(q.contiguous(), self.kt_cache).float() / math.sqrt(self.hd)  # [B, h, 1, max_len]
+        p = torch.softmax(s + mask, -1).to(x.dtype)
+        o = torch.matmul(p, self.v_cache)                                  # [B, h, 1, hd]
         return self.o(o.transpose(1, 2).reshape(B, L, D))
 
 
@@ -103,6 +122,13 @@ class Block(nn.Module):
         e1.record()
         self.moe_events.append((e0, e1))
         return x + m
+
+    def forward_static(self, x, pos_t, mask, moe: bool = True):
+        x = x + self.self_attn.forward_static(self.input_layernorm(x), pos_t, mask)
+        h = self.post_attention_layernorm(x)
+        # without the MoE-MLP the step keeps the norm and the residual add, so the
+        # difference of the two step times is the MoE-MLP call alone
+        return x + (self.mlp(h) if moe else h)
 
 
 class DecoderStack(nn.Module):
@@ -139,6 +165,18 @@ class DecoderStack(nn.Module):
         for blk in self.layers:
             x = blk(x)
         return self.lm_head(self.norm(x[:, -1:]))
+
+    def step_static(self, tok_t, pos_t, moe: bool = True):
+        """One greedy decode step on device state: token ``tok_t`` [1, 1] at position
+        ``pos_t`` [1]; writes the next token into ``tok_t`` and advances ``pos_t``."""
+        ar = torch.arange(self.layers[0].self_attn.max_len, device=tok_t.device)
+        mask = torch.where(ar <= pos_t, 0.0, float("-inf")).to(torch.float32)
+        x = self.embed_tokens(tok_t)
+        for blk in self.layers:
+            x = blk.forward_static(x, pos_t, mask, moe)
+        logits = self.lm_head(self.norm(x))
+        tok_t.copy_(logits.argmax(-1))
+        pos_t.add_(1)
 
 
 @torch.no_grad()
@@ -179,19 +217,57 @@ def run(prompt_len: int = 1024, steps: int = 128, layers: int = 26, tau: float =
     prefill_ms = s0.elapsed_time(s1)
     prefill_moe = moe_ms()
     nxt = logits.argmax(-1)
-    s0.record()
-    for _ in range(steps):
-        logits = model(nxt)
-        nxt = logits.argmax(-1)
-    s1.record()
-    torch.cuda.synchronize()
-    decode_ms = s0.elapsed_time(s1)
-    decode_moe = moe_ms()
+
+    checked = {}
+
+    def decode_ms(moe: bool) -> float:
+        """One captured greedy step replayed ``steps`` times from the prompt's end; the
+        first replays are checked token for token against eager steps from the same state."""
+        tok_t = nxt.clone().view(1, 1)
+        pos_t = torch.tensor([prompt_len], device=dev, dtype=torch.int64)
+        n_chk = min(3, steps)
+        eager = []
+        for _ in range(n_chk):
+            model.step_static(tok_t, pos_t, moe)
+            eager.append(int(tok_t.item()))
+        pos_t.fill_(prompt_len)
+        tok_t.copy_(nxt.view(1, 1))
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):  # warm-up outside the graph (allocator, kernels)
+            for _ in range(2):
+                model.step_static(tok_t, pos_t, moe)
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            model.step_static(tok_t, pos_t, moe)
+        pos_t.fill_(prompt_len)
+        tok_t.copy_(nxt.view(1, 1))
+        replayed = []
+        for _ in range(n_chk):
+            graph.replay()
+            replayed.append(int(tok_t.item()))
+        checked[moe] = replayed == eager
+        pos_t.fill_(prompt_len)
+        tok_t.copy_(nxt.view(1, 1))
+        s0.record()
+        for _ in range(steps):
+            graph.replay()
+        s1.record()
+        torch.cuda.synchronize()
+        return s0.elapsed_time(s1) / steps
+
+    decode_step = decode_ms(True)
+    decode_step_no_moe = decode_ms(False)
+    decode_moe = max(decode_step - decode_step_no_moe, 0.0)
     return {
         "layers": layers, "prompt": prompt_len, "steps": steps, "tau": tau,
         "prefill_ms": prefill_ms, "prefill_moe_ms": prefill_moe, "prefill_moe_share": prefill_moe / prefill_ms,
-        "decode_ms_per_step": decode_ms / steps, "decode_moe_ms_per_step": decode_moe / steps,
-        "decode_moe_share": decode_moe / decode_ms,
-        "decode_moe_us_per_layer": decode_moe / steps / layers * 1000.0,
-        "note": "random-init bf16 weights, random prompt ids; events around each MoE-MLP call on the stream",
+        "decode_ms_per_step": decode_step, "decode_ms_per_step_without_moe": decode_step_no_moe,
+        "decode_moe_ms_per_step": decode_moe, "decode_moe_share": decode_moe / decode_step,
+        "decode_moe_us_per_layer": decode_moe / layers * 1000.0,
+        "graph_replays_match_eager": bool(checked.get(True)) and bool(checked.get(False)),
+        "note": ("random-init bf16 weights, random prompt ids; prefill: events around each MoE-MLP call; "
+                 "decode: one graph-captured greedy step (static-shape attention over the full cache) "
+                 "replayed, MoE share = step time with minus without the MoE-MLP"),
     }
