@@ -52,6 +52,8 @@ def parse():
     ap.add_argument("--tau", type=float, default=0.70)
     ap.add_argument("--prefill-tokens", type=int, default=2048)
     ap.add_argument("--prefill-reps", type=int, default=20)
+    ap.add_argument("--prefill-zipf", action="store_true",
+                    help="prefill section with the config-3 router bias (log Zipf(1.2)), e.g. for profiling small batches")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
@@ -202,12 +204,13 @@ def main():
     if not args.no_prefill:
         N = args.prefill_tokens
         R = args.prefill_reps
+        pbias = torch.from_numpy(gi.zipf_bias(E)).to(dev) if args.prefill_zipf else None
         xp = torch.randn(R, N, H, device=dev, generator=g)
         wsp = torch.empty(ops.prefill_workspace_bytes(N, H, E, G), dtype=torch.uint8, device=dev)
         outp = torch.empty(N, H, dtype=torch.bfloat16, device=dev)
         for r in range(2):
             packed, rp, _ = layers[r % len(layers)]
-            ops.moe_prefill(xp[r], rp, None, E, G, args.tau, packed, workspace=wsp, out=outp)
+            ops.moe_prefill(xp[r], rp, pbias, E, G, args.tau, packed, workspace=wsp, out=outp)
         torch.cuda.synchronize()
         gp = torch.cuda.CUDAGraph()
         s = torch.cuda.Stream()
@@ -216,7 +219,7 @@ def main():
             with torch.cuda.graph(gp, stream=s):
                 for r in range(R):
                     packed, rp, _ = layers[r % len(layers)]
-                    ops.moe_prefill(xp[r], rp, None, E, G, args.tau, packed, workspace=wsp, out=outp)
+                    ops.moe_prefill(xp[r], rp, pbias, E, G, args.tau, packed, workspace=wsp, out=outp)
         torch.cuda.current_stream().wait_stream(s)
         gp.replay()
         torch.cuda.synchronize()
@@ -229,12 +232,12 @@ def main():
         P = 0
         for r in range(R):
             packed, rp, _ = layers[r % len(layers)]
-            P += int(ops.route(xp[r], rp, E, args.tau, want_logits=False)["count"].sum())
+            P += int(ops.route(xp[r], rp, E, args.tau, bias=pbias, want_logits=False)["count"].sum())
         P_mean = P / R
         # the two grouped GEMMs alone, graph-replayed on a fixed bucket layout
         packed, rp, _ = layers[0]
         xb = xp[0].to(torch.bfloat16)
-        rt = ops.route(xb, rp, E, args.tau, want_logits=False)
+        rt = ops.route(xb, rp, E, args.tau, bias=pbias, want_logits=False)
         bk = ops.bucket(rt["mask"], rt["gates"])
         P0 = int(rt["count"].sum())
         act = ops.expert_gateup(xb, packed, E, G, bk)
@@ -282,7 +285,8 @@ def main():
         fl_gu = 4.0 * P0 * H * G
         fl_dn = 2.0 * P0 * H * G
         prefill = {
-            "tokens": N, "tau": args.tau, "pairs_mean": P_mean, "ms_per_call": pf_ms,
+            "tokens": N, "tau": args.tau, "router_bias": "zipf(1.2)" if args.prefill_zipf else None,
+            "pairs_mean": P_mean, "ms_per_call": pf_ms,
             "tokens_per_s": N / (pf_ms * 1e-3),
             "gemm_flops": fl_gu + fl_dn,
             "gateup_us": gu_ms * 1e3, "down_us": dn_ms * 1e3,
