@@ -1017,7 +1017,8 @@ int pp_bucket_from_counts(const uint8_t* mask, const float* gates, int64_t N, in
                           const int32_t* blkcnt, int cb, int32_t* offsets, int32_t* token_ids, float* pair_gates,
                           int32_t* token_pairs, int32_t* tiles, int32_t* meta, hipStream_t st, uint32_t* zero,
                           int nzero);
-bool pp_bucket_counts16_fit(int64_t N, int E);
+bool pp_bucket_counts_fit(int64_t N, int E, int cb);
+int pp_route_count_block(int64_t N, int H, int E);
 int pp_bucket_impl(const uint8_t* mask, const float* gates, int64_t N, int E, int tile_m, int32_t* offsets,
                    int32_t* token_ids, float* pair_gates, int32_t* token_pairs, int32_t* tiles, int32_t* meta,
                    void* workspace, hipStream_t st, uint32_t* zero, int nzero);
@@ -1047,7 +1048,7 @@ static PrefillWs prefill_layout(int64_t N, int H, int E, int G) {
   L.tiles = take((size_t)mt * 16);
   L.meta = take(16);
   L.bws = take(pp_bucket_workspace_bytes(N, E));
-  L.blk16 = take((size_t)((N + 15) / 16) * 16 * 4);  // route16's per-16-token expert counts
+  L.blk16 = take((size_t)((N + 3) / 4) * 16 * 4);  // the E = 16 router's per-block expert counts (>= 4 tokens a block)
   L.xbf = take((size_t)N * H * 2);
   L.act = take((size_t)P * G * 2);
   L.y = take((size_t)P * H * 4);
@@ -1094,12 +1095,13 @@ extern "C" int pp_moe_prefill(const void* x, int x_dtype, int64_t n_tokens, int 
   const int nzero = gws ? (int)(1 + gemm_split_slots()) : 0;
   // E = 16: the router kernel also counts selections per 16-token block, and the
   // bucketing is one kernel from those counts (no counting or scan pass)
-  int32_t* blk16 = (E == 16 && pp_bucket_counts16_fit(n_tokens, E)) ? (int32_t*)(ws + L.blk16) : nullptr;
+  const int cb = pp_route_count_block(n_tokens, H, E);
+  int32_t* blk16 = pp_bucket_counts_fit(n_tokens, E, cb) ? (int32_t*)(ws + L.blk16) : nullptr;
   if ((rc = pp_route_impl(x, x_dtype, nullptr, n_tokens, H, router_packed, bias, E, tau, nullptr, nullptr, gates,
                           mask, count, x_dtype == PP_DTYPE_BF16 ? nullptr : xbf, st, blk16)))
     return rc;
   if (blk16)
-    rc = pp_bucket_from_counts(mask, gates, n_tokens, E, tile_m, blk16, 16, offsets, token_ids, pair_gates,
+    rc = pp_bucket_from_counts(mask, gates, n_tokens, E, tile_m, blk16, cb, offsets, token_ids, pair_gates,
                                token_pairs, tiles, meta, st, (uint32_t*)gws, nzero);
   else
     rc = pp_bucket_impl(mask, gates, n_tokens, E, tile_m, offsets, token_ids, pair_gates, token_pairs, tiles, meta,

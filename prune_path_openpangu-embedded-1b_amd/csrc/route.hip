@@ -361,8 +361,128 @@ __global__ __launch_bounds__(64 * RT16_WAVES) void route16_kernel(
   }
 }
 
-// blkcnt_out (E = 16 path only, else untouched): per 16-token block, per expert, the
-// number of selections -- the bucketing's block counts, so it needs no counting pass.
+// ---- few tokens (E = 16, N <= RT_FEW_MAX_N, H = 512 CPL with CPL <= 4). route16_kernel
+// runs such batches on one or four workgroups, each walking the whole K loop at one
+// CU's load rate (~10 us at 16 tokens). Here a workgroup takes RT_FEW_TOK tokens: it
+// reads the router once and x of its tokens straight into registers (8 waves; wave w
+// takes the K slice w of 8, lane (row, col) of 4 x 16 the experts row + 4 i and the
+// float4 chunks col + 16 c of the slice), rows add by DPP, the eight wave partials add
+// in wave order (fixed order: deterministic logits); wave 0 runs route16_select with
+// group g = token g. The counts go out per RT_FEW_TOK-token block.
+#define RT_FEW_TOK 4
+#define RT_FEW_MAX_N 64
+template <typename XT, int CPL>
+__global__ __launch_bounds__(512) void route16_few_kernel(
+    const XT* __restrict__ x, int64_t N, const float* __restrict__ router, const float* __restrict__ bias,
+    float tau, float* __restrict__ logits_out, float* __restrict__ probs_out, float* __restrict__ gates_out,
+    uint8_t* __restrict__ mask_out, int32_t* __restrict__ count_out, bf16_t* __restrict__ xbf_out,
+    int32_t* __restrict__ blkcnt_out) {
+  constexpr int H = 512 * CPL, NW = 8, T = RT_FEW_TOK;
+  __shared__ __align__(16) float part_s[T][16][NW];
+  __shared__ __align__(16) float lg_s[16][16];
+  __shared__ __align__(16) float ev_s[16][16];
+  __shared__ __align__(16) float srt_s[16][16];
+  __shared__ int cnt_s[16];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int64_t tok0 = (int64_t)blockIdx.x * T;
+  const int64_t tok_end = min(N, tok0 + T);
+  if (tid < 16) cnt_s[tid] = 0;
+  const int rw = lane >> 4, cl = lane & 15;
+  const int ch0 = 16 * CPL * wv + cl;  // float4 chunk of x / of a router row
+  float4 xv[T][CPL], wr[4][CPL];
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    const int64_t row = min(tok0 + t, N - 1);  // rows past N repeat row N - 1, never stored
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) xv[t][c] = load_x4<XT>(x, row * H + 4 * (ch0 + 16 * c));
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) wr[i][c] = *(const float4*)(router + (rw + 4 * i) * H + 4 * (ch0 + 16 * c));
+#pragma unroll
+  for (int t = 0; t < T; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float s = 0.0f;
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) {
+        s = __builtin_fmaf(xv[t][c].x, wr[i][c].x, s);
+        s = __builtin_fmaf(xv[t][c].y, wr[i][c].y, s);
+        s = __builtin_fmaf(xv[t][c].z, wr[i][c].z, s);
+        s = __builtin_fmaf(xv[t][c].w, wr[i][c].w, s);
+      }
+      s = row16_sum(s);
+      if (cl == 0) part_s[t][rw + 4 * i][wv] = s;
+    }
+  // x as bf16 for the grouped GEMMs (fp32 x only): lanes of row rw store token rw
+  // (static token index per store: a register array indexed by rw would go to scratch)
+  if (sizeof(XT) == 4 && xbf_out && tok0 + rw < N) {
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+      if (rw == t)
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+          const float4 v = xv[t][c];
+          uint2 pk;
+          pk.x = (uint32_t)f32_to_bf16(v.x) | ((uint32_t)f32_to_bf16(v.y) << 16);
+          pk.y = (uint32_t)f32_to_bf16(v.z) | ((uint32_t)f32_to_bf16(v.w) << 16);
+          *(uint2*)(xbf_out + (tok0 + t) * H + 4 * (ch0 + 16 * c)) = pk;
+        }
+  }
+  __syncthreads();
+  if (tid < 16 * T) {
+    const int t = tid >> 4, e = tid & 15;
+    const float4 p0 = *(const float4*)&part_s[t][e][0];
+    const float4 p1 = *(const float4*)&part_s[t][e][4];
+    float l = p0.x;
+    l = __fadd_rn(l, p0.y);
+    l = __fadd_rn(l, p0.z);
+    l = __fadd_rn(l, p0.w);
+    l = __fadd_rn(l, p1.x);
+    l = __fadd_rn(l, p1.y);
+    l = __fadd_rn(l, p1.z);
+    l = __fadd_rn(l, p1.w);
+    if (bias) l = __fadd_rn(l, bias[e]);
+    lg_s[t][e] = l;
+  }
+  __syncthreads();
+  if (wv == 0)
+    route16_select(lg_s, ev_s, srt_s, cnt_s, tok0, tok_end, tau, lane, 0, logits_out, probs_out, gates_out,
+                   mask_out, count_out);
+  if (blkcnt_out) {
+    __syncthreads();
+    if (tid < 16) blkcnt_out[(int64_t)blockIdx.x * 16 + tid] = cnt_s[tid];
+  }
+}
+
+// Tokens per count block of the E = 16 router kernels (0: the kernel writes no counts).
+static bool route_few_fits(int64_t N, int H) { return N <= RT_FEW_MAX_N && H % 512 == 0 && H <= 2048; }
+int pp_route_count_block(int64_t N, int H, int E) {
+  if (E != 16) return 0;
+  return route_few_fits(N, H) ? RT_FEW_TOK : 16;
+}
+
+template <typename XT>
+static void launch_route_few(const XT* x, int64_t N, int H, const float* router, const float* bias, float tau,
+                             float* logits_out, float* probs_out, float* gates_out, uint8_t* mask_out,
+                             int32_t* count_out, bf16_t* xbf_out, int32_t* blkcnt_out, hipStream_t st) {
+  const unsigned g = (unsigned)((N + RT_FEW_TOK - 1) / RT_FEW_TOK);
+#define PP_FEW(C)                                                                                               \
+  route16_few_kernel<XT, C><<<g, 512, 0, st>>>(x, N, router, bias, tau, logits_out, probs_out, gates_out,      \
+                                               mask_out, count_out, xbf_out, blkcnt_out)
+  switch (H / 512) {
+    case 1: PP_FEW(1); break;
+    case 2: PP_FEW(2); break;
+    case 3: PP_FEW(3); break;
+    default: PP_FEW(4); break;
+  }
+#undef PP_FEW
+}
+
+// blkcnt_out (E = 16 path only, else untouched): per block of pp_route_count_block
+// tokens, per expert, the number of selections -- the bucketing's block counts, so it
+// needs no counting pass.
 int pp_route_impl(const void* x, int x_dtype, const float* logits_in, int64_t N, int H,
                   const float* router, const float* bias, int E, float tau, float* logits_out,
                   float* probs_out, float* gates_out, uint8_t* mask_out, int32_t* count_out,
@@ -371,6 +491,15 @@ int pp_route_impl(const void* x, int x_dtype, const float* logits_in, int64_t N,
   const int grid = (int)((N + ROUTE_TOK - 1) / ROUTE_TOK);
   const size_t smem = 0;
   const int threads = 256;
+  if (!logits_in && E == 16 && route_few_fits(N, H)) {
+    if (x_dtype == PP_DTYPE_F32)
+      launch_route_few<float>((const float*)x, N, H, router, bias, tau, logits_out, probs_out, gates_out, mask_out,
+                              count_out, xbf_out, blkcnt_out, st);
+    else
+      launch_route_few<bf16_t>((const bf16_t*)x, N, H, router, bias, tau, logits_out, probs_out, gates_out,
+                               mask_out, count_out, xbf_out, blkcnt_out, st);
+    return pp_check_launch("route16_few_kernel");
+  }
   if (!logits_in && E == 16) {
     const int g16 = (int)((N + 15) / 16);
     if (x_dtype == PP_DTYPE_F32)
@@ -813,8 +942,8 @@ int pp_bucket_impl(const uint8_t* mask, const float* gates, int64_t N, int E, in
   return pp_check_launch("pp_bucket");
 }
 
-// Whether pp_bucket_from_counts can take route16's 16-token counts for N tokens.
-bool pp_bucket_counts16_fit(int64_t N, int E) { return bucket_place_fits((N + 15) / 16, E); }
+// Whether pp_bucket_from_counts can take the router kernel's cb-token counts for N tokens.
+bool pp_bucket_counts_fit(int64_t N, int E, int cb) { return cb > 0 && bucket_place_fits((N + cb - 1) / cb, E); }
 
 extern "C" int pp_bucket(const uint8_t* mask, const float* gates, int64_t n_tokens, int E, int tile_m,
                          int32_t* offsets, int32_t* token_ids, float* pair_gates, int32_t* token_pairs,
