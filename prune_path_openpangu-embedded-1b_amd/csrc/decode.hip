@@ -584,20 +584,26 @@ __global__ __launch_bounds__(64 * NW) void decode16_kernel(
   }
   const float m = row16_max(xl);
 
-  // ---- speculative top expert. Rank 0 is always selected and is the expert with the
-  // largest logit unless probabilities tie (then the lowest index among equal p), so
-  // while wave 0 runs the selection, waves 1..7 start loading this workgroup's share of
-  // the records of e1 = the lowest index with the largest logit (at most one record per
-  // wave: G <= 7 W). After the selection barrier they are used if e1 was selected (then
-  // the main stream skips e1) and dropped otherwise; either way every selected record is
-  // used exactly once. No speculation for non-finite or NaN logits.
-  // (wave 0 evaluates e1 after its rank step, off its critical path)
-  auto top_expert = [&]() -> int {
+  // ---- speculative top experts. Rank 0 is always selected and is the expert with the
+  // largest logit unless probabilities tie (then the lowest index among equal p); rank 1
+  // usually is too. So while wave 0 runs the selection, waves 1..7 start loading this
+  // workgroup's share of the records of e1 = the lowest index with the largest logit and,
+  // when two shares fit (G <= 3 W), of e2 = the lowest index with the largest logit
+  // among the rest -- one record per wave, e1's share on the first waves. After the
+  // selection barrier a speculative record is used if its expert was selected (then the
+  // main stream skips that expert) and dropped otherwise; either way every selected
+  // record is used exactly once. No speculation for non-finite or NaN logits.
+  // (wave 0 evaluates e1, e2 after its rank step, off its critical path)
+  auto top_experts = [&](int& t1, int& t2) {
+    t1 = t2 = -1;
     const bool finite = __all(xl == xl) && __fsub_rn(m, m) == 0.0f;
-    if (!(DEC16_SPEC(CPL) && finite && G <= 7 * W)) return -1;
-    return __builtin_amdgcn_readfirstlane(row16_min_i(xl == m ? j : 16));
+    if (!(DEC16_SPEC(CPL) && finite && G <= 7 * W)) return;
+    t1 = __builtin_amdgcn_readfirstlane(row16_min_i(xl == m ? j : 16));
+    if (G > 3 * W) return;
+    const float m2 = row16_max(j != t1 ? xl : -__builtin_inff());
+    t2 = __builtin_amdgcn_readfirstlane(row16_min_i((j != t1 && xl == m2) ? j : 16));
   };
-  int e1 = -1;
+  int e1 = -1, e2 = -1;
   // ---- selection (wave 0), same arithmetic as select_small. Lane (g, j) = 16 g + j
   // serves expert j; the critical path is short dependent chains, so the four 16-lane
   // groups split the work instead of repeating it:
@@ -648,34 +654,47 @@ __global__ __launch_bounds__(64 * NW) void decode16_kernel(
       sel = rank < k;
     }
     // full selection in rank order (telemetry), and the main stream's list: the same
-    // without e1 when e1 was selected (its records come from the speculative loads)
-    e1 = top_expert();
-    const bool e1_sel = e1 >= 0 && ((__ballot(sel) >> e1) & 1ull);
+    // without e1 / e2 when selected (their records come from the speculative loads)
+    top_experts(e1, e2);
+    const unsigned long long selm = __ballot(sel);
+    const bool e1_sel = e1 >= 0 && ((selm >> e1) & 1ull);
+    const bool e2_sel = e2 >= 0 && ((selm >> e2) & 1ull);
     const int rank_e1 = e1 >= 0 ? __builtin_amdgcn_readlane(rank, e1) : 0;
+    const int rank_e2 = e2 >= 0 ? __builtin_amdgcn_readlane(rank, e2) : 0;
     if (lane < 16 && sel) {
       sel_ids_s[rank] = j;
       sel_g_s[rank] = pg_s[16 + j];
-      if (!(e1_sel && j == e1)) {
-        const int mi = rank - ((e1_sel && rank > rank_e1) ? 1 : 0);
+      if (!(e1_sel && j == e1) && !(e2_sel && j == e2)) {
+        const int mi = rank - ((e1_sel && rank > rank_e1) ? 1 : 0) - ((e2_sel && rank > rank_e2) ? 1 : 0);
         main_ids_s[mi] = j;
         main_g_s[mi] = pg_s[16 + j];
       }
     }
     if (lane == 0) {
       k_s = k;
-      kmain_s = k - (e1_sel ? 1 : 0);
-      spec_s = e1_sel ? 1 : 0;
+      kmain_s = k - (e1_sel ? 1 : 0) - (e2_sel ? 1 : 0);
+      spec_s = (e1_sel ? 1 : 0) | (e2_sel ? 2 : 0);
     }
   }
-  int s0 = 0, s1 = 0;
+  // wave wv >= 1 loads speculative record wv - 1 of this workgroup's shares: e1's share
+  // [s0, s1) first, then e2's
+  int s0 = 0, s1 = 0, es = -1, ebit = 0, rs = 0;
   if (wv != 0) {
-    e1 = top_expert();
-    if (e1 >= 0) pp_split((uint32_t)G, (uint32_t)W, (uint32_t)b, s0, s1);
+    top_experts(e1, e2);
+    if (e1 >= 0) {
+      pp_split((uint32_t)G, (uint32_t)W, (uint32_t)b, s0, s1);
+      const int q = wv - 1, nsh = s1 - s0;
+      if (q < nsh) {
+        es = e1, ebit = 1, rs = s0 + q;
+      } else if (e2 >= 0 && q < 2 * nsh) {
+        es = e2, ebit = 2, rs = s0 + q - nsh;
+      }
+    }
   }
-  const bool have_spec = wv >= 1 && e1 >= 0 && s0 + wv - 1 < s1;
+  const bool have_spec = es >= 0;
   uint4 sg[CPL], su[CPL], sd[CPL];
   if (have_spec) {
-    const uint4* rec = (const uint4*)(rows + ((int64_t)e1 * G + s0 + wv - 1) * 3 * H);
+    const uint4* rec = (const uint4*)(rows + ((int64_t)es * G + rs) * 3 * H);
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
       sg[c] = rec[lane + 64 * c];
@@ -737,8 +756,8 @@ __global__ __launch_bounds__(64 * NW) void decode16_kernel(
       dq[c] = rec[2 * HC + lane + 64 * c];
     }
   }
-  // the speculative record (loaded before the selection) with e1's gate
-  if (have_spec && spec_used) process(sg, su, sd, pg_s[16 + e1]);
+  // the speculative record (loaded before the selection) with its expert's gate
+  if (have_spec && (spec_s & ebit)) process(sg, su, sd, pg_s[16 + es]);
   for (; r < r_end; ++r) {
     uint4 g2[CPL], u2[CPL], d2[CPL];
 #pragma unroll
