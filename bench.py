@@ -377,6 +377,42 @@ def main():
         extra["e192_g32_decode"] = {"us_per_layer": us, "k_mean": k2, "hbm_gbs": byt / (us * 1e-6) / 1e9,
                                     "weight_sets": NS}
         del l192
+        # masked training path: the expert gating of MoELayer.forward and its backward on
+        # a training batch of 16 x 1024 tokens, bf16 activations [16384, 6144] (200 MB per
+        # tensor, beyond the MALL); bytes = activations read + written (+ gates)
+        torch.cuda.empty_cache()
+        Nt = 16384
+        ids = torch.randperm(I, device=dev, generator=g) % E
+        lay = ops.masked_gate_layout(ids, E)
+        inter = torch.randn(Nt, I, device=dev, generator=g).to(torch.bfloat16)
+        d_o = torch.randn(Nt, I, device=dev, generator=g).to(torch.bfloat16)
+        gts = torch.rand(Nt, E, device=dev, generator=g)
+        mg = {}
+        for name, fn, byt in (
+                ("fwd", lambda: ops.masked_gate_fwd(inter, gts, lay[0]), 2 * Nt * I * 2 + Nt * E * 4),
+                ("bwd", lambda: ops.masked_gate_bwd(d_o, inter, gts, *lay), 3 * Nt * I * 2 + 2 * Nt * E * 4)):
+            fn()
+            torch.cuda.synchronize()
+            R = 10
+            gm = torch.cuda.CUDAGraph()
+            sm = torch.cuda.Stream()
+            sm.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(sm):
+                with torch.cuda.graph(gm, stream=sm):
+                    for _ in range(R):
+                        fn()
+            torch.cuda.current_stream().wait_stream(sm)
+            gm.replay()
+            torch.cuda.synchronize()
+            e0.record()
+            gm.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) * 1000.0 / R
+            mg[name] = {"us": us, "hbm_gbs": byt / (us * 1e-6) / 1e9, "frac": byt / (us * 1e-6) / 1e9 / PEAK_HBM_GBS}
+            del gm
+        extra["masked_gate_train"] = {"rows": Nt, "intermediate": I, "experts": E, "dtype": "bf16", **mg}
+        del inter, d_o, gts
         # config 5: 26-layer decoder-shaped stack, 1024-token prompt + 128 greedy steps
         torch.cuda.empty_cache()
         extra["decoder_stack"] = pkg.decoder_stack.run(prompt_len=1024, steps=128, layers=26, tau=args.tau)

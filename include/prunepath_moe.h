@@ -174,6 +174,28 @@ int pp_expert_down(const void* act_bf16, int H, int G, const void* packed, int E
 int pp_combine(const float* y_f32, const int32_t* token_pairs, const int32_t* count,
                int64_t n_tokens, int H, int E, void* out_bf16, void* stream);
 
+/* ------------------------------------------------------------------------- *
+ * Masked training path: the expert gating of MoELayer.forward
+ * (src/MoEBlock_origin.py:205-212: self_moe_mask = experts_prob @ experts_masks;
+ * intermediate * self_moe_mask) and its backward, for the dense masked MLP that
+ * IntegratedOpenPanguMoEMLP trains (src/openpangu_moe_origin.py:83-120).
+ *   forward:  out[n,d] = inter[n,d] * gates[n, expert_ids[d]]
+ *   backward: d_inter[n,d] = d_out[n,d] * gates[n, expert_ids[d]] (d_inter may be NULL);
+ *             d_gates[n,e] = sum of d_out[n,d] * inter[n,d] over the neurons d of expert e
+ *             (fp32, fixed order: repeated calls give the same bits).
+ * inter / out / d_out / d_inter are [n_rows, I] fp32 or bf16 (dtype), 16-byte aligned;
+ * gates / d_gates fp32 [n_rows, E]; expert_ids int32 [I] (16-byte aligned, values in
+ * [0, E)); perm int32 [I]: the neurons sorted by expert id (stable), seg int32 [E+1]:
+ * expert e owns perm[seg[e] .. seg[e+1]). bf16 activations: the gate is rounded to
+ * bf16 before the multiply and the product to bf16 (the all-bf16 reference).
+ * Supported: 1 <= E <= 256, I % 8 == 0, 8 <= I <= 16384. out may alias inter.
+ * ------------------------------------------------------------------------- */
+int pp_masked_gate_fwd(const void* inter, int dtype, const float* gates, const int32_t* expert_ids,
+                       int64_t n_rows, int I, int E, void* out, void* stream);
+int pp_masked_gate_bwd(const void* d_out, const void* inter, int dtype, const float* gates,
+                       const int32_t* expert_ids, const int32_t* perm, const int32_t* seg, int64_t n_rows,
+                       int I, int E, void* d_inter, float* d_gates, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

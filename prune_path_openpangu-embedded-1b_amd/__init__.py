@@ -11,8 +11,8 @@ from ._lib import build
 from . import ops
 from .tau_sparse_moe import TauSparseMoE
 from .model import (IntegratedOpenPanguMoEMLP, MoELayer, experts_masks_from_ids, load_cluster_ids,
-                    physical_reorder_for_inference)
+                    penalty_losses, physical_reorder_for_inference)
 from . import decoder_stack
 
 __all__ = ["TauSparseMoE", "IntegratedOpenPanguMoEMLP", "MoELayer", "experts_masks_from_ids", "load_cluster_ids",
-           "physical_reorder_for_inference", "decoder_stack", "ops", "build", "_lib"]
+           "penalty_losses", "physical_reorder_for_inference", "decoder_stack", "ops", "build", "_lib"]

@@ -1,4 +1,5 @@
-"""Model-side drop-in for the openPangu MoE MLP, eval path.
+"""Model-side drop-in for the openPangu MoE MLP: the eval path on the sparse kernels and
+the masked training path.
 
 Mirrors the module tree the reference builds around its kernels, so reference
 checkpoints and model code line up key for key:
@@ -14,9 +15,13 @@ checkpoints and model code line up key for key:
 * ``load_cluster_ids`` reads the reference's partition files
   (``Pangu_Clusters/layer_{i}_k{G}.txt``, written by ``np.savetxt`` as floats,
   src/openpangu_moe.py:188-209).
-
-The masked training forward (dense projections + ``MoELayer`` masking and its losses)
-is not part of this build: ``forward`` in training mode raises.
+* Training (``IntegratedOpenPanguMoEMLP.train()``, src/openpangu_moe_origin.py:83-120):
+  dense gate/up projections, ``MoELayer.forward`` (src/MoEBlock_origin.py:174-214) with
+  the tau selection of the routing kernel on the fp32 router scores and the expert
+  gating ``intermediate * (experts_prob @ experts_masks)`` as the masked-gate HIP
+  kernels (forward and backward), then the down projection; the softmax probabilities
+  go to ``penalize_logits_list`` for ``penalty_losses`` (entropy and load balance,
+  src/openpangu_moe_origin.py:236-261).
 """
 from __future__ import annotations
 
@@ -27,6 +32,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from . import ops
 from .tau_sparse_moe import TauSparseMoE
 
 
@@ -47,9 +53,9 @@ def experts_masks_from_ids(ids, num_experts: int, dtype=torch.float32) -> torch.
 
 
 class MoELayer(nn.Module):
-    """State of the reference's masked routing layer (src/MoEBlock.py:110-152): the
-    router projection and the expert partition, under the reference's names. Only
-    the state is kept; the masked forward belongs to the training path."""
+    """The reference's masked routing layer (src/MoEBlock_origin.py:110-214): the router
+    projection and the expert partition under the reference's names, and its forward
+    ``(hidden_states, intermediate) -> (intermediate * mask, probs | None)``."""
 
     def __init__(self, hidden_size: int, intermediate_size: int, experts: int, tau: float = 0.95,
                  experts_id=None):
@@ -73,12 +79,41 @@ class MoELayer(nn.Module):
         """Neuron -> expert id [I] (argmax over the one-hot masks, src/openpangu_moe.py:229-230)."""
         return torch.argmax(self.experts_masks.to(torch.int32), dim=0)
 
-    def forward(self, *args, **kwargs):
-        raise NotImplementedError("MoELayer: the masked training forward is not part of this build")
+    def _layout(self):
+        """Expert ids / expert-sorted order for the masked-gate kernels, rebuilt when
+        ``experts_masks`` changes (storage or in-place update)."""
+        key = (self.experts_masks.data_ptr(), self.experts_masks._version, self.experts_masks.device)
+        if getattr(self, "_layout_key", None) != key:
+            self._layout_cache = ops.masked_gate_layout(self.expert_ids(), self.experts)
+            self._layout_key = key
+        return self._layout_cache
+
+    def forward(self, hidden_states: torch.Tensor, intermediate: torch.Tensor):
+        """src/MoEBlock_origin.py:174-214. score = router(hidden_states); the tau
+        selection (softmax, descending sort, fp64-accumulated cumsum < tau, rank 0 always;
+        src/MoEBlock_origin.py:50-97) comes from the routing kernel on the fp32 scores --
+        bit-exact with the reference's torch ops given the same fp32 scores -- and
+        experts_prob = sigmoid(score) on the selected experts, 0 elsewhere (the gradient of
+        sigmoid(where(select, score, finfo.min))); the gating is the masked-gate kernel.
+        Training returns the softmax probabilities for the penalties, eval updates
+        ``activated_statistics``."""
+        score = self.mlp_router(hidden_states)
+        E = self.experts
+        flat = score.detach().reshape(-1, E).float().contiguous()
+        _, _, sel, _ = ops.route_logits(flat, float(self.tau))
+        select = sel.view(score.shape).bool()
+        experts_prob = torch.where(select, torch.sigmoid(score), torch.zeros((), dtype=score.dtype,
+                                                                              device=score.device))
+        probs = torch.softmax(score, dim=-1) if self.training else None
+        if not self.training:
+            self.activated_statistics.add_(sel.reshape(-1, E).sum(dim=0))
+        out = ops.masked_gate(intermediate, experts_prob, self._layout())
+        return out, probs
 
 
 class IntegratedOpenPanguMoEMLP(nn.Module):
-    """Eval-mode MoE MLP with the reference's module tree (src/openpangu_moe.py:43-130).
+    """MoE MLP with the reference's module tree (src/openpangu_moe.py:43-130): eval runs
+    the sparse kernels, training the masked path (src/openpangu_moe_origin.py:83-120).
 
     ``config`` needs ``hidden_size`` (and optionally ``intermediate_size``, default
     4 * hidden_size); ``train_args`` needs ``group_size`` (and optionally ``tau``).
@@ -110,9 +145,19 @@ class IntegratedOpenPanguMoEMLP(nn.Module):
         self.tau_moe = TauSparseMoE(H, I, E, G, tau)
 
     def forward(self, hidden_states: torch.Tensor, *args, **kwargs) -> torch.Tensor:
-        if self.training:
-            raise NotImplementedError("IntegratedOpenPanguMoEMLP: only the eval (inference) path is built")
-        return self.tau_moe(hidden_states)
+        """Eval: the sparse kernels through ``tau_moe`` (src/openpangu_moe.py:123-127).
+        Training: the masked path of src/openpangu_moe_origin.py:83-120 (dense gate/up,
+        ``moelayer``, dense down); the probabilities go to ``penalize_logits_list``."""
+        if not self.training:
+            return self.tau_moe(hidden_states)
+        if self.moelayer is None:
+            raise RuntimeError("IntegratedOpenPanguMoEMLP: reordered for inference (projections dropped); "
+                               "the masked training path needs them")
+        intermediate = self.act_fn(self.gate_proj(hidden_states)) * self.up_proj(hidden_states)
+        moe_intermediate, probs = self.moelayer(hidden_states, intermediate)
+        if probs is not None and self.penalize_logits_list is not None:
+            self.penalize_logits_list.append(probs)
+        return self.down_proj(moe_intermediate)
 
     @torch.no_grad()
     def physical_reorder_for_inference(self, tau: float) -> None:
@@ -138,3 +183,33 @@ def physical_reorder_for_inference(layers: Iterable[nn.Module], tau: float) -> N
             mlp.physical_reorder_for_inference(tau)
     if torch.cuda.is_available():
         torch.cuda.empty_cache()
+
+
+def penalty_losses(penalize_logits_list: List[torch.Tensor], attention_mask: Optional[torch.Tensor],
+                   experts: int, gamma: float, lb_gamma: Optional[float] = None):
+    """Entropy and load-balance regularizers of the masked training step
+    (src/openpangu_moe_origin.py:236-261), averaged over the recorded layers:
+    entropy = mean over valid tokens of sum_e entr(p) (times gamma); load balance =
+    experts * sum_e (mean over valid tokens of p_e)^2 (times lb_gamma, default gamma).
+    Returns (entropy_loss, load_balance_loss); zeros when nothing was recorded."""
+    if not penalize_logits_list:
+        z = torch.zeros(())
+        return z, z.clone()
+    p0 = penalize_logits_list[0]
+    dev = p0.device
+    if attention_mask is None:
+        mask_float = torch.ones(p0.shape[:-1], dtype=torch.float, device=dev)
+    else:
+        mask_float = attention_mask.float().to(dev)
+    valid = mask_float.sum()
+    eps = 1e-6
+    lbg = gamma if lb_gamma is None else lb_gamma
+    ent = torch.zeros((), device=dev)
+    lb = torch.zeros((), device=dev)
+    for probs in penalize_logits_list:
+        entropy = torch.special.entr(probs).sum(dim=-1)
+        ent = ent + (entropy * mask_float).sum() / (valid + eps) * gamma
+        avg = (probs * mask_float.unsqueeze(-1)).reshape(-1, experts).sum(dim=0) / (valid + eps)
+        lb = lb + (avg ** 2).sum() * experts * lbg
+    n = len(penalize_logits_list)
+    return ent / n, lb / n

@@ -298,6 +298,81 @@ def combine(y: torch.Tensor, token_pairs: torch.Tensor, count: torch.Tensor, H: 
     return out
 
 
+# ----------------------------------------------------------------------------- masked gating
+def masked_gate_layout(expert_ids: torch.Tensor, E: int):
+    """(expert_ids int32, perm, seg) for the masked-gate kernels: perm = neurons sorted by
+    expert id (stable), seg [E+1] = expert segment offsets in perm."""
+    eid = expert_ids.to(torch.int32).contiguous()
+    if eid.numel() and (int(eid.min()) < 0 or int(eid.max()) >= E):
+        raise RuntimeError(f"prunepath.masked_gate_layout: expert ids outside [0, {E})")
+    perm = torch.argsort(eid, stable=True).to(torch.int32)
+    seg = torch.zeros(E + 1, dtype=torch.int32, device=eid.device)
+    seg[1:] = torch.cumsum(torch.bincount(eid.long(), minlength=E), 0).to(torch.int32)
+    return eid, perm, seg
+
+
+def _mg_rows(t: torch.Tensor, last: int):
+    return t.reshape(-1, last).contiguous()
+
+
+def _mg_dtype(t: torch.Tensor) -> int:
+    if t.dtype == torch.float32:
+        return L.PP_DTYPE_F32
+    if t.dtype == torch.bfloat16:
+        return L.PP_DTYPE_BF16
+    raise RuntimeError(f"prunepath.masked_gate: activations must be float32 or bfloat16 (got {t.dtype})")
+
+
+def masked_gate_fwd(inter: torch.Tensor, gates: torch.Tensor, eid: torch.Tensor) -> torch.Tensor:
+    """inter [..., I] * gates[..., expert_ids] (MoELayer.forward's mask matmul and multiply,
+    src/MoEBlock_origin.py:205-212), same dtype and shape as inter."""
+    I, E = inter.shape[-1], gates.shape[-1]
+    x = _mg_rows(inter, I)
+    g = _mg_rows(gates.float(), E)
+    _need_gpu("masked_gate_fwd", x, g, eid)
+    out = torch.empty_like(x)
+    rc = L.lib().pp_masked_gate_fwd(_vp(x), _mg_dtype(x), _vp(g), _vp(eid), x.shape[0], I, E, _vp(out),
+                                    _stream(x))
+    L.check(rc, "masked_gate_fwd")
+    return out.view(inter.shape)
+
+
+def masked_gate_bwd(d_out: torch.Tensor, inter: torch.Tensor, gates: torch.Tensor, eid: torch.Tensor,
+                    perm: torch.Tensor, seg: torch.Tensor, need_d_inter: bool = True):
+    """(d_inter or None, d_gates fp32) of masked_gate_fwd."""
+    I, E = inter.shape[-1], gates.shape[-1]
+    x = _mg_rows(inter, I)
+    go = _mg_rows(d_out.to(inter.dtype), I)
+    g = _mg_rows(gates.float(), E)
+    _need_gpu("masked_gate_bwd", go, x, g, eid, perm, seg)
+    d_inter = torch.empty_like(x) if need_d_inter else None
+    d_gates = torch.empty(x.shape[0], E, dtype=torch.float32, device=x.device)
+    rc = L.lib().pp_masked_gate_bwd(_vp(go), _vp(x), _mg_dtype(x), _vp(g), _vp(eid), _vp(perm), _vp(seg),
+                                    x.shape[0], I, E, _vp(d_inter), _vp(d_gates), _stream(x))
+    L.check(rc, "masked_gate_bwd")
+    return (d_inter.view(inter.shape) if d_inter is not None else None), d_gates.view(gates.shape)
+
+
+class _MaskedGate(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, inter, gates, eid, perm, seg):
+        ctx.save_for_backward(inter, gates, eid, perm, seg)
+        return masked_gate_fwd(inter, gates, eid)
+
+    @staticmethod
+    def backward(ctx, d_out):
+        inter, gates, eid, perm, seg = ctx.saved_tensors
+        d_inter, d_gates = masked_gate_bwd(d_out, inter, gates, eid, perm, seg, ctx.needs_input_grad[0])
+        return d_inter, d_gates.to(gates.dtype), None, None, None
+
+
+def masked_gate(inter: torch.Tensor, gates: torch.Tensor, layout) -> torch.Tensor:
+    """Differentiable masked gating: inter * (gates @ experts_masks) with the HIP forward
+    and backward kernels; ``layout`` from masked_gate_layout."""
+    eid, perm, seg = layout
+    return _MaskedGate.apply(inter, gates, eid, perm, seg)
+
+
 # ----------------------------------------------------------------------------- torch.library
 @torch.library.custom_op("prunepath::route_logits", mutates_args=())
 def _route_logits_op(logits: torch.Tensor, tau: float) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor,

@@ -43,12 +43,40 @@ def test_original_mlp_projections_are_taken_over(pkg):
     assert m.gate_proj is orig.gate_proj and m.down_proj is orig.down_proj
 
 
-def test_training_forward_is_not_built(pkg):
+def test_training_forward_has_no_cpu_fallback(pkg):
+    """The masked training path runs the routing and gating kernels: CPU tensors are
+    refused, not computed on the host."""
     cfg, ta = _cfg()
     m = pkg.IntegratedOpenPanguMoEMLP(cfg, ta)
     m.train()
-    with pytest.raises(NotImplementedError):
+    with pytest.raises(RuntimeError, match="GPU"):
         m(torch.zeros(1, 1, 256))
+
+
+def test_penalty_losses_closed_forms(pkg):
+    """src/openpangu_moe_origin.py:236-261 on inputs whose values are fixed by the
+    definitions: uniform probabilities give entropy ln E and load balance 1; one-hot
+    probabilities give entropy 0 and load balance E * sum_e f_e^2 (f_e = share of the
+    valid tokens routed to e); masked-out tokens do not count; two layers average."""
+    E, gamma, lbg = 16, 0.3, 0.7
+    B, Lq = 2, 5
+    uni = torch.full((B, Lq, E), 1.0 / E)
+    ent, lb = pkg.penalty_losses([uni], None, E, gamma, lbg)
+    assert abs(float(ent) - gamma * np.log(E)) < 1e-5
+    assert abs(float(lb) - lbg * 1.0) < 1e-4
+    ids = torch.tensor([[0, 0, 3, 5, 5], [5, 1, 0, 9, 9]])
+    onehot = torch.nn.functional.one_hot(ids, E).float()
+    am = torch.tensor([[1, 1, 1, 1, 0], [1, 1, 1, 0, 0]])  # 7 valid tokens: experts 0,0,3,5,5,1,0
+    ent, lb = pkg.penalty_losses([onehot], am, E, gamma, lbg)
+    assert float(ent) == 0.0
+    f = np.bincount([0, 0, 3, 5, 5, 1, 0], minlength=E) / 7.0
+    assert abs(float(lb) - lbg * E * float((f ** 2).sum())) < 1e-4
+    # default lb_gamma = gamma; the two-layer average of the uniform and one-hot cases
+    ent2, lb2 = pkg.penalty_losses([uni, onehot], am, E, gamma)
+    assert abs(float(ent2) - gamma * np.log(E) / 2) < 1e-5
+    assert abs(float(lb2) - gamma * (1.0 + E * float((f ** 2).sum())) / 2) < 1e-4
+    z = pkg.penalty_losses([], None, E, gamma)
+    assert float(z[0]) == 0.0 and float(z[1]) == 0.0
 
 
 def test_load_cluster_ids_reference_format(pkg, tmp_path):
