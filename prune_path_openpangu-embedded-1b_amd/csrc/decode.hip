@@ -503,7 +503,7 @@ __global__ __launch_bounds__(64 * NW) void decode16_kernel(
   constexpr int H = 512 * CPL;
   constexpr int HC = H / 8;
   constexpr int NT = 64 * NW;
-  extern __shared__ __align__(16) float red[];  // [NW-1][H]
+  extern __shared__ __align__(16) float red[];  // [NW][H]
   __shared__ __align__(16) float part_s[16 * NW];
   __shared__ __align__(16) float lg_s[16];
   __shared__ __align__(16) float pg_s[32];
@@ -777,27 +777,16 @@ __global__ __launch_bounds__(64 * NW) void decode16_kernel(
   }
 
   // ---- workgroup reduction -> one of DEC16_NCOPY fp32 accumulators
-  // waves 1..NW-1 park partials in LDS, wave 0 adds its own into slot 0, then every
-  // thread folds the slots in order for contiguous h and adds to the copy
-  // (uniform over the workgroup: whether it has records of e1, from the same split)
+  // every wave parks its partials in its LDS slot, then every thread folds the slots in
+  // wave order for contiguous h and adds to the copy (uniform over the workgroup:
+  // whether it has records of a speculated expert, from the same split)
   const bool spec_wg = spec_used && ((uint32_t)G / (uint32_t)W > 0u || (uint32_t)b < (uint32_t)G % (uint32_t)W);
   if (n > 0 || spec_wg) {
-    if (wv > 0) {
 #pragma unroll
-      for (int c = 0; c < CPL; ++c) {
-        float4* dst = (float4*)(red + (wv - 1) * H + (lane + 64 * c) * 8);
-        dst[0] = make_float4(oacc[c][0], oacc[c][1], oacc[c][2], oacc[c][3]);
-        dst[1] = make_float4(oacc[c][4], oacc[c][5], oacc[c][6], oacc[c][7]);
-      }
-    }
-    __syncthreads();
-    if (wv == 0) {
-#pragma unroll
-      for (int c = 0; c < CPL; ++c) {
-        float* dst = red + (lane + 64 * c) * 8;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) dst[i] = oacc[c][i] + dst[i];
-      }
+    for (int c = 0; c < CPL; ++c) {
+      float4* dst = (float4*)(red + wv * H + (lane + 64 * c) * 8);
+      dst[0] = make_float4(oacc[c][0], oacc[c][1], oacc[c][2], oacc[c][3]);
+      dst[1] = make_float4(oacc[c][4], oacc[c][5], oacc[c][6], oacc[c][7]);
     }
     __syncthreads();
     float* accc = dec_acc_set(acc, H, epoch) + (b % DEC16_NCOPY) * H;
@@ -807,7 +796,7 @@ __global__ __launch_bounds__(64 * NW) void decode16_kernel(
       if (h < H) {
         float v = red[h];
 #pragma unroll
-        for (int w = 1; w < NW - 1; ++w) v += red[w * H + h];
+        for (int w = 1; w < NW; ++w) v += red[w * H + h];
         unsafeAtomicAdd(accc + h, v);
       }
     }
@@ -908,7 +897,7 @@ extern "C" int pp_moe_decode(const void* x, int x_dtype, int H, const float* rou
   hipStream_t s = (hipStream_t)stream;
   if (E == 16 && H % 512 == 0) {
     const int c = H / 512;
-    const size_t smem16 = (size_t)(DEC16_NW - 1) * H * sizeof(float);
+    const size_t smem16 = (size_t)DEC16_NW * H * sizeof(float);
     if (grid_in == 0) grid = pp_device_cus() / 2;  // measured best: one 8-wave workgroup per two CUs
 #define PP_DEC16_CASE(C)                                                                                     \
   case C:                                                                                                    \
