@@ -11,7 +11,8 @@ atol 2e-3) with the selection bit-exact against the oracle on the kernel's own l
 * prefill GEMMs: gemm_s_kernel (N <= 64, G % 64 == 0, H >= 384), gemm_v3_kernel
   (G % 64 == 0 otherwise) and gateup_kernel / down_kernel (G % 64 == 32);
 * the limits: H = 128 and 4096, E = 1 and 256, G = 32 and 8192, tau above 1 (every
-  expert selected) and 0 (rank 0 only), bf16 and fp32 x.
+  expert selected) and 0 (rank 0 only), bf16 and fp32 x; a router bias (log Zipf) on
+  every router variant.
 """
 import numpy as np
 import pytest
@@ -21,32 +22,34 @@ from helpers import assert_close, gi, make_module, oracle, sparse_expected, to_g
 
 pytestmark = pytest.mark.gpu
 
-# (H, E, G, N, tau, x dtype)
+# (H, E, G, N, tau, x dtype, router bias)
 CASES = [
-    (128, 16, 32, 3, 0.7, torch.float32),       # smallest H; G % 64 == 32 GEMMs; route16_few
-    (640, 16, 64, 1, 0.7, torch.float32),       # E = 16 but H % 512 != 0: decode_kernel
-    (640, 16, 64, 70, 0.7, torch.float32),      # route16 with H % 512 != 0; gemm_v3 at N = 70
-    (4096, 16, 128, 1, 0.7, torch.float32),     # decode16 at CPL = 8 (no speculative loads)
-    (4096, 16, 128, 40, 0.5, torch.bfloat16),   # H > 2048: route16 at N <= 64; short tiles
-    (2048, 16, 64, 64, 0.95, torch.float32),    # route16_few at CPL = 4; short tiles at N = 64
-    (1024, 8, 96, 33, 0.9, torch.float32),      # route_kernel (E = 8); gateup/down kernels (G = 96)
-    (1024, 8, 96, 1, 0.9, torch.bfloat16),      # decode_kernel, E = 8, bf16 x
-    (512, 256, 32, 5, 0.7, torch.float32),      # E = 256
-    (512, 256, 32, 1, 0.7, torch.float32),      # decode with E = 256
-    (768, 4, 8192, 2, 1.05, torch.float32),     # G = 8192; tau > 1 selects every expert
-    (768, 4, 8192, 1, 0.0, torch.float32),      # decode, tau = 0: rank 0 only
-    (1536, 1, 64, 17, 0.7, torch.float32),      # E = 1
-    (1536, 16, 384, 129, 0.7, torch.bfloat16),  # bf16 x, ragged N past two 64-token blocks
-    (1536, 16, 384, 1, 0.7, torch.bfloat16),    # decode16 at the configured shape, bf16 x
+    (128, 16, 32, 3, 0.7, torch.float32, False),       # smallest H; G % 64 == 32 GEMMs; route16_few
+    (640, 16, 64, 1, 0.7, torch.float32, False),       # E = 16 but H % 512 != 0: decode_kernel
+    (640, 16, 64, 70, 0.7, torch.float32, True),       # route16 with H % 512 != 0 and a bias; gemm_v3 at N = 70
+    (4096, 16, 128, 1, 0.7, torch.float32, False),     # decode16 at CPL = 8 (no speculative loads)
+    (4096, 16, 128, 40, 0.5, torch.bfloat16, False),   # H > 2048: route16 at N <= 64; short tiles
+    (2048, 16, 64, 64, 0.95, torch.float32, True),     # route16_few at CPL = 4 with a bias; short tiles at N = 64
+    (1024, 8, 96, 33, 0.9, torch.float32, False),      # route_kernel (E = 8); gateup/down kernels (G = 96)
+    (1024, 8, 96, 1, 0.9, torch.bfloat16, True),       # decode_kernel with local logits, E = 8, bf16 x, bias
+    (512, 256, 32, 5, 0.7, torch.float32, False),      # E = 256
+    (512, 256, 32, 1, 0.7, torch.float32, True),       # decode with E = 256 (published logits), bias
+    (768, 4, 8192, 2, 1.05, torch.float32, False),     # G = 8192; tau > 1 selects every expert
+    (768, 4, 8192, 1, 0.0, torch.float32, False),      # decode, tau = 0: rank 0 only
+    (1536, 1, 64, 17, 0.7, torch.float32, False),      # E = 1
+    (1536, 16, 384, 129, 0.7, torch.bfloat16, False),  # bf16 x, ragged N past two 64-token blocks
+    (1536, 16, 384, 1, 0.7, torch.bfloat16, False),    # decode16 at the configured shape, bf16 x
+    (1536, 16, 384, 1, 0.95, torch.float32, True),     # decode16 with the config-3 router bias
 ]
 
 
-@pytest.mark.parametrize("H,E,G,N,tau,xdt", CASES,
-                         ids=[f"H{c[0]}-E{c[1]}-G{c[2]}-N{c[3]}-tau{c[4]}-{str(c[5])[6:]}" for c in CASES])
-def test_layer_shape_vs_oracle(pkg, H, E, G, N, tau, xdt):
+@pytest.mark.parametrize("H,E,G,N,tau,xdt,with_bias", CASES,
+                         ids=[f"H{c[0]}-E{c[1]}-G{c[2]}-N{c[3]}-tau{c[4]}-{str(c[5])[6:]}{'-bias' if c[6] else ''}"
+                              for c in CASES])
+def test_layer_shape_vs_oracle(pkg, H, E, G, N, tau, xdt, with_bias):
     seed = H * 7 + E * 3 + G + N
     w = gi.layer_weights(seed, H=H, I=E * G, E=E)
-    m = make_module(pkg, w, tau)
+    m = make_module(pkg, w, tau, bias=gi.zipf_bias(E) if with_bias else None)
     x = gi.tokens(seed + 1, N, H=H)
     xg = to_gpu(x, xdt)
     out = m(xg[None]).float().cpu().numpy()[0]
@@ -60,7 +63,7 @@ def test_layer_shape_vs_oracle(pkg, H, E, G, N, tau, xdt):
         np.testing.assert_array_equal(st["sel_ids"].numpy(), sel.ranked[0][:k])
         np.testing.assert_array_equal(st["sel_gates"].numpy(), sel.gates[0][sel.ranked[0][:k]])
     else:
-        res = pkg.ops.route(xg, m.router_packed, E, tau)
+        res = pkg.ops.route(xg, m.router_packed, E, tau, bias=m.router_bias)
         logits = res["logits"].cpu().numpy()
         sel = oracle.select(logits, tau)
         np.testing.assert_array_equal(res["mask"].cpu().numpy(), sel.mask)
