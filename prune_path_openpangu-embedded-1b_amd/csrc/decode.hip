@@ -36,7 +36,7 @@
 #include "pp_common.h"
 
 #define DEC_THREADS 256
-#define DEC_NCOPY 8   // accumulator copies per set (general kernel; the allocation)
+#define DEC_NCOPY 4   // accumulator copies per set (general kernel; the allocation): 4 beat 8 and 16 at E = 192
 #define DEC16_NCOPY 4 // copies the E = 16 kernel uses (128 workgroups: 32 per address)
 #define DEC16_SPEC(CPL) ((CPL) <= 4)  // speculative top-expert loads (register budget)
 #ifndef DEC16_NW
