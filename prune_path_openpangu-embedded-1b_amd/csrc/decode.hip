@@ -186,11 +186,24 @@ __global__ __launch_bounds__(DEC_THREADS) void decode_kernel(
   __shared__ int k_s;
   __shared__ int sel_ids_s[PP_MAX_EXPERTS];
   __shared__ float sel_g_s[PP_MAX_EXPERTS];
+  __shared__ __align__(16) unsigned char xs_raw[4096 * sizeof(XT)];  // x as given, for the stream
 
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int W = gridDim.x, b = blockIdx.x;
   const int HC = H >> 3;  // 16-byte chunks per row
   const uint32_t epoch = ld_rlx(&st->router_ticket);
+
+  // x for the stream goes global -> LDS by DMA now (no registers held through the
+  // routing); the stream reads it from LDS. Loaded at the stream's start, x cost ~3 us at
+  // E = 192; loaded into registers here, +1.7 us (registers live through the selection).
+  // 1 KB per instruction; lanes past the end re-read the last chunk (in bounds) into the
+  // spare end of xs_raw.
+  if (wv == DEC_THREADS / 64 - 1) {
+    const int nbytes = H * (int)sizeof(XT), nch = nbytes >> 4;
+    for (int c0 = 0; c0 < nch; c0 += 64)
+      __builtin_amdgcn_global_load_lds((const unsigned char*)x + 16 * min(c0 + lane, nch - 1),
+                                       (__attribute__((address_space(3))) void*)(xs_raw + 16 * c0), 16, 0, 0);
+  }
 
   if (LOCAL) {
     // ---------------- every workgroup routes the token itself
@@ -288,6 +301,21 @@ __global__ __launch_bounds__(DEC_THREADS) void decode_kernel(
     }
   }
   const int k = k_s;
+  // x, rounded to bf16 like the reference's x.to(bfloat16), as fp32 in registers, from
+  // the LDS copy (the DMA issued at the start has landed: the issuing wave waits for its
+  // loads, then the barrier; the other waves' stores are not waited for)
+  if (wv == DEC_THREADS / 64 - 1) vm_wait();
+  __syncthreads();
+  float xr[CPL][8];
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) {
+    const int ch = lane + 64 * c;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float vx = ch < HC ? load_as_f32<XT>((const XT*)xs_raw, (int64_t)ch * 8 + i) : 0.0f;
+      xr[c][i] = bf16_to_f32(f32_to_bf16(vx));
+    }
+  }
   dec_clear_previous(acc, H, epoch, b, W, tid, DEC_THREADS);
 
   // ---------------- stream the selected neuron records
@@ -300,17 +328,6 @@ __global__ __launch_bounds__(DEC_THREADS) void decode_kernel(
   int r = v0 + (n * wv) / 4;
   const int r_end = v0 + (n * (wv + 1)) / 4;
 
-  // x, rounded to bf16 like the reference's x.to(bfloat16), as fp32 in registers
-  float xr[CPL][8];
-#pragma unroll
-  for (int c = 0; c < CPL; ++c) {
-    const int ch = lane + 64 * c;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float vx = ch < HC ? load_as_f32<XT>(x, (int64_t)ch * 8 + i) : 0.0f;
-      xr[c][i] = bf16_to_f32(f32_to_bf16(vx));
-    }
-  }
   float oacc[CPL][8];
 #pragma unroll
   for (int c = 0; c < CPL; ++c)
