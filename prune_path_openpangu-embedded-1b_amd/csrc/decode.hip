@@ -35,7 +35,14 @@
 // hundreds of workgroups cannot afford inside a 5 us kernel.
 #include "pp_common.h"
 
-#define DEC_THREADS 256
+// Waves per workgroup of the general kernel: eight while the registers fit 256 per lane
+// (CPL <= 5), else four. Eight waves keep twice the records per CU in flight
+// (E = 192, G = 32: 25.6 -> 24.7 us per layer).
+template <int CPL>
+struct DecNW {
+  static constexpr int NW = CPL <= 5 ? 8 : 4;
+  static constexpr int NT = 64 * NW;
+};
 #define DEC_NCOPY 4   // accumulator copies per set (general kernel; the allocation): 4 beat 8 and 16 at E = 192
 #define DEC16_NCOPY 4 // copies the E = 16 kernel uses (128 workgroups: 32 per address)
 #define DEC16_SPEC(CPL) ((CPL) <= 4)  // speculative top-expert loads (register budget)
@@ -135,15 +142,16 @@ __device__ void local_logits(const XT* __restrict__ x, int H, const float* __res
       xv[i] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
   }
-  for (int e0 = 0; e0 < E; e0 += 16) {
+  for (int e0 = 0; e0 < E; e0 += 4 * DecNW<CPL>::NW) {
     float4 wr[4][NC];
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int i = 0; i < NC; ++i) {
         const int c = lane + 64 * i;
-        wr[j][i] = c < HC4 ? *(const float4*)(router + (int64_t)(e0 + 4 * wv + j) * H + 4 * c)
-                           : make_float4(0.f, 0.f, 0.f, 0.f);
+        const int er = e0 + 4 * wv + j;  // rows past E (the zero padding, or beyond) are not read
+        wr[j][i] = (c < HC4 && er < E) ? *(const float4*)(router + (int64_t)er * H + 4 * c)
+                                       : make_float4(0.f, 0.f, 0.f, 0.f);
       }
     float part[4];
 #pragma unroll
@@ -173,13 +181,14 @@ __device__ void local_logits(const XT* __restrict__ x, int H, const float* __res
 }
 
 template <typename XT, int CPL, bool LOCAL>
-__global__ __launch_bounds__(DEC_THREADS) void decode_kernel(
+__global__ __launch_bounds__(DecNW<CPL>::NT) void decode_kernel(
     const XT* __restrict__ x, int H, const float* __restrict__ router, const float* __restrict__ bias,
     int E, int G, float tau, const bf16_t* __restrict__ rows, bf16_t* __restrict__ out,
     pp_decode_state* __restrict__ st, float* __restrict__ acc, int R) {
-  extern __shared__ __align__(16) float red[];  // [3][H] wave partials
+  constexpr int NW = DecNW<CPL>::NW, NT = DecNW<CPL>::NT;
+  extern __shared__ __align__(16) float red[];  // [NW - 1][H] wave partials
   __shared__ SelScratch ss;
-  __shared__ float red4[4];
+  __shared__ float red4[NW];
   __shared__ unsigned long long keys_s[PP_MAX_EXPERTS];
   __shared__ float lg_s[PP_MAX_EXPERTS];
   __shared__ int flag_s;
@@ -198,7 +207,7 @@ __global__ __launch_bounds__(DEC_THREADS) void decode_kernel(
   // E = 192; loaded into registers here, +1.7 us (registers live through the selection).
   // 1 KB per instruction; lanes past the end re-read the last chunk (in bounds) into the
   // spare end of xs_raw.
-  if (wv == DEC_THREADS / 64 - 1) {
+  if (wv == NT / 64 - 1) {
     const int nbytes = H * (int)sizeof(XT), nch = nbytes >> 4;
     for (int c0 = 0; c0 < nch; c0 += 64)
       __builtin_amdgcn_global_load_lds((const unsigned char*)x + 16 * min(c0 + lane, nch - 1),
@@ -220,8 +229,8 @@ __global__ __launch_bounds__(DEC_THREADS) void decode_kernel(
     }
     __syncthreads();
     if (b == 0) {  // telemetry for the caller: logits and selection of this call
-      for (int j = tid; j < E; j += DEC_THREADS) st_rlx(&st->logits[j], lg_s[j]);
-      for (int q = tid; q < k_s; q += DEC_THREADS) {
+      for (int j = tid; j < E; j += NT) st_rlx(&st->logits[j], lg_s[j]);
+      for (int q = tid; q < k_s; q += NT) {
         st_rlx(&st->sel_ids[q], sel_ids_s[q]);
         st_rlx(&st->sel_gates[q], sel_g_s[q]);
       }
@@ -239,23 +248,25 @@ __global__ __launch_bounds__(DEC_THREADS) void decode_kernel(
     if (b < E) {
       // H <= 4096: at most 16 elements per thread, all loaded before the first FMA
       // (one memory round trip), then added in k order
-      constexpr int KPT = 4096 / DEC_THREADS;
+      constexpr int KPT = 4096 / NT;
       float xv[KPT], wr[KPT];
 #pragma unroll
       for (int i = 0; i < KPT; ++i) {
-        const int kk = tid + i * DEC_THREADS;
+        const int kk = tid + i * NT;
         xv[i] = kk < H ? load_as_f32<XT>(x, kk) : 0.0f;
         wr[i] = kk < H ? router[(int64_t)b * H + kk] : 0.0f;
       }
       float sacc = 0.0f;
 #pragma unroll
       for (int i = 0; i < KPT; ++i)
-        if (tid + i * DEC_THREADS < H) sacc = __builtin_fmaf(xv[i], wr[i], sacc);
+        if (tid + i * NT < H) sacc = __builtin_fmaf(xv[i], wr[i], sacc);
       sacc = wave_sum(sacc);
       if (lane == 0) red4[wv] = sacc;
       __syncthreads();
       if (tid == 0) {
-        float l = __fadd_rn(__fadd_rn(__fadd_rn(red4[0], red4[1]), red4[2]), red4[3]);
+        float l = red4[0];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) l = __fadd_rn(l, red4[w]);
         if (bias) l = __fadd_rn(l, bias[b]);
         st_rlx(&slots[b], ((unsigned long long)tag << 32) | __float_as_uint(l));
       }
@@ -263,7 +274,7 @@ __global__ __launch_bounds__(DEC_THREADS) void decode_kernel(
     // router workgroup e publishes {tag, logit} in its own 64-bit slot; every workgroup
     // gathers the E slots (bounded spin). No counter is shared while routing (E
     // increments of one address serialise at the memory side).
-    for (int j = tid; j < E; j += DEC_THREADS) {
+    for (int j = tid; j < E; j += NT) {
       unsigned long long v = ld_rlx(&slots[j]);
       uint32_t n = 0;
       while ((uint32_t)(v >> 32) != tag) {
@@ -281,10 +292,10 @@ __global__ __launch_bounds__(DEC_THREADS) void decode_kernel(
       if (wv == 0) select_one_token([&](int j) { return lg_s[j]; }, E, tau, &ss, lane);
       __syncthreads();
     } else {
-      select_one_token_wg([&](int j) { return lg_s[j]; }, E, tau, &ss, keys_s, red4, tid, DEC_THREADS);
+      select_one_token_wg([&](int j) { return lg_s[j]; }, E, tau, &ss, keys_s, red4, tid, NT);
     }
     const int kq = ss.k;
-    for (int q = tid; q < kq; q += DEC_THREADS) {
+    for (int q = tid; q < kq; q += NT) {
       const int e = ss.order[q];
       sel_ids_s[q] = e;
       sel_g_s[q] = pp_sigmoid(lg_s[e]);
@@ -292,8 +303,8 @@ __global__ __launch_bounds__(DEC_THREADS) void decode_kernel(
     if (tid == 0) k_s = kq;
     __syncthreads();
     if (b == 0) {  // telemetry for the caller: logits and selection of this call
-      for (int j = tid; j < E; j += DEC_THREADS) st_rlx(&st->logits[j], lg_s[j]);
-      for (int q = tid; q < k_s; q += DEC_THREADS) {
+      for (int j = tid; j < E; j += NT) st_rlx(&st->logits[j], lg_s[j]);
+      for (int q = tid; q < k_s; q += NT) {
         st_rlx(&st->sel_ids[q], sel_ids_s[q]);
         st_rlx(&st->sel_gates[q], sel_g_s[q]);
       }
@@ -304,7 +315,7 @@ __global__ __launch_bounds__(DEC_THREADS) void decode_kernel(
   // x, rounded to bf16 like the reference's x.to(bfloat16), as fp32 in registers, from
   // the LDS copy (the DMA issued at the start has landed: the issuing wave waits for its
   // loads, then the barrier; the other waves' stores are not waited for)
-  if (wv == DEC_THREADS / 64 - 1) vm_wait();
+  if (wv == NT / 64 - 1) vm_wait();
   __syncthreads();
   float xr[CPL][8];
 #pragma unroll
@@ -316,7 +327,7 @@ __global__ __launch_bounds__(DEC_THREADS) void decode_kernel(
       xr[c][i] = bf16_to_f32(f32_to_bf16(vx));
     }
   }
-  dec_clear_previous(acc, H, epoch, b, W, tid, DEC_THREADS);
+  dec_clear_previous(acc, H, epoch, b, W, tid, NT);
 
   // ---------------- stream the selected neuron records
   // this workgroup: records [v0, v1) of the k*G selected ones; wave wv a contiguous
@@ -325,8 +336,8 @@ __global__ __launch_bounds__(DEC_THREADS) void decode_kernel(
   int v0, v1;
   pp_split((uint32_t)T, (uint32_t)W, (uint32_t)b, v0, v1);
   const int n = v1 - v0;
-  int r = v0 + (n * wv) / 4;
-  const int r_end = v0 + (n * (wv + 1)) / 4;
+  int r = v0 + (n * wv) / NW;
+  const int r_end = v0 + (n * (wv + 1)) / NW;
 
   float oacc[CPL][8];
 #pragma unroll
@@ -384,8 +395,8 @@ __global__ __launch_bounds__(DEC_THREADS) void decode_kernel(
   }
 
   // ---------------- workgroup reduction -> fp32 accumulator copy
-  // waves 1..3 park their partials in LDS, wave 0 adds its own into the first slot,
-  // then all threads fold the three slots for contiguous h and add to the copy.
+  // waves 1..NW-1 park their partials in LDS, wave 0 adds its own into the first slot,
+  // then all threads fold the slots in wave order for contiguous h and add to the copy.
   const bool has_work = n > 0;
   if (has_work && wv > 0) {
 #pragma unroll
@@ -413,8 +424,10 @@ __global__ __launch_bounds__(DEC_THREADS) void decode_kernel(
   __syncthreads();
   if (has_work) {
     float* accc = dec_acc_set(acc, H, epoch) + (size_t)(b % DEC_NCOPY) * H;
-    for (int h = tid; h < H; h += DEC_THREADS) {
-      const float sv = (red[h] + red[H + h]) + red[2 * H + h];
+    for (int h = tid; h < H; h += NT) {
+      float sv = red[h];
+#pragma unroll
+      for (int w = 1; w < NW - 1; ++w) sv += red[(size_t)w * H + h];
       unsafeAtomicAdd(accc + h, sv);
     }
   }
@@ -427,17 +440,17 @@ __global__ __launch_bounds__(DEC_THREADS) void decode_kernel(
     // the first add (one round trip per pass; one pass for H <= 2048)
     constexpr int DEC_FOLD_H = 8;
     const float* accs = dec_acc_set(acc, H, epoch);
-    for (int h0 = 0; h0 < H; h0 += DEC_THREADS * DEC_FOLD_H) {
+    for (int h0 = 0; h0 < H; h0 += NT * DEC_FOLD_H) {
       float sv[DEC_FOLD_H][DEC_NCOPY];
 #pragma unroll
       for (int i = 0; i < DEC_FOLD_H; ++i) {
-        const int h = h0 + tid + i * DEC_THREADS;
+        const int h = h0 + tid + i * NT;
 #pragma unroll
         for (int c = 0; c < DEC_NCOPY; ++c) sv[i][c] = h < H ? ld_rlx(accs + (size_t)c * H + h) : 0.0f;
       }
 #pragma unroll
       for (int i = 0; i < DEC_FOLD_H; ++i) {
-        const int h = h0 + tid + i * DEC_THREADS;
+        const int h = h0 + tid + i * NT;
         if (h < H) {
           float tot = 0.0f;
 #pragma unroll
@@ -872,12 +885,12 @@ extern "C" int pp_decode_workspace_init(void* workspace, int H, int E, void* str
 }
 
 template <typename XT, bool LOCAL>
-static void launch_decode(int cpl, int grid, size_t smem, hipStream_t s, const XT* x, int H, const float* router,
+static void launch_decode(int cpl, int grid, hipStream_t s, const XT* x, int H, const float* router,
                           const float* bias, int E, int G, float tau, const bf16_t* rows, bf16_t* out,
                           pp_decode_state* st, float* acc, int R) {
 #define PP_DEC_CASE(C)                                                                                  \
   case C:                                                                                               \
-    decode_kernel<XT, C, LOCAL><<<grid, DEC_THREADS, smem, s>>>(x, H, router, bias, E, G, tau, rows, out, st, \
+    decode_kernel<XT, C, LOCAL><<<grid, DecNW<C>::NT, (size_t)(DecNW<C>::NW - 1) * H * sizeof(float), s>>>(x, H, router, bias, E, G, tau, rows, out, st, \
                                                                 acc, R);                                \
     break;
   switch (cpl) {
@@ -908,7 +921,6 @@ extern "C" int pp_moe_decode(const void* x, int x_dtype, int H, const float* rou
   if (grid == 0) grid = pp_device_cus();
   if (grid < R) grid = R;  // every expert has its router workgroup
   const int cpl = (H / 8 + 63) / 64;  // 16-byte chunks per lane per row (H <= 4096 -> <= 8)
-  const size_t smem = (size_t)3 * H * sizeof(float);
   pp_decode_state* st = (pp_decode_state*)workspace;
   float* acc = (float*)((char*)workspace + dec_acc_offset());
   hipStream_t s = (hipStream_t)stream;
@@ -942,11 +954,11 @@ extern "C" int pp_moe_decode(const void* x, int x_dtype, int H, const float* rou
   const bf16_t* rows = (const bf16_t*)packed;
   bf16_t* o = (bf16_t*)out_bf16;
   if (x_dtype == PP_DTYPE_F32) {
-    if (local) launch_decode<float, true>(cpl, grid, smem, s, (const float*)x, H, router_packed, bias, E, G, tau, rows, o, st, acc, R);
-    else launch_decode<float, false>(cpl, grid, smem, s, (const float*)x, H, router_packed, bias, E, G, tau, rows, o, st, acc, R);
+    if (local) launch_decode<float, true>(cpl, grid, s, (const float*)x, H, router_packed, bias, E, G, tau, rows, o, st, acc, R);
+    else launch_decode<float, false>(cpl, grid, s, (const float*)x, H, router_packed, bias, E, G, tau, rows, o, st, acc, R);
   } else {
-    if (local) launch_decode<bf16_t, true>(cpl, grid, smem, s, (const bf16_t*)x, H, router_packed, bias, E, G, tau, rows, o, st, acc, R);
-    else launch_decode<bf16_t, false>(cpl, grid, smem, s, (const bf16_t*)x, H, router_packed, bias, E, G, tau, rows, o, st, acc, R);
+    if (local) launch_decode<bf16_t, true>(cpl, grid, s, (const bf16_t*)x, H, router_packed, bias, E, G, tau, rows, o, st, acc, R);
+    else launch_decode<bf16_t, false>(cpl, grid, s, (const bf16_t*)x, H, router_packed, bias, E, G, tau, rows, o, st, acc, R);
   }
   return pp_check_launch("pp_moe_decode");
 }
