@@ -296,7 +296,7 @@ __global__ __launch_bounds__(DecNW<CPL>::NT) void decode_kernel(
     }
     const int kq = ss.k;
     for (int q = tid; q < kq; q += NT) {
-      const int e = ss.order[q];
+      const int e = (int)min((unsigned)ss.order[q], (unsigned)(E - 1));  // (in range by construction; clamped: it addresses HBM)
       sel_ids_s[q] = e;
       sel_g_s[q] = pp_sigmoid(lg_s[e]);
     }

@@ -83,8 +83,8 @@ __device__ __forceinline__ float wave_max(float v) {
 // (__shfl_xor is a ds_bpermute, about a hundred cycles each).
 #define PP_DPP_XOR1 0xB1   // quad_perm [1,0,3,2]: lane i^1
 #define PP_DPP_XOR2 0x4E   // quad_perm [2,3,0,1]: lane i^2
-#define PP_DPP_ROR4 0x124  // row_ror:4: lane (i+4) mod 16 of the row
-#define PP_DPP_ROR8 0x128  // row_ror:8: lane (i+8) mod 16 of the row = i^8
+#define PP_DPP_ROR4 0x124  // row_ror:4: the row rotated by 4 lanes (used where direction does not matter)
+#define PP_DPP_ROR8 0x128  // row_ror:8: the row rotated by 8 lanes = lane i^8
 template <int CTRL>
 __device__ __forceinline__ float dpp_mov(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
@@ -589,6 +589,32 @@ __device__ __forceinline__ unsigned long long sel_key(float p, int j) {
   return ((unsigned long long)(~b) << 32) | (uint32_t)j;
 }
 
+// Value of lane (lane ^ j) for a 64-bit key: DPP for j = 1, 2 (quad permutes) and 8 (the
+// half-row rotation, i ^ 8 whichever way it turns), the LDS permute otherwise. j is a
+// constant after unrolling. (A rotation-based xor 4 depends on the rotation's direction:
+// taken the wrong way round it pairs the wrong lanes and the sort loses keys.)
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xf, 0xf, false);
+}
+__device__ __forceinline__ unsigned long long key_xor(unsigned long long v, int j) {
+  const uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
+  uint32_t a, b;
+  if (j == 1) {
+    a = dpp_u32<PP_DPP_XOR1>(lo);
+    b = dpp_u32<PP_DPP_XOR1>(hi);
+  } else if (j == 2) {
+    a = dpp_u32<PP_DPP_XOR2>(lo);
+    b = dpp_u32<PP_DPP_XOR2>(hi);
+  } else if (j == 8) {
+    a = dpp_u32<PP_DPP_ROR8>(lo);
+    b = dpp_u32<PP_DPP_ROR8>(hi);
+  } else {
+    return __shfl_xor(v, j, PP_WAVE);
+  }
+  return ((unsigned long long)b << 32) | a;
+}
+
 template <typename LG>
 static __device__ void select_one_token_wg(LG lg, int E, float tau, SelScratch* ss, unsigned long long* keys,
                                            float* red, int tid, int nthreads) {
@@ -621,8 +647,8 @@ static __device__ void select_one_token_wg(LG lg, int E, float tau, SelScratch* 
   // shuffles; padding ~0 sorts last), stores the sorted run, and each key's rank is its
   // place in its run plus the number of smaller keys in the other runs (binary search).
   // The same ranks as counting all smaller keys (E LDS reads per key, 2.4 us at E = 192);
-  // the whole E = 192 decode layer 24.7 -> 24.35 us. The 21 dependent 64-bit xor
-  // shuffles of the sort are most of what is left.
+  // the whole E = 192 decode layer 24.7 -> 24.35 us with LDS-permute shuffles; 14 of the
+  // sort's 21 exchanges go through DPP.
   const int nwk = (E + 63) >> 6;  // waves holding keys
   unsigned long long key = tid < E ? sel_key(pt, tid) : ~0ull;
   if (tid < E) ss->e[tid] = pt;
@@ -631,7 +657,7 @@ static __device__ void select_one_token_wg(LG lg, int E, float tau, SelScratch* 
     for (int k2 = 2; k2 <= 64; k2 <<= 1)
 #pragma unroll
       for (int j = k2 >> 1; j > 0; j >>= 1) {
-        const unsigned long long o = __shfl_xor(key, j, PP_WAVE);
+        const unsigned long long o = key_xor(key, j);
         const bool keep_min = ((lane & j) == 0) == ((lane & k2) == 0);
         key = keep_min ? (o < key ? o : key) : (o > key ? o : key);
       }
@@ -650,8 +676,10 @@ static __device__ void select_one_token_wg(LG lg, int E, float tau, SelScratch* 
       rank += lo;
     }
     const int idx = (int)(uint32_t)key;
-    ss->srt[rank] = ss->e[idx];
-    ss->order[rank] = idx;
+    if (rank < E && idx < E) {  // always, for a correct sort; guards the LDS and the ids
+      ss->srt[rank] = ss->e[idx];
+      ss->order[rank] = idx;
+    }
   }
   wg_lds_barrier();
   if (tid < PP_WAVE) {
