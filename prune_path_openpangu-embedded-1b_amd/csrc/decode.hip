@@ -186,7 +186,7 @@ __global__ __launch_bounds__(DecNW<CPL>::NT) void decode_kernel(
     int E, int G, float tau, const bf16_t* __restrict__ rows, bf16_t* __restrict__ out,
     pp_decode_state* __restrict__ st, float* __restrict__ acc, int R) {
   constexpr int NW = DecNW<CPL>::NW, NT = DecNW<CPL>::NT;
-  extern __shared__ __align__(16) float red[];  // [NW - 1][H] wave partials
+  extern __shared__ __align__(16) float red[];  // [NW][H] wave partials
   __shared__ SelScratch ss;
   __shared__ float red4[NW];
   __shared__ unsigned long long keys_s[PP_MAX_EXPERTS];
@@ -395,29 +395,17 @@ __global__ __launch_bounds__(DecNW<CPL>::NT) void decode_kernel(
   }
 
   // ---------------- workgroup reduction -> fp32 accumulator copy
-  // waves 1..NW-1 park their partials in LDS, wave 0 adds its own into the first slot,
-  // then all threads fold the slots in wave order for contiguous h and add to the copy.
+  // every wave parks its partials in its own LDS slot, one barrier, then all threads fold
+  // the slots in wave order for contiguous h and add to the copy
   const bool has_work = n > 0;
-  if (has_work && wv > 0) {
+  if (has_work) {
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
       const int ch = lane + 64 * c;
       if (ch < HC) {
-        float4* dst = (float4*)(red + (size_t)(wv - 1) * H + ch * 8);
+        float4* dst = (float4*)(red + (size_t)wv * H + ch * 8);
         dst[0] = make_float4(oacc[c][0], oacc[c][1], oacc[c][2], oacc[c][3]);
         dst[1] = make_float4(oacc[c][4], oacc[c][5], oacc[c][6], oacc[c][7]);
-      }
-    }
-  }
-  __syncthreads();
-  if (has_work && wv == 0) {
-#pragma unroll
-    for (int c = 0; c < CPL; ++c) {
-      const int ch = lane + 64 * c;
-      if (ch < HC) {
-        float* dst = red + ch * 8;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) dst[i] = oacc[c][i] + dst[i];
       }
     }
   }
@@ -427,7 +415,7 @@ __global__ __launch_bounds__(DecNW<CPL>::NT) void decode_kernel(
     for (int h = tid; h < H; h += NT) {
       float sv = red[h];
 #pragma unroll
-      for (int w = 1; w < NW - 1; ++w) sv += red[(size_t)w * H + h];
+      for (int w = 1; w < NW; ++w) sv += red[(size_t)w * H + h];
       unsafeAtomicAdd(accc + h, sv);
     }
   }
@@ -890,7 +878,7 @@ static void launch_decode(int cpl, int grid, hipStream_t s, const XT* x, int H, 
                           pp_decode_state* st, float* acc, int R) {
 #define PP_DEC_CASE(C)                                                                                  \
   case C:                                                                                               \
-    decode_kernel<XT, C, LOCAL><<<grid, DecNW<C>::NT, (size_t)(DecNW<C>::NW - 1) * H * sizeof(float), s>>>(x, H, router, bias, E, G, tau, rows, out, st, \
+    decode_kernel<XT, C, LOCAL><<<grid, DecNW<C>::NT, (size_t)DecNW<C>::NW * H * sizeof(float), s>>>(x, H, router, bias, E, G, tau, rows, out, st, \
                                                                 acc, R);                                \
     break;
   switch (cpl) {
