@@ -130,14 +130,23 @@ int pp_bucket(const uint8_t* mask, const float* gates, int64_t n_tokens, int E, 
  * overlapping calls on one workspace race. After a call the workspace holds the
  * call's logits, selected experts and gates (struct pp_decode_state below).
  * grid = number of workgroups (0 = automatic).
+ * Shapes other than E = 16 with H % 512 == 0 and (E > 16 or 16*H > 32768) publish
+ * each logit from its own workgroup and every workgroup waits for all E of them, so
+ * the E router workgroups must be resident on the device together: checked from the
+ * occupancy calculator before the launch (PP_ERR_UNSUPPORTED otherwise). A wait that
+ * still cannot finish (e.g. other work holding the device) ends after a bounded spin
+ * with error bit 1 and NaN outputs, never a hang.
  * ------------------------------------------------------------------------- */
 typedef struct pp_decode_state {
   uint32_t router_ticket; /* internal: call epoch, advanced by one per call */
   uint32_t ready;         /* internal */
   uint32_t done;          /* internal */
-  uint32_t error;         /* non-zero: a wait timed out, output invalid */
+  uint32_t error;         /* sticky error bits, 0 = none: 1 a logit-slot wait timed out,
+                             2 the selection was not a permutation of the experts; stays
+                             set until pp_decode_workspace_init clears it */
   int32_t k;              /* experts selected by the last call */
-  int32_t pad[3];
+  uint32_t error_call;    /* call epoch + 1 of the last failed call: that call wrote NaN outputs */
+  int32_t pad[2];
   float logits[PP_MAX_EXPERTS];
   int32_t sel_ids[PP_MAX_EXPERTS];   /* selected experts, descending probability */
   float sel_gates[PP_MAX_EXPERTS];   /* sigmoid(logit) of each selected expert */

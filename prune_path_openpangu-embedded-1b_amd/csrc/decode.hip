@@ -33,6 +33,8 @@
 // completion (s_waitcnt vmcnt(0)) before the dependent atomic. Agent-scope fences are
 // avoided on purpose: on gfx950 each one writes back and invalidates the L2, which
 // hundreds of workgroups cannot afford inside a 5 us kernel.
+#include <mutex>
+
 #include "pp_common.h"
 
 // Waves per workgroup of the general kernel: eight while the registers fit 256 per lane
@@ -73,20 +75,27 @@ __device__ __forceinline__ uint32_t add_rlx(uint32_t* p, uint32_t v) {
 // Call N adds into set N & 1 and its last workgroup only reads it; the workgroups of
 // call N+1 clear set N & 1 early in the call, off the critical path, so call N+2
 // finds it zero. 64-bit logit slots follow the two sets.
-__device__ __forceinline__ float* dec_acc_set(float* acc, int H, uint32_t epoch) {
-  return acc + (size_t)(epoch & 1u) * DEC_NCOPY * H;
+// hs: the stride of one accumulator copy (H for a caller's workspace; the largest
+// supported H for the library's own scratch, so calls of different H share its layout).
+__device__ __forceinline__ float* dec_acc_set(float* acc, int hs, uint32_t epoch) {
+  return acc + (size_t)(epoch & 1u) * DEC_NCOPY * hs;
 }
-__device__ __forceinline__ unsigned long long* dec_slots(float* acc, int H) {
-  return (unsigned long long*)(acc + (size_t)2 * DEC_NCOPY * H);
+__device__ __forceinline__ unsigned long long* dec_slots(float* acc, int hs) {
+  return (unsigned long long*)(acc + (size_t)2 * DEC_NCOPY * hs);
 }
 // this workgroup's share of clearing the other set (the previous call's)
 // (the first ncopy copies of it: the ones the kernel uses)
-__device__ __forceinline__ void dec_clear_previous(float* acc, int H, uint32_t epoch, int b, int W, int tid,
-                                                   int nthreads, int ncopy = DEC_NCOPY) {
-  float* prev = dec_acc_set(acc, H, epoch + 1u);
+// (hclear values of each copy: the previous call's H, or the whole stride when the
+// previous call's H is not known)
+__device__ __forceinline__ void dec_clear_previous(float* acc, int hs, int hclear, uint32_t epoch, int b, int W,
+                                                   int tid, int nthreads, int ncopy = DEC_NCOPY) {
+  float* prev = dec_acc_set(acc, hs, epoch + 1u);
   int lo, hi;
-  pp_split((uint32_t)(ncopy * H), (uint32_t)W, (uint32_t)b, lo, hi);
-  for (int i = lo + tid; i < hi; i += nthreads) st_rlx(prev + i, 0.0f);
+  pp_split((uint32_t)(ncopy * hclear), (uint32_t)W, (uint32_t)b, lo, hi);
+  for (int i = lo + tid; i < hi; i += nthreads) {
+    const int c = (int)((uint32_t)i / (uint32_t)hclear);
+    st_rlx(prev + (size_t)c * hs + (i - c * hclear), 0.0f);
+  }
 }
 
 // 8 bf16 packed in a uint4: dot with x[8], or acc += a * w
@@ -184,7 +193,7 @@ template <typename XT, int CPL, bool LOCAL>
 __global__ __launch_bounds__(DecNW<CPL>::NT) void decode_kernel(
     const XT* __restrict__ x, int H, const float* __restrict__ router, const float* __restrict__ bias,
     int E, int G, float tau, const bf16_t* __restrict__ rows, bf16_t* __restrict__ out,
-    pp_decode_state* __restrict__ st, float* __restrict__ acc, int R) {
+    pp_decode_state* __restrict__ st, float* __restrict__ acc, int hs, int hclear) {
   constexpr int NW = DecNW<CPL>::NW, NT = DecNW<CPL>::NT;
   extern __shared__ __align__(16) float red[];  // [NW][H] wave partials
   __shared__ SelScratch ss;
@@ -243,7 +252,7 @@ __global__ __launch_bounds__(DecNW<CPL>::NT) void decode_kernel(
     // epoch + 1; the last workgroup of the call stores it as the new epoch. No counter
     // is shared while routing (192 increments of one address serialise at the memory
     // side), and no second round trip for a published selection.
-    unsigned long long* slots = dec_slots(acc, H);
+    unsigned long long* slots = dec_slots(acc, hs);
     const uint32_t tag = epoch + 1u;
     if (b < E) {
       // H <= 4096: at most 16 elements per thread, all loaded before the first FMA
@@ -281,6 +290,7 @@ __global__ __launch_bounds__(DecNW<CPL>::NT) void decode_kernel(
         __builtin_amdgcn_s_sleep(1);
         if (++n > DEC_SPIN_LIMIT) {
           __hip_atomic_fetch_or(&st->error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          st_rlx(&st->error_call, epoch + 1u);
           break;
         }
         v = ld_rlx(&slots[j]);
@@ -294,13 +304,23 @@ __global__ __launch_bounds__(DecNW<CPL>::NT) void decode_kernel(
     } else {
       select_one_token_wg([&](int j) { return lg_s[j]; }, E, tau, &ss, keys_s, red4, tid, NT);
     }
-    const int kq = ss.k;
+    // a selection that is not a permutation of the experts (a broken sort; never, for a
+    // correct one) streams nothing and raises the error flag: the output is NaN, not a
+    // wrong-but-plausible layer
+    const bool bad = E > 16 && ss.bad;
+    const int kq = bad ? 0 : ss.k;
     for (int q = tid; q < kq; q += NT) {
-      const int e = (int)min((unsigned)ss.order[q], (unsigned)(E - 1));  // (in range by construction; clamped: it addresses HBM)
+      const int e = ss.order[q];
       sel_ids_s[q] = e;
       sel_g_s[q] = pp_sigmoid(lg_s[e]);
     }
-    if (tid == 0) k_s = kq;
+    if (tid == 0) {
+      k_s = kq;
+      if (bad) {
+        __hip_atomic_fetch_or(&st->error, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        st_rlx(&st->error_call, epoch + 1u);
+      }
+    }
     __syncthreads();
     if (b == 0) {  // telemetry for the caller: logits and selection of this call
       for (int j = tid; j < E; j += NT) st_rlx(&st->logits[j], lg_s[j]);
@@ -327,7 +347,7 @@ __global__ __launch_bounds__(DecNW<CPL>::NT) void decode_kernel(
       xr[c][i] = bf16_to_f32(f32_to_bf16(vx));
     }
   }
-  dec_clear_previous(acc, H, epoch, b, W, tid, NT);
+  dec_clear_previous(acc, hs, hclear, epoch, b, W, tid, NT);
 
   // ---------------- stream the selected neuron records
   // this workgroup: records [v0, v1) of the k*G selected ones; wave wv a contiguous
@@ -411,7 +431,7 @@ __global__ __launch_bounds__(DecNW<CPL>::NT) void decode_kernel(
   }
   __syncthreads();
   if (has_work) {
-    float* accc = dec_acc_set(acc, H, epoch) + (size_t)(b % DEC_NCOPY) * H;
+    float* accc = dec_acc_set(acc, hs, epoch) + (size_t)(b % DEC_NCOPY) * hs;
     for (int h = tid; h < H; h += NT) {
       float sv = red[h];
 #pragma unroll
@@ -427,14 +447,15 @@ __global__ __launch_bounds__(DecNW<CPL>::NT) void decode_kernel(
     // DEC_FOLD_H values of h per thread per pass, every load of a pass issued before
     // the first add (one round trip per pass; one pass for H <= 2048)
     constexpr int DEC_FOLD_H = 8;
-    const float* accs = dec_acc_set(acc, H, epoch);
+    const float* accs = dec_acc_set(acc, hs, epoch);
+    const bool failed = ld_rlx(&st->error_call) == epoch + 1u;  // set before this call's tickets
     for (int h0 = 0; h0 < H; h0 += NT * DEC_FOLD_H) {
       float sv[DEC_FOLD_H][DEC_NCOPY];
 #pragma unroll
       for (int i = 0; i < DEC_FOLD_H; ++i) {
         const int h = h0 + tid + i * NT;
 #pragma unroll
-        for (int c = 0; c < DEC_NCOPY; ++c) sv[i][c] = h < H ? ld_rlx(accs + (size_t)c * H + h) : 0.0f;
+        for (int c = 0; c < DEC_NCOPY; ++c) sv[i][c] = h < H ? ld_rlx(accs + (size_t)c * hs + h) : 0.0f;
       }
 #pragma unroll
       for (int i = 0; i < DEC_FOLD_H; ++i) {
@@ -443,7 +464,7 @@ __global__ __launch_bounds__(DecNW<CPL>::NT) void decode_kernel(
           float tot = 0.0f;
 #pragma unroll
           for (int c = 0; c < DEC_NCOPY; ++c) tot += sv[i][c];
-          out[h] = f32_to_bf16(tot);
+          out[h] = failed ? (bf16_t)0x7fc0 : f32_to_bf16(tot);
         }
       }
     }
@@ -517,7 +538,7 @@ template <typename XT, int CPL, int NW>
 __global__ __launch_bounds__(64 * NW) void decode16_kernel(
     const XT* __restrict__ x, const float* __restrict__ router, const float* __restrict__ bias, int G, float tau,
     const bf16_t* __restrict__ rows, bf16_t* __restrict__ out, pp_decode_state* __restrict__ st,
-    float* __restrict__ acc) {
+    float* __restrict__ acc, int hs, int hclear) {
   constexpr int H = 512 * CPL;
   constexpr int HC = H / 8;
   constexpr int NT = 64 * NW;
@@ -732,7 +753,7 @@ __global__ __launch_bounds__(64 * NW) void decode16_kernel(
     if (tid == 0) st_rlx(&st->k, k);
   }
 
-  dec_clear_previous(acc, H, epoch, b, W, tid, NT, DEC16_NCOPY);
+  dec_clear_previous(acc, hs, hclear, epoch, b, W, tid, NT, DEC16_NCOPY);
 
   // ---- stream the selected neuron records (as decode_kernel)
   const bool spec_used = spec_s != 0;
@@ -807,7 +828,7 @@ __global__ __launch_bounds__(64 * NW) void decode16_kernel(
       dst[1] = make_float4(oacc[c][4], oacc[c][5], oacc[c][6], oacc[c][7]);
     }
     __syncthreads();
-    float* accc = dec_acc_set(acc, H, epoch) + (b % DEC16_NCOPY) * H;
+    float* accc = dec_acc_set(acc, hs, epoch) + (b % DEC16_NCOPY) * hs;
 #pragma unroll
     for (int i = 0; i < (H + NT - 1) / NT; ++i) {
       const int h = tid + NT * i;
@@ -826,14 +847,15 @@ __global__ __launch_bounds__(64 * NW) void decode16_kernel(
   if (flag_s) {  // last workgroup: fold copies, write bf16, advance the epoch, reset the counter
     // every load of the fold is issued before the first add (one round trip)
     constexpr int HPT = (H + NT - 1) / NT;
-    const float* accs = dec_acc_set(acc, H, epoch);
+    const float* accs = dec_acc_set(acc, hs, epoch);
+    const bool failed = ld_rlx(&st->error_call) == epoch + 1u;  // (no wait here; a shared workspace's flag)
     float sv[HPT][DEC16_NCOPY];
 #pragma unroll
     for (int i = 0; i < HPT; ++i)
 #pragma unroll
       for (int c = 0; c < DEC16_NCOPY; ++c) {
         const int h = tid + NT * i;
-        sv[i][c] = h < H ? ld_rlx(accs + c * H + h) : 0.0f;
+        sv[i][c] = h < H ? ld_rlx(accs + c * hs + h) : 0.0f;
       }
 #pragma unroll
     for (int i = 0; i < HPT; ++i) {
@@ -842,7 +864,7 @@ __global__ __launch_bounds__(64 * NW) void decode16_kernel(
         float tot = 0.0f;
 #pragma unroll
         for (int c = 0; c < DEC16_NCOPY; ++c) tot += sv[i][c];
-        out[h] = f32_to_bf16(tot);
+        out[h] = failed ? (bf16_t)0x7fc0 : f32_to_bf16(tot);
       }
     }
     if (tid == 0) {
@@ -872,15 +894,53 @@ extern "C" int pp_decode_workspace_init(void* workspace, int H, int E, void* str
   return pp_check_launch("pp_decode_workspace_init");
 }
 
+// The published-logit mode needs its E router workgroups resident together (each
+// gathers every router workgroup's slot; the dispatcher starts workgroups in index
+// order, so waiting workgroups beyond the first E cannot block them). Checked once per
+// kernel variant and device from the occupancy calculator; PP_ERR_UNSUPPORTED when the
+// device cannot hold E such workgroups at once.
+static int dec_check_coresident(const void* kern, int nt, size_t smem, int E) {
+  static std::mutex mu;
+  static struct { const void* k; int dev; size_t smem; int cap; } cache[64];
+  static int n_cache = 0;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = -1;
+  int cap = -1;
+  {
+    std::lock_guard<std::mutex> lk(mu);
+    for (int i = 0; i < n_cache; ++i)
+      if (cache[i].k == kern && cache[i].dev == dev && cache[i].smem == smem) cap = cache[i].cap;
+  }
+  if (cap < 0) {
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, nt, smem) != hipSuccess) {
+      (void)hipGetLastError();
+      per_cu = 0;
+    }
+    cap = per_cu * pp_device_cus();
+    std::lock_guard<std::mutex> lk(mu);
+    if (n_cache < 64) cache[n_cache++] = {kern, dev, smem, cap};
+  }
+  PP_REQUIRE(cap >= E, PP_ERR_UNSUPPORTED,
+             "pp_moe_decode: the device holds %d decode workgroups at once, fewer than the %d router "
+             "workgroups that must be resident together", cap, E);
+  return PP_OK;
+}
+
 template <typename XT, bool LOCAL>
-static void launch_decode(int cpl, int grid, hipStream_t s, const XT* x, int H, const float* router,
-                          const float* bias, int E, int G, float tau, const bf16_t* rows, bf16_t* out,
-                          pp_decode_state* st, float* acc, int R) {
+static int launch_decode(int cpl, int grid, hipStream_t s, const XT* x, int H, const float* router,
+                         const float* bias, int E, int G, float tau, const bf16_t* rows, bf16_t* out,
+                         pp_decode_state* st, float* acc, int hs, int hclear) {
 #define PP_DEC_CASE(C)                                                                                  \
-  case C:                                                                                               \
-    decode_kernel<XT, C, LOCAL><<<grid, DecNW<C>::NT, (size_t)DecNW<C>::NW * H * sizeof(float), s>>>(x, H, router, bias, E, G, tau, rows, out, st, \
-                                                                acc, R);                                \
-    break;
+  case C: {                                                                                             \
+    const size_t sm = (size_t)DecNW<C>::NW * H * sizeof(float);                                         \
+    if (!LOCAL) {                                                                                       \
+      const int rc = dec_check_coresident((const void*)decode_kernel<XT, C, LOCAL>, DecNW<C>::NT, sm, E); \
+      if (rc) return rc;                                                                                \
+    }                                                                                                   \
+    decode_kernel<XT, C, LOCAL><<<grid, DecNW<C>::NT, sm, s>>>(x, H, router, bias, E, G, tau, rows, out, st, acc, \
+                                                               hs, hclear);                              \
+  } break;
   switch (cpl) {
     PP_DEC_CASE(1)
     PP_DEC_CASE(2)
@@ -892,26 +952,30 @@ static void launch_decode(int cpl, int grid, hipStream_t s, const XT* x, int H, 
     PP_DEC_CASE(8)
   }
 #undef PP_DEC_CASE
+  return PP_OK;
 }
 
-extern "C" int pp_moe_decode(const void* x, int x_dtype, int H, const float* router_packed, const float* bias,
-                             int E, int G, float tau, const void* packed, void* out_bf16, void* workspace,
-                             int grid, void* stream) {
+static int decode_check_args(const void* x, int x_dtype, int H, const float* router_packed, int E, int G,
+                             const void* packed, void* out_bf16, int grid) {
   int rc = pp_check_shape(H, E, G);
   if (rc) return rc;
-  PP_REQUIRE(x && router_packed && packed && out_bf16 && workspace, PP_ERR_INVALID,
-             "pp_moe_decode: null pointer");
+  PP_REQUIRE(x && router_packed && packed && out_bf16, PP_ERR_INVALID, "pp_moe_decode: null pointer");
   PP_REQUIRE(x_dtype == PP_DTYPE_F32 || x_dtype == PP_DTYPE_BF16, PP_ERR_INVALID, "pp_moe_decode: x_dtype %d",
              x_dtype);
   PP_REQUIRE(grid >= 0 && grid <= 65536, PP_ERR_INVALID, "pp_moe_decode: grid %d", grid);
+  return PP_OK;
+}
+
+// The launch shared by both entry points: st / acc = the state and the accumulators of
+// the workspace in use, hs = the stride of one accumulator copy, hclear = how much of
+// each copy of the previous call's set to clear.
+static int decode_dispatch(const void* x, int x_dtype, int H, const float* router_packed, const float* bias,
+                           int E, int G, float tau, const void* packed, void* out_bf16, pp_decode_state* st,
+                           float* acc, int hs, int hclear, int grid, hipStream_t s) {
   const int grid_in = grid;
-  const int R = E;  // router workgroups: one expert each
   if (grid == 0) grid = pp_device_cus();
-  if (grid < R) grid = R;  // every expert has its router workgroup
+  if (grid < E) grid = E;  // every expert has its router workgroup
   const int cpl = (H / 8 + 63) / 64;  // 16-byte chunks per lane per row (H <= 4096 -> <= 8)
-  pp_decode_state* st = (pp_decode_state*)workspace;
-  float* acc = (float*)((char*)workspace + dec_acc_offset());
-  hipStream_t s = (hipStream_t)stream;
   if (E == 16 && H % 512 == 0) {
     const int c = H / 512;
     const size_t smem16 = (size_t)DEC16_NW * H * sizeof(float);
@@ -920,10 +984,10 @@ extern "C" int pp_moe_decode(const void* x, int x_dtype, int H, const float* rou
   case C:                                                                                                    \
     if (x_dtype == PP_DTYPE_F32)                                                                             \
       decode16_kernel<float, C, DEC16_NW><<<grid, 64 * DEC16_NW, smem16, s>>>((const float*)x, router_packed, bias, G, tau, \
-                                                               (const bf16_t*)packed, (bf16_t*)out_bf16, st, acc); \
+                                                               (const bf16_t*)packed, (bf16_t*)out_bf16, st, acc, hs, hclear); \
     else                                                                                                     \
       decode16_kernel<bf16_t, C, DEC16_NW><<<grid, 64 * DEC16_NW, smem16, s>>>((const bf16_t*)x, router_packed, bias, G, tau, \
-                                                                (const bf16_t*)packed, (bf16_t*)out_bf16, st, acc); \
+                                                                (const bf16_t*)packed, (bf16_t*)out_bf16, st, acc, hs, hclear); \
     break;
     switch (c) {
       PP_DEC16_CASE(1)
@@ -941,12 +1005,26 @@ extern "C" int pp_moe_decode(const void* x, int x_dtype, int H, const float* rou
   const bool local = E <= 16 && (int64_t)16 * H <= DEC_LOCAL_ROUTER_FLOATS;
   const bf16_t* rows = (const bf16_t*)packed;
   bf16_t* o = (bf16_t*)out_bf16;
+  int rc;
   if (x_dtype == PP_DTYPE_F32) {
-    if (local) launch_decode<float, true>(cpl, grid, s, (const float*)x, H, router_packed, bias, E, G, tau, rows, o, st, acc, R);
-    else launch_decode<float, false>(cpl, grid, s, (const float*)x, H, router_packed, bias, E, G, tau, rows, o, st, acc, R);
+    if (local) rc = launch_decode<float, true>(cpl, grid, s, (const float*)x, H, router_packed, bias, E, G, tau, rows, o, st, acc, hs, hclear);
+    else rc = launch_decode<float, false>(cpl, grid, s, (const float*)x, H, router_packed, bias, E, G, tau, rows, o, st, acc, hs, hclear);
   } else {
-    if (local) launch_decode<bf16_t, true>(cpl, grid, s, (const bf16_t*)x, H, router_packed, bias, E, G, tau, rows, o, st, acc, R);
-    else launch_decode<bf16_t, false>(cpl, grid, s, (const bf16_t*)x, H, router_packed, bias, E, G, tau, rows, o, st, acc, R);
+    if (local) rc = launch_decode<bf16_t, true>(cpl, grid, s, (const bf16_t*)x, H, router_packed, bias, E, G, tau, rows, o, st, acc, hs, hclear);
+    else rc = launch_decode<bf16_t, false>(cpl, grid, s, (const bf16_t*)x, H, router_packed, bias, E, G, tau, rows, o, st, acc, hs, hclear);
   }
+  if (rc) return rc;
   return pp_check_launch("pp_moe_decode");
+}
+
+extern "C" int pp_moe_decode(const void* x, int x_dtype, int H, const float* router_packed, const float* bias,
+                             int E, int G, float tau, const void* packed, void* out_bf16, void* workspace,
+                             int grid, void* stream) {
+  int rc = decode_check_args(x, x_dtype, H, router_packed, E, G, packed, out_bf16, grid);
+  if (rc) return rc;
+  PP_REQUIRE(workspace, PP_ERR_INVALID, "pp_moe_decode: null workspace");
+  pp_decode_state* st = (pp_decode_state*)workspace;
+  float* acc = (float*)((char*)workspace + dec_acc_offset());
+  return decode_dispatch(x, x_dtype, H, router_packed, bias, E, G, tau, packed, out_bf16, st, acc, H, H, grid,
+                         (hipStream_t)stream);
 }

@@ -183,6 +183,7 @@ struct SelScratch {
   int stk[3 * 24];             // introsort range stack (tie path only)
   int k;                       // number of selected experts
   int tie;                     // a tie group straddles the selection boundary
+  int bad;                     // select_one_token_wg: the ranks are not a permutation (never, for a correct sort)
 };
 
 // Descending comparator of torch's CPU sort on (value, index) pairs (NaN first).
@@ -652,6 +653,7 @@ static __device__ void select_one_token_wg(LG lg, int E, float tau, SelScratch* 
   const int nwk = (E + 63) >> 6;  // waves holding keys
   unsigned long long key = tid < E ? sel_key(pt, tid) : ~0ull;
   if (tid < E) ss->e[tid] = pt;
+  if (tid == 0) ss->bad = 0;
   if (wv < nwk) {
 #pragma unroll
     for (int k2 = 2; k2 <= 64; k2 <<= 1)
@@ -664,8 +666,10 @@ static __device__ void select_one_token_wg(LG lg, int E, float tau, SelScratch* 
     keys[tid] = key;
   }
   wg_lds_barrier();
-  if (wv < nwk && key != ~0ull) {
-    int rank = lane;
+  const bool holder = wv < nwk && key != ~0ull;
+  int rank = lane;
+  const int idx = (int)(uint32_t)key;
+  if (holder) {
     for (int w2 = 0; w2 < nwk; ++w2) {
       if (w2 == wv) continue;
       const unsigned long long* run = keys + 64 * w2;
@@ -675,13 +679,17 @@ static __device__ void select_one_token_wg(LG lg, int E, float tau, SelScratch* 
       lo += (lo == 63 && run[63] < key) ? 1 : 0;
       rank += lo;
     }
-    const int idx = (int)(uint32_t)key;
-    if (rank < E && idx < E) {  // always, for a correct sort; guards the LDS and the ids
+    if (rank < E && idx < E) {  // always, for a correct sort (else ss->bad below)
       ss->srt[rank] = ss->e[idx];
       ss->order[rank] = idx;
     }
   }
   wg_lds_barrier();
+  // Permutation check: E keys, each written to its rank; a lost or duplicated key makes
+  // two writers share a rank, and one of them reads back the other's id. No collision
+  // and every rank in [0, E) means ss->order is a permutation. A failed check is
+  // reported through ss->bad (the caller turns it into an error), never used silently.
+  if (holder && !(rank < E && idx < E && ss->order[rank] == idx)) ss->bad = 1;
   if (tid < PP_WAVE) {
     constexpr int QPL = PP_MAX_EXPERTS / PP_WAVE;  // sorted positions per lane
     float v[QPL];
@@ -719,13 +727,15 @@ static __device__ void select_one_token_wg(LG lg, int E, float tau, SelScratch* 
     }
     if (lane == 0) {
       ss->k = k;
-      const int tie = (k < E && ss->srt[k - 1] == ss->srt[k]) ? 1 : 0;
-      ss->tie = tie;
-      if (tie) {
-        for (int j = 0; j < E; ++j) { ss->srt[j] = ss->e[j]; ss->order[j] = j; }
-        kv_introsort(ss->srt, ss->order, E, ss->stk);
-      }
+      ss->tie = (k < E && ss->srt[k - 1] == ss->srt[k]) ? 1 : 0;
     }
   }
   wg_lds_barrier();
+  if (ss->tie) {  // uniform; after the permutation check, which reads ss->order
+    if (tid == 0) {
+      for (int j = 0; j < E; ++j) { ss->srt[j] = ss->e[j]; ss->order[j] = j; }
+      kv_introsort(ss->srt, ss->order, E, ss->stk);
+    }
+    wg_lds_barrier();
+  }
 }

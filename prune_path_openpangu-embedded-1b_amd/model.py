@@ -53,20 +53,39 @@ def experts_masks_from_ids(ids, num_experts: int, dtype=torch.float32) -> torch.
 
 
 class MoELayer(nn.Module):
-    """The reference's masked routing layer (src/MoEBlock_origin.py:110-214): the router
-    projection and the expert partition under the reference's names, and its forward
-    ``(hidden_states, intermediate) -> (intermediate * mask, probs | None)``."""
+    """The reference's masked routing layer (src/MoEBlock.py:106-200, with the origin
+    twin src/MoEBlock_origin.py:108-214): the router projection and the expert partition
+    under the reference's names, and its forward
+    ``(hidden_states, intermediate) -> (intermediate * mask, probs | None)``.
 
-    def __init__(self, hidden_size: int, intermediate_size: int, experts: int, tau: float = 0.95,
-                 experts_id=None):
+    Constructor as in the reference, ``MoELayer(config, train_args, experts,
+    experts_id=None)``: the width is ``config.intermediate_size`` (the reference uses
+    ``config.hidden_size * 4``, the same number for openPangu-Embedded-1B, and
+    ``hidden_size * 4`` here too when the config has no ``intermediate_size``); the
+    router ``Linear(hidden_size, experts, bias=False)`` starts at zero
+    (``router_weights_init``, src/MoEBlock.py:98-103); ``tau`` comes from
+    ``train_args.tau`` (default 0.95); ``experts_id`` (neuron -> expert, default
+    contiguous blocks) builds the one-hot ``experts_masks`` [E, I].
+
+    Telemetry (src/MoEBlock.py:145-162, 187-196): eval forwards add the per-expert
+    activation counts to ``activated_statistics``; after
+    ``reset_moe_sparsity_statistics()`` they also add the number of dropped (token,
+    expert) gates to ``sparsity_accumulator`` and the number of gates to
+    ``element_counter``, all on the device (no host sync); ``get_sparsity_statistics()``
+    returns ``(element_counter, sparsity_accumulator)`` as Python numbers."""
+
+    def __init__(self, config: Any, train_args: Any, experts: int, experts_id=None):
         super().__init__()
-        if intermediate_size % experts:
-            raise ValueError("intermediate_size must be divisible by the number of experts")
+        self.config = config
+        self.train_args = train_args
         self.experts = experts
-        self.dimension = intermediate_size
-        self.dimension_per_expert = intermediate_size // experts
-        self.tau = tau
-        self.mlp_router = nn.Sequential(nn.Linear(hidden_size, experts, bias=False))
+        hidden = config.hidden_size
+        self.dimension = getattr(config, "intermediate_size", None) or hidden * 4
+        self.mlp_router = nn.Sequential(nn.Linear(hidden, experts, bias=False))
+        nn.init.zeros_(self.mlp_router[0].weight)
+        if self.dimension % experts:
+            raise ValueError(f"MoELayer: dimension {self.dimension} is not divisible by {experts} experts")
+        self.dimension_per_expert = self.dimension // experts
         if experts_id is None:
             experts_id = np.repeat(np.arange(experts), self.dimension_per_expert)
         self.register_buffer("experts_masks", experts_masks_from_ids(experts_id, experts,
@@ -74,6 +93,18 @@ class MoELayer(nn.Module):
         self.register_buffer("activated_statistics", torch.zeros(experts, dtype=torch.long))
         self.register_buffer("sparsity_accumulator", torch.zeros(1, dtype=torch.double))
         self.register_buffer("element_counter", torch.zeros(1, dtype=torch.long))
+        self.sparsity_tracking_enabled = False
+        self.tau = getattr(train_args, "tau", 0.95)
+
+    def reset_moe_sparsity_statistics(self) -> None:
+        """Zero the sparsity counters and start tracking (src/MoEBlock.py:154-158)."""
+        self.sparsity_tracking_enabled = True
+        self.sparsity_accumulator.zero_()
+        self.element_counter.zero_()
+
+    def get_sparsity_statistics(self):
+        """(gates seen, gates dropped) since the last reset (src/MoEBlock.py:160-162)."""
+        return self.element_counter.item(), self.sparsity_accumulator.item()
 
     def expert_ids(self) -> torch.Tensor:
         """Neuron -> expert id [I] (argmax over the one-hot masks, src/openpangu_moe.py:229-230)."""
@@ -106,7 +137,13 @@ class MoELayer(nn.Module):
                                                                               device=score.device))
         probs = torch.softmax(score, dim=-1) if self.training else None
         if not self.training:
-            self.activated_statistics.add_(sel.reshape(-1, E).sum(dim=0))
+            flat = sel.reshape(-1, E)
+            self.activated_statistics.add_(flat.sum(dim=0))
+            if self.sparsity_tracking_enabled:
+                # dropped gates: experts_prob <= 0 (src/MoEBlock.py:193-196); a selected
+                # expert's gate is sigmoid(score) > 0 unless the score is -inf or NaN
+                self.sparsity_accumulator.add_((experts_prob <= 0.0).sum())
+                self.element_counter.add_(experts_prob.numel())
         out = ops.masked_gate(intermediate, experts_prob, self._layout())
         return out, probs
 
@@ -141,7 +178,7 @@ class IntegratedOpenPanguMoEMLP(nn.Module):
             self.down_proj = nn.Linear(I, H, bias=False)
             self.act_fn = nn.SiLU()
         self.penalize_logits_list = penalize_logits_list
-        self.moelayer = MoELayer(H, I, E, tau=getattr(train_args, "tau", 0.95))
+        self.moelayer = MoELayer(config, train_args, E)
         self.tau_moe = TauSparseMoE(H, I, E, G, tau)
 
     def forward(self, hidden_states: torch.Tensor, *args, **kwargs) -> torch.Tensor:

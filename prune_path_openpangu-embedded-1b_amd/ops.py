@@ -212,6 +212,14 @@ def decode_workspace(H: int, E: int, device) -> torch.Tensor:
     """Allocate and zero (with a kernel, once) a decode workspace."""
     n = int(L.lib().pp_decode_workspace_bytes(H, E))
     ws = torch.empty(n, dtype=torch.uint8, device=device)
+    return decode_workspace_init(ws, H, E)
+
+
+def decode_workspace_init(ws: torch.Tensor, H: int, E: int) -> torch.Tensor:
+    """Zero a decode workspace in place (first use, or to clear its error flag)."""
+    if ws.dtype != torch.uint8 or ws.numel() < int(L.lib().pp_decode_workspace_bytes(H, E)):
+        raise RuntimeError("prunepath.decode_workspace_init: workspace too small")
+    _need_gpu("decode_workspace_init", ws)
     rc = L.lib().pp_decode_workspace_init(_vp(ws), H, E, _stream(ws))
     L.check(rc, "decode_workspace_init")
     return ws

@@ -23,6 +23,13 @@ Differences by design (each a documented build choice, not an omission):
   calls ``total_tiles.item()``, :581).
 * Every neuron of every selected expert is computed (the reference decode grid
   covers only 64 neurons per expert, :398-399, 515).
+* Decode failures are not silent (the reference has no failure reporting): a decode
+  kernel that cannot complete its wait, or whose selection is inconsistent, sets a
+  sticky error flag in the decode workspace and writes NaN outputs from then on.
+  ``decode_error()`` reads the flag, ``check_decode()`` raises when it is set, and
+  ``checked = True`` runs that check after every decode call (a host sync, so off by
+  default; graph-captured serving loops check between replays instead);
+  ``reset_decode_error()`` clears it.
 """
 from __future__ import annotations
 
@@ -60,6 +67,7 @@ class TauSparseMoE(nn.Module):
         self.register_buffer("router_packed", None, persistent=False)
         self.register_buffer("decode_workspace", None, persistent=False)
         self._packed_key = None
+        self.checked = False
 
     # ------------------------------------------------------------------ packing
     def _weights_key(self):
@@ -125,10 +133,32 @@ class TauSparseMoE(nn.Module):
         self._packed_key = self._weights_key()
         return self
 
+    # ------------------------------------------------------------------ decode errors
+    def decode_error(self) -> int:
+        """Sticky error bits of the decode workspace (0 = none; 1 = a logit wait timed
+        out, 2 = inconsistent selection). Synchronises with the device."""
+        if self.decode_workspace is None:
+            return 0
+        return ops.decode_state(self.decode_workspace, self.num_experts)["error"]
+
+    def check_decode(self) -> None:
+        """Raise RuntimeError if a decode call of this module failed (its outputs are NaN)."""
+        err = self.decode_error()
+        if err:
+            raise RuntimeError(f"TauSparseMoE: decode failed (error bits {err:#x}); outputs since the failure "
+                               "are NaN -- reset_decode_error() clears the flag")
+
+    def reset_decode_error(self) -> None:
+        """Re-initialise the decode workspace (clears the error flag)."""
+        if self.decode_workspace is not None:
+            ops.decode_workspace_init(self.decode_workspace, self.hidden_size, self.num_experts)
+
     # ------------------------------------------------------------------ forward
     def forward_decode(self, x_flat: torch.Tensor, B: int, L: int, H: int) -> torch.Tensor:
         out = ops.moe_decode(x_flat, self.router_packed, self.router_bias, self.num_experts, self.group_size,
                              self.tau, self.packed_experts, self.decode_workspace)
+        if self.checked:
+            self.check_decode()
         return out.view(B, L, H)
 
     def forward_prefill(self, N: int, x_flat: torch.Tensor, B: int, L: int, H: int) -> torch.Tensor:

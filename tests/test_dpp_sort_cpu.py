@@ -1,0 +1,160 @@
+"""CPU restatement of the workgroup rank computation of the E > 16 decode selection
+(select_one_token_wg in csrc/pp_common.h): per 64-lane wave a bitonic sort of 64-bit
+keys whose partner exchanges use DPP lane moves for xor 1, 2 and 8 and the LDS permute
+otherwise, then each key's rank = its place in its run + the number of smaller keys in
+every other run (binary search). No GPU.
+
+The DPP lane maps are written from the ISA definitions of the two controls the kernel
+uses (lane i of the result reads source lane src[i]):
+* quad_perm [p0, p1, p2, p3]: src[i] = 4 * (i // 4) + p[i % 4];
+* row_ror:n: inside each 16-lane row, the row rotated by n lanes. The direction is the
+  thing that once went wrong (a two-rotation xor 4 that assumed the opposite direction
+  lost keys), so every check below runs under BOTH directions, and the kernel only uses
+  row_ror:8, which is direction-free.
+
+Checks: each DPP exchange the kernel uses is the permutation lane i <-> lane i ^ j
+(an involution pairing i with i ^ j) under either rotation direction; row_ror:4 is not
+i ^ 4 under either direction (why the kernel keeps xor 4 on the LDS permute); the whole
+rank computation equals a plain sort of the keys on random, tie-heavy, all-equal and NaN
+rows for E = 17 .. 256 (a permutation of 0 .. E-1 with no lost or duplicated key).
+"""
+import numpy as np
+import pytest
+
+WAVE = 64
+
+
+def quad_perm(p):
+    return np.array([4 * (i // 4) + p[i % 4] for i in range(WAVE)])
+
+
+def row_ror(n, direction):
+    # direction +1: lane i reads lane i + n of its row; -1: lane i - n
+    return np.array([16 * (i // 16) + (i % 16 + direction * n) % 16 for i in range(WAVE)])
+
+
+XOR1 = [1, 0, 3, 2]  # PP_DPP_XOR1 = 0xB1: quad_perm fields 1,0,3,2 (2 bits each, lane 0 first)
+XOR2 = [2, 3, 0, 1]  # PP_DPP_XOR2 = 0x4E
+
+
+def _decode_quad_perm(ctrl):
+    return [(ctrl >> (2 * k)) & 3 for k in range(4)]
+
+
+def lane_maps(direction):
+    """Source lane of every lane for the partner exchange of distance j, as the kernel
+    does it (key_xor): DPP for j = 1, 2, 8, the LDS permute (exact xor) otherwise."""
+    m = {1: quad_perm(XOR1), 2: quad_perm(XOR2), 8: row_ror(8, direction)}
+    for j in (4, 16, 32):
+        m[j] = np.arange(WAVE) ^ j
+    return m
+
+
+def test_dpp_controls_encode_the_quad_perms():
+    assert _decode_quad_perm(0xB1) == XOR1
+    assert _decode_quad_perm(0x4E) == XOR2
+
+
+@pytest.mark.parametrize("direction", [+1, -1])
+def test_dpp_exchanges_pair_lane_i_with_i_xor_j(direction):
+    lanes = np.arange(WAVE)
+    for j, src in lane_maps(direction).items():
+        np.testing.assert_array_equal(src, lanes ^ j, err_msg=f"j={j}")
+        np.testing.assert_array_equal(src[src], lanes)  # an involution: a pairing
+
+
+@pytest.mark.parametrize("direction", [+1, -1])
+def test_row_ror4_is_not_xor4(direction):
+    assert not np.array_equal(row_ror(4, direction), np.arange(WAVE) ^ 4)
+
+
+def sel_key(p, j):
+    """The kernel's 64-bit rank key: ~bits(p) << 32 | j, NaN mapped to all ones first."""
+    b = p.view(np.uint32).astype(np.uint64)
+    b = np.where(np.isnan(p), np.uint64(0xFFFFFFFF), b)
+    return ((~b & np.uint64(0xFFFFFFFF)) << np.uint64(32)) | j.astype(np.uint64)
+
+
+def wg_ranks(keys, maps):
+    """select_one_token_wg's rank step on E keys (E <= 256): per wave a bitonic sort with
+    the given exchange maps, then ranks by binary search over the other waves' runs.
+    Returns order[rank] = expert id (-1 where no key landed) and the collision flag."""
+    E = keys.size
+    nwk = (E + WAVE - 1) // WAVE
+    allk = np.full(nwk * WAVE, np.uint64(0xFFFFFFFFFFFFFFFF))
+    allk[:E] = keys
+    runs = allk.reshape(nwk, WAVE).copy()
+    lanes = np.arange(WAVE)
+    for w in range(nwk):
+        key = runs[w]
+        k2 = 2
+        while k2 <= WAVE:
+            j = k2 >> 1
+            while j > 0:
+                o = key[maps[j]]
+                keep_min = ((lanes & j) == 0) == ((lanes & k2) == 0)
+                key = np.where(keep_min, np.minimum(o, key), np.maximum(o, key))
+                j >>= 1
+            k2 <<= 1
+        runs[w] = key
+    order = np.full(E, -1, np.int64)
+    writes = np.zeros(E, np.int64)
+    for w in range(nwk):
+        for lane in range(WAVE):
+            key = runs[w, lane]
+            if key == np.uint64(0xFFFFFFFFFFFFFFFF):
+                continue
+            rank = lane
+            for w2 in range(nwk):
+                if w2 == w:
+                    continue
+                run = runs[w2]
+                lo = 0
+                step = 32
+                while step >= 1:
+                    lo += step if run[lo + step - 1] < key else 0
+                    step >>= 1
+                lo += 1 if (lo == 63 and run[63] < key) else 0
+                rank += lo
+            idx = int(key & np.uint64(0xFFFFFFFF))
+            if rank < E and idx < E:
+                order[rank] = idx
+                writes[rank] += 1
+    return order, bool((writes != 1).any())
+
+
+def _rows(E, rng):
+    yield rng.standard_normal(E).astype(np.float32)
+    yield (rng.integers(-2, 3, E) * 0.25).astype(np.float32)          # many exact ties
+    yield np.full(E, np.float32(1.0 / E))                              # all equal: index order
+    p = rng.random(E).astype(np.float32)
+    p[rng.choice(E, 3, replace=False)] = np.nan                        # NaN first
+    yield p
+    yield np.zeros(E, np.float32)
+
+
+@pytest.mark.parametrize("direction", [+1, -1])
+@pytest.mark.parametrize("E", [17, 24, 32, 63, 64, 65, 100, 127, 128, 129, 191, 192, 200, 255, 256])
+def test_wg_ranks_equal_a_plain_sort(E, direction):
+    rng = np.random.default_rng(E * 3 + (direction > 0))
+    maps = lane_maps(direction)
+    for p in _rows(E, rng):
+        keys = sel_key(p, np.arange(E))
+        order, collided = wg_ranks(keys, maps)
+        assert not collided
+        np.testing.assert_array_equal(order, np.argsort(keys, kind="stable"))
+        # torch's descending order with NaN first and equal values by index
+        assert sorted(order.tolist()) == list(range(E))
+
+
+def test_a_wrong_exchange_is_caught_by_the_permutation_check():
+    """The failure mode the kernel now reports instead of hiding: xor 4 done as one
+    row rotation by 4 loses keys, two keys share a rank and the collision flag is set
+    (the kernel raises its error flag and streams nothing)."""
+    E = 192
+    rng = np.random.default_rng(1)
+    maps = lane_maps(+1)
+    maps[4] = row_ror(4, +1)
+    keys = sel_key(rng.standard_normal(E).astype(np.float32), np.arange(E))
+    order, collided = wg_ranks(keys, maps)
+    assert collided and (order == -1).any()

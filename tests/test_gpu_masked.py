@@ -154,21 +154,32 @@ def test_masked_mlp_training_step_vs_reference(pkg, H, I, G, tau):
 
 def test_masked_layer_eval_statistics(pkg):
     """Eval-mode MoELayer.forward (the reference's origin path) counts the selections per
-    expert in activated_statistics and returns no probabilities."""
+    expert in activated_statistics and returns no probabilities; after
+    reset_moe_sparsity_statistics the dropped / total gate counts accumulate on the device
+    (src/MoEBlock.py:154-162, 187-196)."""
+    import types
     H, I, E = 256, 1024, 16
-    layer = pkg.MoELayer(H, I, E, tau=0.7).to(dev())
+    cfg = types.SimpleNamespace(hidden_size=H, intermediate_size=I)
+    layer = pkg.MoELayer(cfg, types.SimpleNamespace(tau=0.7), E).to(dev())
+    assert float(layer.mlp_router[0].weight.abs().sum()) == 0.0  # router_weights_init: zeros
     with torch.no_grad():
         layer.mlp_router[0].weight.normal_(0, 0.1)
     layer.eval()
     x = torch.randn(3, 5, H, device=dev())
     inter = torch.randn(3, 5, I, device=dev())
+    assert layer.get_sparsity_statistics() == (0, 0.0)
+    layer.reset_moe_sparsity_statistics()
     with torch.no_grad():
         out, probs = layer(x, inter)
+        layer(x[:1], inter[:1])
     assert probs is None
     with torch.no_grad():
         score = layer.mlp_router(x).reshape(-1, E).cpu().numpy()
     sel = oracle.select(score, 0.7)
-    np.testing.assert_array_equal(layer.activated_statistics.cpu().numpy(), sel.mask.sum(0))
+    sel1 = oracle.select(score.reshape(3, 5, E)[:1].reshape(-1, E), 0.7)
+    np.testing.assert_array_equal(layer.activated_statistics.cpu().numpy(), sel.mask.sum(0) + sel1.mask.sum(0))
+    n, dropped = layer.get_sparsity_statistics()
+    assert n == 20 * E and dropped == float(20 * E - sel.mask.sum() - sel1.mask.sum())
     ids = layer.expert_ids().cpu().numpy()
     ref = inter.cpu().numpy().reshape(-1, I) * sel.gates[:, ids]
     np.testing.assert_allclose(out.cpu().numpy().reshape(-1, I), ref, rtol=1e-6, atol=1e-7)

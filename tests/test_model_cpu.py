@@ -95,3 +95,26 @@ def test_load_cluster_ids_reference_format(pkg, tmp_path):
     np.savetxt(bad, np.array([0.0, 1.5]))
     with pytest.raises(ValueError):
         pkg.load_cluster_ids(str(bad))
+
+
+def test_moelayer_reference_constructor_and_statistics(pkg):
+    """MoELayer(config, train_args, experts, experts_id=None) as in src/MoEBlock.py:106-162:
+    width from the config (hidden_size * 4 when it has no intermediate_size), zero router,
+    tau from train_args (0.95 default), contiguous default partition, counters that reset
+    and report (element_counter, sparsity_accumulator)."""
+    cfg = types.SimpleNamespace(hidden_size=64)
+    m = pkg.MoELayer(cfg, types.SimpleNamespace(), 8)
+    assert m.dimension == 256 and m.dimension_per_expert == 32 and m.tau == 0.95
+    assert m.mlp_router[0].weight.shape == (8, 64) and float(m.mlp_router[0].weight.abs().sum()) == 0.0
+    np.testing.assert_array_equal(m.expert_ids().numpy(), np.repeat(np.arange(8), 32))
+    ids = np.random.default_rng(0).permutation(np.repeat(np.arange(8), 32))
+    m2 = pkg.MoELayer(types.SimpleNamespace(hidden_size=64, intermediate_size=256),
+                      types.SimpleNamespace(tau=0.7), 8, experts_id=ids)
+    assert m2.tau == 0.7
+    np.testing.assert_array_equal(m2.expert_ids().numpy(), ids)
+    assert m2.get_sparsity_statistics() == (0, 0.0) and not m2.sparsity_tracking_enabled
+    m2.element_counter.fill_(5)
+    m2.reset_moe_sparsity_statistics()
+    assert m2.sparsity_tracking_enabled and m2.get_sparsity_statistics() == (0, 0.0)
+    with pytest.raises(ValueError):
+        pkg.MoELayer(types.SimpleNamespace(hidden_size=64, intermediate_size=250), types.SimpleNamespace(), 8)
