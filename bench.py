@@ -15,8 +15,11 @@ tokens/s + MFMA util.
 * prefill: N=2048 tokens, tau=0.70; tokens/s of the whole
   prefill path and MFMA utilisation of the two grouped GEMMs
   (FLOPs = P*6*H*G over selected pairs P, no padding) against 2.5 PFLOP/s bf16 dense.
-* cpu_baseline: the oracle's dense masked layer (oracle/oracle.py masked_moe_mlp,
-  numpy float64) on one token per call, timed on this host for ~10 s.
+* cpu_baseline: the reference's own CPU path, restated op for op in torch fp32
+  (oracle/torch_masked.py: dense gate/up over all neurons, softmax_thresholding, the
+  expert mask, down), timed on this host with all allowed threads and with one thread,
+  median of >= 20 runs after warm-up, for decode bs=1, bs=16/64 (tau 0.95, Zipf bias) and
+  prefill 2048 (tau 0.70); value = decode bs=1 on all threads, us per layer-token.
 * roofline.traffic: HBM bytes per decode launch from rocprofv3 FETCH_SIZE and
   WRITE_SIZE (two --pmc runs of this script with --calibrate-copy-mib), each scaled
   by the ratio of known bytes to the same counter on a plain elementwise pass of
@@ -54,7 +57,7 @@ def parse():
     ap.add_argument("--prefill-reps", type=int, default=20)
     ap.add_argument("--prefill-zipf", action="store_true",
                     help="prefill section with the config-3 router bias (log Zipf(1.2)), e.g. for profiling small batches")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-runs", type=int, default=20, help="timed calls per CPU-baseline configuration")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-extra", action="store_true",
@@ -106,6 +109,74 @@ def read_traffic():
         if line.startswith("hbm_bytes_per_launch:"):
             return float(line.split(":", 1)[1])
     return None
+
+
+def _cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or "unknown"
+
+
+def _allowed_threads() -> int:
+    """Cores this process may use: the affinity mask, capped by OMP_NUM_THREADS when set
+    (the GPU box grants each job a share of the host)."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    omp = os.environ.get("OMP_NUM_THREADS")
+    return max(1, min(n, int(omp))) if omp and omp.isdigit() else n
+
+
+def cpu_baseline(args):
+    """The reference's CPU path (oracle/torch_masked.py, torch fp32, op for op
+    src/openpangu_moe_origin.py:96-118 + src/MoEBlock_origin.py:188-212) on the BASELINE
+    shapes: median wall time of >= 20 calls after 3 warm-up calls, per configuration, with
+    all allowed threads and with one thread. One-thread prefill runs a 256-token sample per
+    call (the dense layer's time is linear in tokens) scaled to 2048 tokens."""
+    import numpy as np
+    import torch
+
+    import inputs as gi
+    from oracle.torch_masked import MaskedLayer
+    w = gi.layer_weights(0)
+    plain = MaskedLayer(w["w_gate"], w["w_up"], w["w_down"], w["w_router"], w["expert_ids"])
+    zipf = MaskedLayer(w["w_gate"], w["w_up"], w["w_down"], w["w_router"], w["expert_ids"], bias=gi.zipf_bias(E))
+    rng = np.random.default_rng(5)
+    cfgs = [("decode_bs1", 1, 0.70, plain), ("bs16", 16, 0.95, zipf), ("bs64", 64, 0.95, zipf),
+            ("prefill2048", 2048, 0.70, plain)]
+    n_all = _allowed_threads()
+    out = {}
+    t_start = time.perf_counter()
+    for threads in (n_all, 1):
+        torch.set_num_threads(threads)
+        for name, n, tau, layer in cfgs:
+            n_run = 256 if (threads == 1 and n > 256) else n
+            x = torch.from_numpy(rng.standard_normal((n_run, H)).astype(np.float32))
+            for _ in range(3):
+                layer(x, tau)
+            ts = []
+            for _ in range(args.cpu_runs):
+                t0 = time.perf_counter()
+                layer(x, tau)
+                ts.append(time.perf_counter() - t0)
+            us = float(np.median(ts)) * 1e6 * (n / n_run)
+            out.setdefault(name, {"tokens": n, "tau": tau, "router_bias": "zipf(1.2)" if layer is zipf else None})
+            out[name][f"threads_{threads}" if threads == 1 else "threads_all"] = {
+                "us_per_call": us, "us_per_token": us / n, "runs": args.cpu_runs,
+                "sample_tokens_per_call": n_run}
+    torch.set_num_threads(n_all)
+    d = out["decode_bs1"]
+    return {"value": d["threads_all"]["us_per_call"], "unit": "us/layer", "cores": n_all, "kind": "port",
+            "sample": (f"oracle/torch_masked.py (torch fp32 dense masked layer, the reference's CPU path), "
+                       f"H={H} E={E} G={G}; median of {args.cpu_runs} calls per configuration after 3 warm-up "
+                       f"calls; value = decode bs=1 tau 0.70 on {n_all} threads; "
+                       f"{time.perf_counter() - t_start:.1f} s of CPU work in total"),
+            "threads_1_value": d["threads_1"]["us_per_call"],
+            "cpu_model": _cpu_model(), "torch_cpu_capability": torch.backends.cpu.get_cpu_capability(),
+            "torch_threads": n_all, "configs": out}
 
 
 def main():
@@ -417,23 +488,8 @@ def main():
         torch.cuda.empty_cache()
         extra["decoder_stack"] = pkg.decoder_stack.run(prompt_len=1024, steps=128, layers=26, tau=args.tau)
 
-    # ---------------- CPU baseline: oracle dense masked layer, one token per call
-    cpu = None
-    if not args.no_cpu:
-        from oracle import oracle
-        wl = gi.layer_weights(0)
-        rng = np.random.default_rng(0)
-        n, t0 = 0, time.perf_counter()
-        while time.perf_counter() - t0 < args.cpu_seconds or n < 3:
-            xc = rng.standard_normal((1, H)).astype(np.float32)
-            oracle.masked_moe_mlp(xc, wl["w_gate"], wl["w_up"], wl["w_down"], wl["w_router"], wl["expert_ids"],
-                                  args.tau)
-            n += 1
-        el = time.perf_counter() - t0
-        threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-        cpu = {"value": el / n * 1e6, "unit": "us/layer", "cores": threads, "kind": "port",
-               "sample": f"{n} decode tokens (1 per call) through oracle.masked_moe_mlp "
-                         f"(dense masked layer, numpy float64), H={H}, E={E}, G={G}, tau={args.tau}"}
+    # ---------------- CPU baseline: the reference's dense masked layer, torch fp32 on the host
+    cpu = None if args.no_cpu else cpu_baseline(args)
 
     res = {
         "metric": METRIC, "value": us_per_step, "unit": "us/layer", "n_gpus": 1, "steps": K, "warmup": W,

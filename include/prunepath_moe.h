@@ -121,7 +121,9 @@ int pp_bucket(const uint8_t* mask, const float* gates, int64_t n_tokens, int E, 
 /* ------------------------------------------------------------------------- *
  * Decode (N == 1): one fused kernel -- router GEMV (fp32), selection, gate/up
  * GEMVs over the selected experts' neurons, silu(g)*u*gate, down GEMV and the
- * cross-workgroup fp32 reduction, bf16 output.
+ * cross-workgroup reduction in 64-bit fixed point (value * 2^32: the sum does not
+ * depend on the order the workgroups finish in, so the bf16 output is the same bits on
+ * every call), bf16 output.
  * Replaces TauSparseMoE.forward_decode with moe_router_select_kernel_decode and
  * moe_decode_swiglu_fused_kernel (src/tl_kernel_optimized_Ultimate_PanGU.py:335-462, 494-530).
  * The workspace (pp_decode_workspace_bytes) must be zeroed once with
@@ -141,9 +143,11 @@ typedef struct pp_decode_state {
   uint32_t router_ticket; /* internal: call epoch, advanced by one per call */
   uint32_t ready;         /* internal */
   uint32_t done;          /* internal */
-  uint32_t error;         /* sticky error bits, 0 = none: 1 a logit-slot wait timed out,
-                             2 the selection was not a permutation of the experts; stays
-                             set until pp_decode_workspace_init clears it */
+  uint32_t error;         /* sticky error bits, 0 = none: 1 a logit-slot wait timed out
+                             (every later call on the workspace writes NaN), 2 the selection
+                             was not a permutation of the experts, 4 a workgroup partial sum
+                             was not finite or reached 2^30 (beyond the fixed-point
+                             reduction); stays set until pp_decode_workspace_init clears it */
   int32_t k;              /* experts selected by the last call */
   uint32_t error_call;    /* call epoch + 1 of the last failed call: that call wrote NaN outputs */
   int32_t pad[2];

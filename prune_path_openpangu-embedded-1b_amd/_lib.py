@@ -11,6 +11,8 @@ import subprocess
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libprunepath_moe.so")
+# torch.library registration of the ops (csrc/torch_ops.cpp), linked against LIB_PATH
+TORCH_LIB_PATH = os.path.join(_HERE, "libprunepath_torch.so")
 CSRC = os.path.join(_HERE, "csrc")
 
 PP_OK = 0
@@ -64,8 +66,9 @@ SIGNATURES = {
 
 
 def build(jobs: int = 8) -> str:
-    """Compile libprunepath_moe.so for gfx950 with csrc/Makefile (always recompiles
-    what changed; hipcc cross-compiles without a GPU)."""
+    """Compile libprunepath_moe.so (hipcc, gfx950; cross-compiles without a GPU) and the
+    torch.library extension libprunepath_torch.so (g++) with csrc/Makefile, recompiling
+    what changed."""
     subprocess.run(["make", "-s", "-C", CSRC, f"-j{jobs}"], check=True)
     return LIB_PATH
 
@@ -84,6 +87,22 @@ def lib():
             fn.argtypes = args
         _lib = handle
     return _lib
+
+
+_ops = None
+
+
+def torch_ops():
+    """``torch.ops.prunepath`` with the C++ extension loaded; raises if it has not been built."""
+    global _ops
+    if _ops is None:
+        lib()  # the C ABI library first (the extension resolves it by soname)
+        if not os.path.exists(TORCH_LIB_PATH):
+            raise RuntimeError(f"prunepath: {TORCH_LIB_PATH} is missing -- build it (make -C {CSRC})")
+        import torch
+        torch.ops.load_library(TORCH_LIB_PATH)
+        _ops = torch.ops.prunepath
+    return _ops
 
 
 def check(rc: int, what: str) -> None:

@@ -54,7 +54,7 @@ struct DecNW {
 #define DEC_SPIN_LIMIT (1u << 22)
 #define DEC_LOCAL_ROUTER_FLOATS 32768  // Epad*H at or below this: every workgroup routes
 
-static inline size_t dec_acc_offset() { return (sizeof(pp_decode_state) + 255) / 256 * 256; }
+static constexpr size_t dec_acc_offset() { return (sizeof(pp_decode_state) + 255) / 256 * 256; }
 
 
 __device__ __forceinline__ void vm_wait() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
@@ -70,32 +70,56 @@ __device__ __forceinline__ uint32_t add_rlx(uint32_t* p, uint32_t v) {
   return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Accumulators: two sets of DEC_NCOPY x H fp32, used by alternate calls (parity of the
+// Accumulators hold 64-bit fixed point (value * 2^32, two's complement). Integer
+// addition is associative, so the sum of the workgroups' partials has the same bits
+// whatever order their atomics land in: the decode output is bitwise reproducible.
+// A partial must stay below 2^30 in magnitude (finite): the sum of up to 2^31 such
+// partials cannot overflow, and the quantisation step 2^-32 per partial is far below the
+// bf16 output's resolution. A partial outside that range sets error bit 4 and the call's
+// output is NaN (never a wrapped value).
+typedef unsigned long long dec_acc_t;
+#define DEC_FIXED_SCALE 0x1p32
+__device__ __forceinline__ float dec_from_fixed(dec_acc_t v) {
+  return (float)((double)(long long)v * (1.0 / DEC_FIXED_SCALE));
+}
+
+// Accumulators: two sets of DEC_NCOPY x H fixed-point words, used by alternate calls (parity of the
 // call epoch, st->router_ticket, which the last workgroup of every call advances).
 // Call N adds into set N & 1 and its last workgroup only reads it; the workgroups of
 // call N+1 clear set N & 1 early in the call, off the critical path, so call N+2
 // finds it zero. 64-bit logit slots follow the two sets.
-// hs: the stride of one accumulator copy (H for a caller's workspace; the largest
-// supported H for the library's own scratch, so calls of different H share its layout).
-__device__ __forceinline__ float* dec_acc_set(float* acc, int hs, uint32_t epoch) {
+// hs: the stride of one accumulator copy (H for a caller's workspace; a fixed larger
+// stride keeps one layout for a workspace shared by calls of different H).
+__device__ __forceinline__ dec_acc_t* dec_acc_set(dec_acc_t* acc, int hs, uint32_t epoch) {
   return acc + (size_t)(epoch & 1u) * DEC_NCOPY * hs;
 }
-__device__ __forceinline__ unsigned long long* dec_slots(float* acc, int hs) {
+__device__ __forceinline__ unsigned long long* dec_slots(dec_acc_t* acc, int hs) {
   return (unsigned long long*)(acc + (size_t)2 * DEC_NCOPY * hs);
 }
 // this workgroup's share of clearing the other set (the previous call's)
 // (the first ncopy copies of it: the ones the kernel uses)
 // (hclear values of each copy: the previous call's H, or the whole stride when the
 // previous call's H is not known)
-__device__ __forceinline__ void dec_clear_previous(float* acc, int hs, int hclear, uint32_t epoch, int b, int W,
+__device__ __forceinline__ void dec_clear_previous(dec_acc_t* acc, int hs, int hclear, uint32_t epoch, int b, int W,
                                                    int tid, int nthreads, int ncopy = DEC_NCOPY) {
-  float* prev = dec_acc_set(acc, hs, epoch + 1u);
+  dec_acc_t* prev = dec_acc_set(acc, hs, epoch + 1u);
   int lo, hi;
   pp_split((uint32_t)(ncopy * hclear), (uint32_t)W, (uint32_t)b, lo, hi);
   for (int i = lo + tid; i < hi; i += nthreads) {
     const int c = (int)((uint32_t)i / (uint32_t)hclear);
-    st_rlx(prev + (size_t)c * hs + (i - c * hclear), 0.0f);
+    st_rlx(prev + (size_t)c * hs + (i - c * hclear), (dec_acc_t)0);
   }
+}
+
+// Add one partial (fp32) to a fixed-point accumulator; out-of-range partials flag the call.
+__device__ __forceinline__ void dec_acc_add(dec_acc_t* p, float v, pp_decode_state* st, uint32_t epoch) {
+  if (!(fabsf(v) < 0x1p30f)) {  // also NaN
+    __hip_atomic_fetch_or(&st->error, 4u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    st_rlx(&st->error_call, epoch + 1u);
+    v = 0.0f;
+  }
+  __hip_atomic_fetch_add(p, (dec_acc_t)__double2ll_rn((double)v * DEC_FIXED_SCALE), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // 8 bf16 packed in a uint4: dot with x[8], or acc += a * w
@@ -193,7 +217,7 @@ template <typename XT, int CPL, bool LOCAL>
 __global__ __launch_bounds__(DecNW<CPL>::NT) void decode_kernel(
     const XT* __restrict__ x, int H, const float* __restrict__ router, const float* __restrict__ bias,
     int E, int G, float tau, const bf16_t* __restrict__ rows, bf16_t* __restrict__ out,
-    pp_decode_state* __restrict__ st, float* __restrict__ acc, int hs, int hclear) {
+    pp_decode_state* __restrict__ st, dec_acc_t* __restrict__ acc, int hs, int hclear) {
   constexpr int NW = DecNW<CPL>::NW, NT = DecNW<CPL>::NT;
   extern __shared__ __align__(16) float red[];  // [NW][H] wave partials
   __shared__ SelScratch ss;
@@ -431,12 +455,12 @@ __global__ __launch_bounds__(DecNW<CPL>::NT) void decode_kernel(
   }
   __syncthreads();
   if (has_work) {
-    float* accc = dec_acc_set(acc, hs, epoch) + (size_t)(b % DEC_NCOPY) * hs;
+    dec_acc_t* accc = dec_acc_set(acc, hs, epoch) + (size_t)(b % DEC_NCOPY) * hs;
     for (int h = tid; h < H; h += NT) {
       float sv = red[h];
 #pragma unroll
       for (int w = 1; w < NW; ++w) sv += red[(size_t)w * H + h];
-      unsafeAtomicAdd(accc + h, sv);
+      dec_acc_add(accc + h, sv, st, epoch);
     }
   }
   vm_wait();  // every wave's accumulator atomics are performed before the ticket
@@ -447,24 +471,24 @@ __global__ __launch_bounds__(DecNW<CPL>::NT) void decode_kernel(
     // DEC_FOLD_H values of h per thread per pass, every load of a pass issued before
     // the first add (one round trip per pass; one pass for H <= 2048)
     constexpr int DEC_FOLD_H = 8;
-    const float* accs = dec_acc_set(acc, hs, epoch);
-    const bool failed = ld_rlx(&st->error_call) == epoch + 1u;  // set before this call's tickets
+    const dec_acc_t* accs = dec_acc_set(acc, hs, epoch);
+    const bool failed = ld_rlx(&st->error_call) == epoch + 1u || (ld_rlx(&st->error) & 1u) != 0u;
     for (int h0 = 0; h0 < H; h0 += NT * DEC_FOLD_H) {
-      float sv[DEC_FOLD_H][DEC_NCOPY];
+      dec_acc_t sv[DEC_FOLD_H][DEC_NCOPY];
 #pragma unroll
       for (int i = 0; i < DEC_FOLD_H; ++i) {
         const int h = h0 + tid + i * NT;
 #pragma unroll
-        for (int c = 0; c < DEC_NCOPY; ++c) sv[i][c] = h < H ? ld_rlx(accs + (size_t)c * hs + h) : 0.0f;
+        for (int c = 0; c < DEC_NCOPY; ++c) sv[i][c] = h < H ? ld_rlx(accs + (size_t)c * hs + h) : (dec_acc_t)0;
       }
 #pragma unroll
       for (int i = 0; i < DEC_FOLD_H; ++i) {
         const int h = h0 + tid + i * NT;
         if (h < H) {
-          float tot = 0.0f;
+          dec_acc_t tot = 0;
 #pragma unroll
           for (int c = 0; c < DEC_NCOPY; ++c) tot += sv[i][c];
-          out[h] = failed ? (bf16_t)0x7fc0 : f32_to_bf16(tot);
+          out[h] = failed ? (bf16_t)0x7fc0 : f32_to_bf16(dec_from_fixed(tot));
         }
       }
     }
@@ -538,7 +562,7 @@ template <typename XT, int CPL, int NW>
 __global__ __launch_bounds__(64 * NW) void decode16_kernel(
     const XT* __restrict__ x, const float* __restrict__ router, const float* __restrict__ bias, int G, float tau,
     const bf16_t* __restrict__ rows, bf16_t* __restrict__ out, pp_decode_state* __restrict__ st,
-    float* __restrict__ acc, int hs, int hclear) {
+    dec_acc_t* __restrict__ acc, int hs, int hclear) {
   constexpr int H = 512 * CPL;
   constexpr int HC = H / 8;
   constexpr int NT = 64 * NW;
@@ -828,7 +852,7 @@ __global__ __launch_bounds__(64 * NW) void decode16_kernel(
       dst[1] = make_float4(oacc[c][4], oacc[c][5], oacc[c][6], oacc[c][7]);
     }
     __syncthreads();
-    float* accc = dec_acc_set(acc, hs, epoch) + (b % DEC16_NCOPY) * hs;
+    dec_acc_t* accc = dec_acc_set(acc, hs, epoch) + (b % DEC16_NCOPY) * hs;
 #pragma unroll
     for (int i = 0; i < (H + NT - 1) / NT; ++i) {
       const int h = tid + NT * i;
@@ -836,7 +860,7 @@ __global__ __launch_bounds__(64 * NW) void decode16_kernel(
         float v = red[h];
 #pragma unroll
         for (int w = 1; w < NW; ++w) v += red[w * H + h];
-        unsafeAtomicAdd(accc + h, v);
+        dec_acc_add(accc + h, v, st, epoch);
       }
     }
   }
@@ -847,24 +871,24 @@ __global__ __launch_bounds__(64 * NW) void decode16_kernel(
   if (flag_s) {  // last workgroup: fold copies, write bf16, advance the epoch, reset the counter
     // every load of the fold is issued before the first add (one round trip)
     constexpr int HPT = (H + NT - 1) / NT;
-    const float* accs = dec_acc_set(acc, hs, epoch);
-    const bool failed = ld_rlx(&st->error_call) == epoch + 1u;  // (no wait here; a shared workspace's flag)
-    float sv[HPT][DEC16_NCOPY];
+    const dec_acc_t* accs = dec_acc_set(acc, hs, epoch);
+    const bool failed = ld_rlx(&st->error_call) == epoch + 1u || (ld_rlx(&st->error) & 1u) != 0u;
+    dec_acc_t sv[HPT][DEC16_NCOPY];
 #pragma unroll
     for (int i = 0; i < HPT; ++i)
 #pragma unroll
       for (int c = 0; c < DEC16_NCOPY; ++c) {
         const int h = tid + NT * i;
-        sv[i][c] = h < H ? ld_rlx(accs + c * hs + h) : 0.0f;
+        sv[i][c] = h < H ? ld_rlx(accs + c * hs + h) : (dec_acc_t)0;
       }
 #pragma unroll
     for (int i = 0; i < HPT; ++i) {
       const int h = tid + NT * i;
       if (h < H) {
-        float tot = 0.0f;
+        dec_acc_t tot = 0;
 #pragma unroll
         for (int c = 0; c < DEC16_NCOPY; ++c) tot += sv[i][c];
-        out[h] = failed ? (bf16_t)0x7fc0 : f32_to_bf16(tot);
+        out[h] = failed ? (bf16_t)0x7fc0 : f32_to_bf16(dec_from_fixed(tot));
       }
     }
     if (tid == 0) {
@@ -879,10 +903,10 @@ __global__ void decode_ws_clear_kernel(uint32_t* p, size_t n_words) {
     p[i] = 0u;
 }
 
-// state | 2 x DEC_NCOPY x H fp32 accumulators | PP_MAX_EXPERTS 64-bit logit slots
+// state | 2 x DEC_NCOPY x H fixed-point accumulators | PP_MAX_EXPERTS 64-bit logit slots
 extern "C" size_t pp_decode_workspace_bytes(int H, int E) {
   (void)E;
-  return dec_acc_offset() + (size_t)2 * DEC_NCOPY * H * sizeof(float) + PP_MAX_EXPERTS * sizeof(unsigned long long);
+  return dec_acc_offset() + (size_t)2 * DEC_NCOPY * H * sizeof(dec_acc_t) + PP_MAX_EXPERTS * sizeof(unsigned long long);
 }
 
 extern "C" int pp_decode_workspace_init(void* workspace, int H, int E, void* stream) {
@@ -899,7 +923,18 @@ extern "C" int pp_decode_workspace_init(void* workspace, int H, int E, void* str
 // order, so waiting workgroups beyond the first E cannot block them). Checked once per
 // kernel variant and device from the occupancy calculator; PP_ERR_UNSUPPORTED when the
 // device cannot hold E such workgroups at once.
+static int dec_capacity(const void* kern, int nt, size_t smem);
 static int dec_check_coresident(const void* kern, int nt, size_t smem, int E) {
+  const int cap = dec_capacity(kern, nt, smem);
+  PP_REQUIRE(cap >= E, PP_ERR_UNSUPPORTED,
+             "pp_moe_decode: the device holds %d decode workgroups at once, fewer than the %d router "
+             "workgroups that must be resident together", cap, E);
+  return PP_OK;
+}
+
+// Workgroups of `kern` the current device holds at once (occupancy calculator), cached
+// per kernel, dynamic LDS size and device.
+static int dec_capacity(const void* kern, int nt, size_t smem) {
   static std::mutex mu;
   static struct { const void* k; int dev; size_t smem; int cap; } cache[64];
   static int n_cache = 0;
@@ -921,16 +956,13 @@ static int dec_check_coresident(const void* kern, int nt, size_t smem, int E) {
     std::lock_guard<std::mutex> lk(mu);
     if (n_cache < 64) cache[n_cache++] = {kern, dev, smem, cap};
   }
-  PP_REQUIRE(cap >= E, PP_ERR_UNSUPPORTED,
-             "pp_moe_decode: the device holds %d decode workgroups at once, fewer than the %d router "
-             "workgroups that must be resident together", cap, E);
-  return PP_OK;
+  return cap;
 }
 
 template <typename XT, bool LOCAL>
 static int launch_decode(int cpl, int grid, hipStream_t s, const XT* x, int H, const float* router,
                          const float* bias, int E, int G, float tau, const bf16_t* rows, bf16_t* out,
-                         pp_decode_state* st, float* acc, int hs, int hclear) {
+                         pp_decode_state* st, dec_acc_t* acc, int hs, int hclear) {
 #define PP_DEC_CASE(C)                                                                                  \
   case C: {                                                                                             \
     const size_t sm = (size_t)DecNW<C>::NW * H * sizeof(float);                                         \
@@ -971,7 +1003,7 @@ static int decode_check_args(const void* x, int x_dtype, int H, const float* rou
 // each copy of the previous call's set to clear.
 static int decode_dispatch(const void* x, int x_dtype, int H, const float* router_packed, const float* bias,
                            int E, int G, float tau, const void* packed, void* out_bf16, pp_decode_state* st,
-                           float* acc, int hs, int hclear, int grid, hipStream_t s) {
+                           dec_acc_t* acc, int hs, int hclear, int grid, hipStream_t s) {
   const int grid_in = grid;
   if (grid == 0) grid = pp_device_cus();
   if (grid < E) grid = E;  // every expert has its router workgroup
@@ -1024,7 +1056,7 @@ extern "C" int pp_moe_decode(const void* x, int x_dtype, int H, const float* rou
   if (rc) return rc;
   PP_REQUIRE(workspace, PP_ERR_INVALID, "pp_moe_decode: null workspace");
   pp_decode_state* st = (pp_decode_state*)workspace;
-  float* acc = (float*)((char*)workspace + dec_acc_offset());
+  dec_acc_t* acc = (dec_acc_t*)((char*)workspace + dec_acc_offset());
   return decode_dispatch(x, x_dtype, H, router_packed, bias, E, G, tau, packed, out_bf16, st, acc, H, H, grid,
                          (hipStream_t)stream);
 }

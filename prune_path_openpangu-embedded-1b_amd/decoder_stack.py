@@ -166,24 +166,27 @@ class DecoderStack(nn.Module):
             x = blk(x)
         return self.lm_head(self.norm(x[:, -1:]))
 
-    def step_static(self, tok_t, pos_t, moe: bool = True):
+    def step_static(self, tok_t, pos_t, moe: bool = True, finite_t=None):
         """One greedy decode step on device state: token ``tok_t`` [1, 1] at position
-        ``pos_t`` [1]; writes the next token into ``tok_t`` and advances ``pos_t``."""
+        ``pos_t`` [1]; writes the next token into ``tok_t`` and advances ``pos_t``.
+        ``finite_t`` ([1] bool, optional) is and-ed with "every logit is finite"."""
         ar = torch.arange(self.layers[0].self_attn.max_len, device=tok_t.device)
         mask = torch.where(ar <= pos_t, 0.0, float("-inf")).to(torch.float32)
         x = self.embed_tokens(tok_t)
         for blk in self.layers:
             x = blk.forward_static(x, pos_t, mask, moe)
         logits = self.lm_head(self.norm(x))
+        if finite_t is not None:
+            finite_t.logical_and_(torch.isfinite(logits).all().view(1))
         tok_t.copy_(logits.argmax(-1))
         pos_t.add_(1)
 
 
 @torch.no_grad()
-def run(prompt_len: int = 1024, steps: int = 128, layers: int = 26, tau: float = 0.70, seed: int = 0,
-        device: str = "cuda:0") -> Dict[str, float]:
-    """Prefill ``prompt_len`` random token ids, then ``steps`` greedy decode steps at
-    batch 1. Returns per-step and prefill times and the MoE-MLP share."""
+def build(prompt_len: int = 1024, steps: int = 128, layers: int = 26, tau: float = 0.70, seed: int = 0,
+          device: str = "cuda:0"):
+    """The random-init bf16 stack, reordered for inference (fp32 routers), with empty KV
+    caches, and the random prompt ids [1, prompt_len]."""
     dev = torch.device(device)
     model = DecoderStack(layers=layers, max_len=prompt_len + steps).to(dev)
     model.init_random(seed)
@@ -196,6 +199,22 @@ def run(prompt_len: int = 1024, steps: int = 128, layers: int = 26, tau: float =
     g = torch.Generator(device="cpu")
     g.manual_seed(seed + 1)
     ids = torch.randint(0, VOCAB, (1, prompt_len), generator=g).to(dev)
+    return model, ids
+
+
+@torch.no_grad()
+def run(prompt_len: int = 1024, steps: int = 128, layers: int = 26, tau: float = 0.70, seed: int = 0,
+        device: str = "cuda:0", verify_steps: int = 3, moe_hook=None, moe_hook_steps: int = 0) -> Dict[str, float]:
+    """Prefill ``prompt_len`` random token ids, then ``steps`` greedy decode steps at
+    batch 1. Returns per-step and prefill times and the MoE-MLP share.
+
+    Checks: the first ``verify_steps`` graph replays give the eager steps' tokens
+    (``graph_replays_match_eager``) and every logit of those eager steps is finite
+    (``logits_finite``). ``moe_hook(layer, mlp, hidden, out)``, when given, is called for
+    every layer's MoE-MLP call of the first ``moe_hook_steps`` eager decode steps (e.g. to
+    check each call against an oracle)."""
+    dev = torch.device(device)
+    model, ids = build(prompt_len, steps, layers, tau, seed, device)
 
     def moe_ms():
         torch.cuda.synchronize()
@@ -219,16 +238,24 @@ def run(prompt_len: int = 1024, steps: int = 128, layers: int = 26, tau: float =
     nxt = logits.argmax(-1)
 
     checked = {}
+    finite_t = torch.ones(1, dtype=torch.bool, device=dev)
 
     def decode_ms(moe: bool) -> float:
         """One captured greedy step replayed ``steps`` times from the prompt's end; the
         first replays are checked token for token against eager steps from the same state."""
         tok_t = nxt.clone().view(1, 1)
         pos_t = torch.tensor([prompt_len], device=dev, dtype=torch.int64)
-        n_chk = min(3, steps)
+        n_chk = min(verify_steps, steps)
         eager = []
-        for _ in range(n_chk):
-            model.step_static(tok_t, pos_t, moe)
+        for i in range(n_chk):
+            handles = []
+            if moe and moe_hook is not None and i < moe_hook_steps:
+                for li, blk in enumerate(model.layers):
+                    handles.append(blk.mlp.register_forward_hook(
+                        lambda mod, args, out, li=li: moe_hook(li, mod, args[0], out)))
+            model.step_static(tok_t, pos_t, moe, finite_t)
+            for h in handles:
+                h.remove()
             eager.append(int(tok_t.item()))
         pos_t.fill_(prompt_len)
         tok_t.copy_(nxt.view(1, 1))
@@ -267,6 +294,7 @@ def run(prompt_len: int = 1024, steps: int = 128, layers: int = 26, tau: float =
         "decode_moe_ms_per_step": decode_moe, "decode_moe_share": decode_moe / decode_step,
         "decode_moe_us_per_layer": decode_moe / layers * 1000.0,
         "graph_replays_match_eager": bool(checked.get(True)) and bool(checked.get(False)),
+        "verified_steps": min(verify_steps, steps), "logits_finite": bool(finite_t.item()),
         "note": ("random-init bf16 weights, random prompt ids; prefill: events around each MoE-MLP call; "
                  "decode: one graph-captured greedy step (static-shape attention over the full cache) "
                  "replayed, MoE share = step time with minus without the MoE-MLP"),

@@ -1,13 +1,15 @@
 """Torch-level entry points over the C ABI (include/prunepath_moe.h).
 
-PyTorch only provides device memory and the current HIP stream here: every
-function checks shapes/devices, allocates its outputs with torch and calls the
-hand-written gfx950 kernels through ctypes. All work is enqueued on
-``torch.cuda.current_stream()``; nothing synchronises with the host, so the calls
-can be captured in a CUDA (HIP) graph.
-
-The same functions are registered as ``torch.library`` ops in the ``prunepath``
-namespace (``torch.ops.prunepath.route`` etc.) at the bottom of this file.
+PyTorch only provides device memory and the current HIP stream here. The hot-path
+ops -- ``route``, ``route_logits``, ``bucket``, ``pack_experts``, ``pack_router``,
+``decode_workspace_init``, ``moe_decode``, ``moe_prefill`` -- are ``torch.library``
+ops of the C++ extension ``libprunepath_torch.so`` (csrc/torch_ops.cpp, namespace
+``prunepath``: ``torch.ops.prunepath.route`` etc.), which checks arguments, allocates
+outputs and calls the C ABI; the functions below only adapt their results to
+dicts / defaults. The test-level stage entry points (``expert_gateup``,
+``expert_down``, ``combine``) and the masked-gate training kernels call the C ABI
+through ctypes. All work is enqueued on ``torch.cuda.current_stream()``; nothing
+synchronises with the host, so the calls can be captured in a CUDA (HIP) graph.
 """
 from __future__ import annotations
 
@@ -43,130 +45,48 @@ def _need_gpu(name: str, *ts: Optional[torch.Tensor]) -> None:
             raise RuntimeError(f"prunepath.{name}: tensors on different devices ({dev}, {t.device})")
 
 
-def _x_dtype(x: torch.Tensor):
-    """(tensor, PP dtype code) -- bf16 and fp32 pass through, other floats go to fp32."""
-    if x.dtype == torch.bfloat16:
-        return x, L.PP_DTYPE_BF16
-    if x.dtype == torch.float32:
-        return x, L.PP_DTYPE_F32
-    if x.is_floating_point():
-        return x.float(), L.PP_DTYPE_F32
-    raise RuntimeError(f"prunepath: unsupported input dtype {x.dtype}")
-
-
-def _src_dtype(t: torch.Tensor):
-    if t.dtype == torch.float32:
-        return L.PP_DTYPE_F32
-    if t.dtype == torch.bfloat16:
-        return L.PP_DTYPE_BF16
-    raise RuntimeError(f"prunepath: weights must be float32 or bfloat16, got {t.dtype}")
-
-
 # ----------------------------------------------------------------------------- rearrangement
 def packed_expert_numel(H: int, E: int, G: int) -> int:
     return int(L.lib().pp_packed_expert_bytes(H, E, G)) // 2
 
 
 def pack_experts(w_gate: torch.Tensor, w_up: torch.Tensor, w_down: torch.Tensor, E: int, G: int,
-                 perm: Optional[torch.Tensor] = None, layout: str = "linear",
-                 out: Optional[torch.Tensor] = None) -> torch.Tensor:
+                 perm: Optional[torch.Tensor] = None, layout: str = "linear") -> torch.Tensor:
     """One-time physical rearrangement (physical_reorder_for_inference,
-    src/openpangu_moe.py:212-256) into the packed bf16 expert buffer.
+    src/openpangu_moe.py:212-256) into the packed bf16 expert buffer
+    (``torch.ops.prunepath.pack_experts``).
 
     layout="linear": nn.Linear weights, gate/up [I,H], down [H,I].
     layout="tau":    TauSparseMoE buffers, W_gate/W_up [H,I], W_down [I,H].
     perm[j] (int32, device) = source neuron of rearranged neuron j (None = identity).
     """
-    if layout == "linear":
-        I, H = w_gate.shape
-        s_n, s_h, d_n, d_h = H, 1, 1, I
-        assert w_down.shape == (H, I)
-    elif layout == "tau":
-        H, I = w_gate.shape
-        s_n, s_h, d_n, d_h = 1, I, H, 1
-        assert w_down.shape == (I, H)
-    else:
-        raise ValueError(f"layout {layout!r}")
-    if w_up.shape != w_gate.shape or w_up.dtype != w_gate.dtype or w_down.dtype != w_gate.dtype:
-        raise RuntimeError("prunepath.pack_experts: gate/up/down shapes or dtypes disagree")
-    if I != E * G:
-        raise RuntimeError(f"prunepath.pack_experts: I={I} != E*G={E * G}")
-    if perm is not None:
-        if perm.dtype != torch.int32 or perm.numel() != I:
-            raise RuntimeError("prunepath.pack_experts: perm must be int32 [I]")
-    _need_gpu("pack_experts", w_gate, w_up, w_down, perm)
-    n = packed_expert_numel(H, E, G)
-    if out is None:
-        out = torch.empty(n, dtype=torch.bfloat16, device=w_gate.device)
-    elif out.numel() != n or out.dtype != torch.bfloat16:
-        raise RuntimeError("prunepath.pack_experts: bad out buffer")
-    rc = L.lib().pp_pack_experts(_vp(w_gate), _vp(w_up), s_n, s_h, _vp(w_down), d_n, d_h,
-                                 _src_dtype(w_gate), _vp(perm), H, E, G, _vp(out), _stream(w_gate))
-    L.check(rc, "pack_experts")
-    return out
+    return L.torch_ops().pack_experts(w_gate, w_up, w_down, E, G, perm, layout)
 
 
 def pack_router(w_router: torch.Tensor, layout: str = "linear") -> torch.Tensor:
     """Router weights to fp32 [Epad, H] (Epad = E rounded up to 16, zero rows).
     layout="linear": MoELayer router weight [E,H]; layout="tau": TauSparseMoE.router [H,E]."""
-    if layout == "linear":
-        E, H = w_router.shape
-        s_e, s_h = H, 1
-    elif layout == "tau":
-        H, E = w_router.shape
-        s_e, s_h = 1, E
-    else:
-        raise ValueError(f"layout {layout!r}")
-    _need_gpu("pack_router", w_router)
-    Epad = (E + 15) // 16 * 16
-    out = torch.empty(Epad, H, dtype=torch.float32, device=w_router.device)
-    rc = L.lib().pp_pack_router(_vp(w_router), s_e, s_h, _src_dtype(w_router), H, E, _vp(out),
-                                _stream(w_router))
-    L.check(rc, "pack_router")
-    return out
+    return L.torch_ops().pack_router(w_router, layout)
 
 
 # ----------------------------------------------------------------------------- routing
 def route(x: torch.Tensor, router_packed: torch.Tensor, E: int, tau: float,
           bias: Optional[torch.Tensor] = None, want_logits: bool = True, want_probs: bool = False):
-    """fp32 router + tau selection for x [N,H]. Returns dict with gates [N,E] fp32,
-    mask [N,E] uint8, count [N] int32 and optionally logits / probs [N,E] fp32."""
-    x, xd = _x_dtype(x)
-    N, H = x.shape
-    if bias is not None and (bias.dtype != torch.float32 or bias.numel() != E):
-        raise RuntimeError("prunepath.route: bias must be float32 [E]")
-    _need_gpu("route", x, router_packed, bias)
-    dev = x.device
-    res = {
-        "gates": torch.empty(N, E, dtype=torch.float32, device=dev),
-        "mask": torch.empty(N, E, dtype=torch.uint8, device=dev),
-        "count": torch.empty(N, dtype=torch.int32, device=dev),
-        "logits": torch.empty(N, E, dtype=torch.float32, device=dev) if want_logits else None,
-        "probs": torch.empty(N, E, dtype=torch.float32, device=dev) if want_probs else None,
-    }
-    rc = L.lib().pp_route(_vp(x), xd, N, H, _vp(router_packed), _vp(bias), E, float(tau),
-                          _vp(res["logits"]), _vp(res["probs"]), _vp(res["gates"]), _vp(res["mask"]),
-                          _vp(res["count"]), _stream(x))
-    L.check(rc, "route")
-    return res
+    """fp32 router + tau selection for x [N,H] (``torch.ops.prunepath.route``). Returns dict
+    with gates [N,E] fp32, mask [N,E] uint8, count [N] int32, logits and probs [N,E] fp32
+    (None unless asked for)."""
+    if x.dtype not in (torch.float32, torch.bfloat16) and x.is_floating_point():
+        x = x.float()
+    logits, probs, gates, mask, count = L.torch_ops().route(x, router_packed, bias, E, float(tau))
+    return {"gates": gates, "mask": mask, "count": count, "logits": logits if want_logits else None,
+            "probs": probs if want_probs else None}
 
 
 def route_logits(logits: torch.Tensor, tau: float):
     """Tau selection from given fp32 logits [N,E] (bit-exact with torch CPU
-    softmax_thresholding, src/MoEBlock_origin.py:50-97). Returns (probs, gates, mask, count)."""
-    if logits.dtype != torch.float32 or logits.dim() != 2:
-        raise RuntimeError("prunepath.route_logits: logits must be float32 [N,E]")
-    _need_gpu("route_logits", logits)
-    N, E = logits.shape
-    dev = logits.device
-    probs = torch.empty(N, E, dtype=torch.float32, device=dev)
-    gates = torch.empty(N, E, dtype=torch.float32, device=dev)
-    mask = torch.empty(N, E, dtype=torch.uint8, device=dev)
-    count = torch.empty(N, dtype=torch.int32, device=dev)
-    rc = L.lib().pp_route_logits(_vp(logits), N, E, float(tau), _vp(probs), _vp(gates), _vp(mask),
-                                 _vp(count), _stream(logits))
-    L.check(rc, "route_logits")
-    return probs, gates, mask, count
+    softmax_thresholding, src/MoEBlock_origin.py:50-97; ``torch.ops.prunepath.route_logits``).
+    Returns (probs, gates, mask, count)."""
+    return L.torch_ops().route_logits(logits, float(tau))
 
 
 # ----------------------------------------------------------------------------- bucketing
@@ -179,32 +99,14 @@ def max_tiles(N: int, E: int, tile_m: Optional[int] = None) -> int:
 
 
 def bucket(mask: torch.Tensor, gates: torch.Tensor, tile_m: Optional[int] = None):
-    """Token -> expert CSR layout (experts ascending, tokens ascending inside an expert).
-    Returns dict: offsets [E+1], token_ids [N*E], pair_gates [N*E], token_pairs [N,E],
-    tiles [max_tiles,4], meta [4] (all int32 except pair_gates fp32). Only the first
-    offsets[E] entries of token_ids / pair_gates and the first meta[0] tiles are valid."""
-    if mask.dtype != torch.uint8 or gates.dtype != torch.float32 or mask.shape != gates.shape:
-        raise RuntimeError("prunepath.bucket: mask uint8 [N,E] and gates float32 [N,E] required")
-    _need_gpu("bucket", mask, gates)
-    N, E = mask.shape
-    tm = tile_m or gemm_tile_m()
-    dev = mask.device
-    mt = max_tiles(N, E, tm)
-    r = {
-        "offsets": torch.empty(E + 1, dtype=torch.int32, device=dev),
-        "token_ids": torch.empty(max(N * E, 1), dtype=torch.int32, device=dev),
-        "pair_gates": torch.empty(max(N * E, 1), dtype=torch.float32, device=dev),
-        "token_pairs": torch.empty(N, E, dtype=torch.int32, device=dev),
-        "tiles": torch.empty(max(mt, 1), 4, dtype=torch.int32, device=dev),
-        "meta": torch.empty(4, dtype=torch.int32, device=dev),
-        "max_tiles": mt,
-    }
-    ws = torch.empty(int(L.lib().pp_bucket_workspace_bytes(N, E)), dtype=torch.uint8, device=dev)
-    rc = L.lib().pp_bucket(_vp(mask), _vp(gates), N, E, tm, _vp(r["offsets"]), _vp(r["token_ids"]),
-                           _vp(r["pair_gates"]), _vp(r["token_pairs"]), _vp(r["tiles"]), _vp(r["meta"]),
-                           _vp(ws), _stream(mask))
-    L.check(rc, "bucket")
-    return r
+    """Token -> expert CSR layout, experts ascending, tokens ascending inside an expert
+    (``torch.ops.prunepath.bucket``). Returns dict: offsets [E+1], token_ids [N*E],
+    pair_gates [N*E], token_pairs [N,E], tiles [max_tiles,4], meta [4] (all int32 except
+    pair_gates fp32) and max_tiles. Only the first offsets[E] entries of token_ids /
+    pair_gates and the first meta[0] tiles are valid."""
+    off, tok, pg, tp, tiles, meta = L.torch_ops().bucket(mask, gates, int(tile_m or 0))
+    return {"offsets": off, "token_ids": tok, "pair_gates": pg, "token_pairs": tp, "tiles": tiles, "meta": meta,
+            "max_tiles": max_tiles(mask.shape[0], mask.shape[1], tile_m)}
 
 
 # ----------------------------------------------------------------------------- decode
@@ -217,11 +119,7 @@ def decode_workspace(H: int, E: int, device) -> torch.Tensor:
 
 def decode_workspace_init(ws: torch.Tensor, H: int, E: int) -> torch.Tensor:
     """Zero a decode workspace in place (first use, or to clear its error flag)."""
-    if ws.dtype != torch.uint8 or ws.numel() < int(L.lib().pp_decode_workspace_bytes(H, E)):
-        raise RuntimeError("prunepath.decode_workspace_init: workspace too small")
-    _need_gpu("decode_workspace_init", ws)
-    rc = L.lib().pp_decode_workspace_init(_vp(ws), H, E, _stream(ws))
-    L.check(rc, "decode_workspace_init")
+    L.torch_ops().decode_workspace_init(ws, H, E)
     return ws
 
 
@@ -241,15 +139,14 @@ def decode_state(ws: torch.Tensor, E: int) -> dict:
 def moe_decode(x: torch.Tensor, router_packed: torch.Tensor, bias: Optional[torch.Tensor], E: int, G: int,
                tau: float, packed: torch.Tensor, workspace: torch.Tensor, grid: int = 0,
                out: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """Fused single-token MoE-MLP layer. x [H] or [1,H]; returns bf16 [1,H]."""
-    x, xd = _x_dtype(x.reshape(1, -1))
-    H = x.shape[1]
-    _need_gpu("moe_decode", x, router_packed, bias, packed, workspace)
+    """Fused single-token MoE-MLP layer (``torch.ops.prunepath.moe_decode``, or
+    ``moe_decode_into`` writing ``out``). x [H] or [1,H]; returns bf16 [1,H]."""
+    x = x.reshape(1, -1)
+    if x.dtype not in (torch.float32, torch.bfloat16):
+        x = x.float()
     if out is None:
-        out = torch.empty(1, H, dtype=torch.bfloat16, device=x.device)
-    rc = L.lib().pp_moe_decode(_vp(x), xd, H, _vp(router_packed), _vp(bias), E, G, float(tau), _vp(packed),
-                               _vp(out), _vp(workspace), int(grid), _stream(x))
-    L.check(rc, "moe_decode")
+        return L.torch_ops().moe_decode(x, router_packed, bias, E, G, float(tau), packed, workspace, int(grid))
+    L.torch_ops().moe_decode_into(x, router_packed, bias, E, G, float(tau), packed, workspace, out, int(grid))
     return out
 
 
@@ -262,18 +159,19 @@ def moe_prefill(x: torch.Tensor, router_packed: torch.Tensor, bias: Optional[tor
                 tau: float, packed: torch.Tensor, workspace: Optional[torch.Tensor] = None,
                 out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Route -> bucket -> grouped gate/up GEMM (SwiGLU) -> grouped down GEMM -> combine.
-    x [N,H]; returns bf16 [N,H]."""
-    x, xd = _x_dtype(x)
+    x [N,H]; returns bf16 [N,H]. ``torch.ops.prunepath.moe_prefill`` (workspace from the
+    caching allocator), or ``moe_prefill_into`` when a workspace / output is given."""
+    if x.dtype not in (torch.float32, torch.bfloat16):
+        x = x.float()
+    ops = L.torch_ops()
+    if workspace is None and out is None:
+        return ops.moe_prefill(x, router_packed, bias, E, G, float(tau), packed)
     N, H = x.shape
-    _need_gpu("moe_prefill", x, router_packed, bias, packed, workspace)
-    need = prefill_workspace_bytes(N, H, E, G)
-    if workspace is None or workspace.numel() < need:
-        workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
+    if workspace is None or workspace.numel() < prefill_workspace_bytes(N, H, E, G):
+        workspace = torch.empty(prefill_workspace_bytes(N, H, E, G), dtype=torch.uint8, device=x.device)
     if out is None:
         out = torch.empty(N, H, dtype=torch.bfloat16, device=x.device)
-    rc = L.lib().pp_moe_prefill(_vp(x), xd, N, H, _vp(router_packed), _vp(bias), E, G, float(tau), _vp(packed),
-                                _vp(out), _vp(workspace), _stream(x))
-    L.check(rc, "moe_prefill")
+    ops.moe_prefill_into(x, router_packed, bias, E, G, float(tau), packed, workspace, out)
     return out
 
 
@@ -379,39 +277,3 @@ def masked_gate(inter: torch.Tensor, gates: torch.Tensor, layout) -> torch.Tenso
     and backward kernels; ``layout`` from masked_gate_layout."""
     eid, perm, seg = layout
     return _MaskedGate.apply(inter, gates, eid, perm, seg)
-
-
-# ----------------------------------------------------------------------------- torch.library
-@torch.library.custom_op("prunepath::route_logits", mutates_args=())
-def _route_logits_op(logits: torch.Tensor, tau: float) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor,
-                                                                  torch.Tensor]:
-    return route_logits(logits, tau)
-
-
-@_route_logits_op.register_fake
-def _(logits, tau):
-    N, E = logits.shape
-    return (logits.new_empty(N, E), logits.new_empty(N, E), logits.new_empty(N, E, dtype=torch.uint8),
-            logits.new_empty(N, dtype=torch.int32))
-
-
-@torch.library.custom_op("prunepath::moe_prefill", mutates_args=())
-def _moe_prefill_op(x: torch.Tensor, router_packed: torch.Tensor, bias: Optional[torch.Tensor], E: int, G: int,
-                    tau: float, packed: torch.Tensor) -> torch.Tensor:
-    return moe_prefill(x, router_packed, bias, E, G, tau, packed)
-
-
-@_moe_prefill_op.register_fake
-def _(x, router_packed, bias, E, G, tau, packed):
-    return x.new_empty(x.shape, dtype=torch.bfloat16)
-
-
-@torch.library.custom_op("prunepath::moe_decode", mutates_args=("workspace",))
-def _moe_decode_op(x: torch.Tensor, router_packed: torch.Tensor, bias: Optional[torch.Tensor], E: int, G: int,
-                   tau: float, packed: torch.Tensor, workspace: torch.Tensor) -> torch.Tensor:
-    return moe_decode(x, router_packed, bias, E, G, tau, packed, workspace)
-
-
-@_moe_decode_op.register_fake
-def _(x, router_packed, bias, E, G, tau, packed, workspace):
-    return x.new_empty(1, x.numel(), dtype=torch.bfloat16)

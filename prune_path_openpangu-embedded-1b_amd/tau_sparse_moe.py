@@ -24,9 +24,10 @@ Differences by design (each a documented build choice, not an omission):
 * Every neuron of every selected expert is computed (the reference decode grid
   covers only 64 neurons per expert, :398-399, 515).
 * Decode failures are not silent (the reference has no failure reporting): a decode
-  kernel that cannot complete its wait, or whose selection is inconsistent, sets a
-  sticky error flag in the decode workspace and writes NaN outputs from then on.
-  ``decode_error()`` reads the flag, ``check_decode()`` raises when it is set, and
+  call whose selection is inconsistent or whose reduction leaves the fixed-point range
+  writes NaN outputs, and one whose cross-workgroup wait times out writes NaN from then
+  on; each sets a sticky error bit in the decode workspace.
+  ``decode_error()`` reads the bits, ``check_decode()`` raises when one is set, and
   ``checked = True`` runs that check after every decode call (a host sync, so off by
   default; graph-captured serving loops check between replays instead);
   ``reset_decode_error()`` clears it.
@@ -136,7 +137,7 @@ class TauSparseMoE(nn.Module):
     # ------------------------------------------------------------------ decode errors
     def decode_error(self) -> int:
         """Sticky error bits of the decode workspace (0 = none; 1 = a logit wait timed
-        out, 2 = inconsistent selection). Synchronises with the device."""
+        out, 2 = inconsistent selection, 4 = reduction out of range). Synchronises."""
         if self.decode_workspace is None:
             return 0
         return ops.decode_state(self.decode_workspace, self.num_experts)["error"]

@@ -66,6 +66,30 @@ def sparse_expected(x: np.ndarray, w: dict, gates: np.ndarray) -> np.ndarray:
                                             gates, G)
 
 
+def sparse_expected_gpu(x: np.ndarray, w: dict, gates: np.ndarray) -> np.ndarray:
+    """sparse_expected in torch float64 on cuda:0, for sizes where the numpy restatement
+    is slow (e.g. 8200 tokens): every expert's SwiGLU on every token, times the gate
+    (0 for unselected experts, so those terms vanish exactly), down projection. Same
+    operands as sparse_expected (bf16-rounded x and weights, rearranged neurons);
+    test_prefill_full_rows pins it against sparse_expected on a slice."""
+    E = w["w_router"].shape[0]
+    I = w["w_gate"].shape[0]
+    G = I // E
+    perm = oracle.pack_permutation(w["expert_ids"])
+    d = dev()
+
+    def t(a):
+        return torch.from_numpy(np.ascontiguousarray(a)).to(d, torch.float64)
+
+    xr = t(bf16_round(x))
+    WgT = t(bf16_round(w["w_gate"])[perm].T)        # [H, I], contiguous right operands
+    WuT = t(bf16_round(w["w_up"])[perm].T)
+    WdT = t(bf16_round(w["w_down"])[:, perm].T)     # [I, H]
+    g = xr @ WgT
+    a = g / (1.0 + torch.exp(-g)) * (xr @ WuT) * t(gates).repeat_interleave(G, dim=1)
+    return (a @ WdT).cpu().numpy()
+
+
 def assert_close_fp32(got: np.ndarray, ref32: np.ndarray, ref_q: np.ndarray, what=""):
     """bf16 output vs the fp32 reference (original fp32 weights and x).
 

@@ -5,7 +5,9 @@ checked against the float64 sparse restatement on the same bf16 operands (rtol 2
 atol 2e-3) with the selection bit-exact against the oracle on the kernel's own logits:
 
 * decode: decode16_kernel (E = 16, H % 512 == 0; with and without the speculative
-  loads, CPL <= 4 / CPL = 8) and decode_kernel (any other E or H);
+  loads, CPL <= 4 / CPL = 8) and decode_kernel (any other E or H; eight waves for
+  H <= 2560, four above; the workgroup selection's rank merge over one to four 64-key
+  runs, with and without a padded last run);
 * prefill routing: route16_few_kernel (E = 16, N <= 64, H % 512 == 0, H <= 2048),
   route16_kernel (other E = 16 cases) and route_kernel (E != 16);
 * prefill GEMMs: gemm_s_kernel (N <= 64, G % 64 == 0, H >= 384), gemm_v3_kernel
@@ -40,6 +42,9 @@ CASES = [
     (1536, 16, 384, 129, 0.7, torch.bfloat16, False),  # bf16 x, ragged N past two 64-token blocks
     (1536, 16, 384, 1, 0.7, torch.bfloat16, False),    # decode16 at the configured shape, bf16 x
     (1536, 16, 384, 1, 0.95, torch.float32, True),     # decode16 with the config-3 router bias
+    (4096, 192, 32, 1, 0.7, torch.float32, False),     # decode_kernel with four waves (CPL 8), three key runs
+    (3072, 100, 32, 1, 0.7, torch.bfloat16, False),    # four waves (CPL 6); two key runs, the last padded
+    (1536, 200, 32, 1, 0.95, torch.float32, True),     # eight waves; four key runs, the last padded; bias
 ]
 
 
@@ -70,7 +75,4 @@ def test_layer_shape_vs_oracle(pkg, H, E, G, N, tau, xdt, with_bias):
     xr = xg.float().cpu().numpy()
     assert_close(out, sparse_expected(xr, w, sel.gates), what=f"layer H={H} E={E} G={G} N={N}")
     out2 = m(xg[None]).float().cpu().numpy()[0]
-    if N > 1:  # prefill is deterministic bit for bit (decode adds partials with float atomics)
-        np.testing.assert_array_equal(out2, out)
-    else:
-        assert_close(out2, out, what="decode repeat")
+    np.testing.assert_array_equal(out2, out)  # prefill and decode are deterministic bit for bit

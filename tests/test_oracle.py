@@ -230,6 +230,35 @@ def test_masked_layer_vs_torch_fixture(oracle, name):
         np.testing.assert_allclose(out, ref, rtol=1e-4, atol=1e-5)
 
 
+@pytest.mark.parametrize("name", ["c1_layer", "c1_layer_contig"])
+def test_torch_masked_layer_vs_fixture(oracle, name):
+    """oracle/torch_masked.py (the torch-fp32 CPU baseline) reproduces the config-1
+    fixture's logits, gates (bit for bit) and outputs, and its selection equals
+    oracle.select's on the same logits; with the Zipf bias its selection is
+    oracle.select of (logits + bias)."""
+    import torch
+    from oracle.torch_masked import MaskedLayer
+    z, w, x = _c1(name)
+    layer = MaskedLayer(w["w_gate"], w["w_up"], w["w_down"], w["w_router"], w["expert_ids"])
+    torch.set_num_threads(1)
+    for ti, tau in enumerate(z["taus"]):
+        score, (gates, sel) = layer.route(torch.from_numpy(x), float(tau))
+        np.testing.assert_allclose(score.numpy(), z["logits"], rtol=1e-6, atol=1e-6)
+        ref = oracle.select(score.numpy(), float(tau))
+        np.testing.assert_array_equal(sel.numpy(), ref.mask.astype(bool))
+        np.testing.assert_array_equal(_bits(gates.numpy()), _bits(ref.gates))
+        if np.array_equal(score.numpy(), z["logits"]):
+            np.testing.assert_array_equal(_bits(gates.numpy()), _bits(z[f"tau{ti}/gates"]))
+        out = layer(torch.from_numpy(x), float(tau)).numpy()
+        np.testing.assert_allclose(out, z[f"tau{ti}/out"], rtol=1e-4, atol=1e-5)
+    bias = gi.zipf_bias(16)
+    lb = MaskedLayer(w["w_gate"], w["w_up"], w["w_down"], w["w_router"], w["expert_ids"], bias=bias)
+    score, (gates, sel) = lb.route(torch.from_numpy(x), 0.95)
+    ref = oracle.select(score.numpy(), 0.95)
+    np.testing.assert_array_equal(sel.numpy(), ref.mask.astype(bool))
+    np.testing.assert_allclose(score.numpy(), z["logits"] + bias, rtol=1e-6, atol=1e-6)
+
+
 def test_masked_equals_sparse_form(oracle):
     z, w, x = _c1("c1_layer")
     perm = oracle.pack_permutation(w["expert_ids"])
