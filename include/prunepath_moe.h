@@ -162,6 +162,19 @@ int pp_moe_decode(const void* x, int x_dtype, int H, const float* router_packed,
                   const float* bias, int E, int G, float tau, const void* packed,
                   void* out_bf16, void* workspace, int grid, void* stream);
 
+/* Allocation-free decode. No counterpart in the reference: for callers that cannot
+ * allocate device memory (code under hipGraph capture, serving loops or harnesses that
+ * forbid hipMalloc). Same arguments and results as pp_moe_decode without the workspace:
+ * the library's own 261 KB device array is the workspace (one per GPU, zeroed by a fill
+ * kernel on the caller's stream at the first call on that GPU, held until the process
+ * ends). Limits: H <= 4096, E <= 256 (the library's shape limits; PP_ERR_UNSUPPORTED
+ * beyond). Every call on a GPU shares that GPU's array: calls that overlap on one GPU
+ * (different streams, threads or processes' graphs replayed concurrently) race; calls
+ * ordered on one stream of any shapes are safe. The call allocates and frees nothing. */
+int pp_moe_decode_noalloc(const void* x, int x_dtype, int H, const float* router_packed,
+                          const float* bias, int E, int G, float tau, const void* packed,
+                          void* out_bf16, int grid, void* stream);
+
 /* ------------------------------------------------------------------------- *
  * Prefill / N > 1: route -> bucket -> grouped gate/up GEMM with fused SwiGLU
  * epilogue (bf16 MFMA) -> grouped down GEMM -> per-token combine in fp32 -> bf16.

@@ -1060,3 +1060,60 @@ extern "C" int pp_moe_decode(const void* x, int x_dtype, int H, const float* rou
   return decode_dispatch(x, x_dtype, H, router_packed, bias, E, G, tau, packed, out_bf16, st, acc, H, H, grid,
                          (hipStream_t)stream);
 }
+
+// ------------------------------------------------------------------ allocation-free entry
+// pp_moe_decode_noalloc: pp_moe_decode with the library's own workspace, for callers that
+// cannot allocate (code under graph capture, serving loops that forbid hipMalloc). The
+// workspace is `scratch`, a file-scope device array of fixed size, one copy per GPU, laid
+// out for the largest supported H (accumulator stride 4096) so calls of any shape share
+// it; each call clears the whole accumulator set of the previous call. Host code never
+// passes `scratch` itself (in host code it names a host-side stand-in, not device
+// memory): the device address comes from hipGetSymbolAddress, once per device.
+#define PP_DECODE_SCRATCH_HS 4096
+static constexpr size_t kDecScratchBytes =
+    dec_acc_offset() + (size_t)2 * DEC_NCOPY * PP_DECODE_SCRATCH_HS * sizeof(dec_acc_t) +
+    PP_MAX_EXPERTS * sizeof(unsigned long long);
+static_assert(kDecScratchBytes == 267520, "decode scratch: 261 KB per GPU (state, int64 accumulators at stride 4096, slots)");
+static __device__ __align__(256) unsigned char scratch[kDecScratchBytes];
+
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[64];
+
+// Device address of this device's scratch; the first call on a device also zeroes it
+// (a fill kernel on the caller's stream, ordered before the caller's decode).
+static int decode_scratch(hipStream_t s, void** out) {
+  int dev = 0;
+  PP_REQUIRE(hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64, PP_ERR_HIP,
+             "pp_moe_decode_noalloc: no current device");
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    PP_REQUIRE(e == hipSuccess && ptr != nullptr, PP_ERR_HIP, "pp_moe_decode_noalloc: hipGetSymbolAddress: %s",
+               hipGetErrorString(e));
+    decode_ws_clear_kernel<<<64, 256, 0, s>>>((uint32_t*)ptr, kDecScratchBytes / 4);
+    const int rc = pp_check_launch("pp_moe_decode_noalloc (scratch init)");
+    if (rc) return rc;
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return PP_OK;
+}
+
+extern "C" int pp_moe_decode_noalloc(const void* x, int x_dtype, int H, const float* router_packed,
+                                     const float* bias, int E, int G, float tau, const void* packed, void* out_bf16,
+                                     int grid, void* stream) {
+  int rc = decode_check_args(x, x_dtype, H, router_packed, E, G, packed, out_bf16, grid);
+  if (rc) return rc;
+  PP_REQUIRE(H <= PP_DECODE_SCRATCH_HS && E <= PP_MAX_EXPERTS, PP_ERR_UNSUPPORTED,
+             "pp_moe_decode_noalloc: H=%d E=%d beyond the scratch maximum (H <= %d, E <= %d)", H, E,
+             PP_DECODE_SCRATCH_HS, PP_MAX_EXPERTS);
+  hipStream_t s = (hipStream_t)stream;
+  void* ptr = nullptr;
+  rc = decode_scratch(s, &ptr);
+  if (rc) return rc;
+  pp_decode_state* st = (pp_decode_state*)ptr;
+  dec_acc_t* acc = (dec_acc_t*)((char*)ptr + dec_acc_offset());
+  return decode_dispatch(x, x_dtype, H, router_packed, bias, E, G, tau, packed, out_bf16, st, acc,
+                         PP_DECODE_SCRATCH_HS, PP_DECODE_SCRATCH_HS, grid, s);
+}
