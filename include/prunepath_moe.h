@@ -141,8 +141,8 @@ int pp_bucket(const uint8_t* mask, const float* gates, int64_t n_tokens, int E, 
  * ------------------------------------------------------------------------- */
 typedef struct pp_decode_state {
   uint32_t router_ticket; /* internal: call epoch, advanced by one per call */
-  uint32_t ready;         /* internal */
-  uint32_t done;          /* internal */
+  uint32_t ready;         /* internal (unused) */
+  uint32_t done;          /* internal (unused) */
   uint32_t error;         /* sticky error bits, 0 = none: 1 a logit-slot wait timed out
                              (every later call on the workspace writes NaN), 2 the selection
                              was not a permutation of the experts, 4 a workgroup partial sum
@@ -165,7 +165,7 @@ int pp_moe_decode(const void* x, int x_dtype, int H, const float* router_packed,
 /* Allocation-free decode. No counterpart in the reference: for callers that cannot
  * allocate device memory (code under hipGraph capture, serving loops or harnesses that
  * forbid hipMalloc). Same arguments and results as pp_moe_decode without the workspace:
- * the library's own 261 KB device array is the workspace (one per GPU, zeroed by a fill
+ * the library's own 299 KB device array is the workspace (one per GPU, zeroed by a fill
  * kernel on the caller's stream at the first call on that GPU, held until the process
  * ends). Limits: H <= 4096, E <= 256 (the library's shape limits; PP_ERR_UNSUPPORTED
  * beyond). Every call on a GPU shares that GPU's array: calls that overlap on one GPU

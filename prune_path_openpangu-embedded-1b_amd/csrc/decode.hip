@@ -93,6 +93,7 @@ __device__ __forceinline__ float dec_from_fixed(dec_acc_t v) {
 __device__ __forceinline__ dec_acc_t* dec_acc_set(dec_acc_t* acc, int hs, uint32_t epoch) {
   return acc + (size_t)(epoch & 1u) * DEC_NCOPY * hs;
 }
+#define DEC_SLOT_REPS 16  // replicas of the logit slots (each written by its router workgroup)
 __device__ __forceinline__ unsigned long long* dec_slots(dec_acc_t* acc, int hs) {
   return (unsigned long long*)(acc + (size_t)2 * DEC_NCOPY * hs);
 }
@@ -109,6 +110,35 @@ __device__ __forceinline__ void dec_clear_previous(dec_acc_t* acc, int hs, int h
     const int c = (int)((uint32_t)i / (uint32_t)hclear);
     st_rlx(prev + (size_t)c * hs + (i - c * hclear), (dec_acc_t)0);
   }
+}
+
+// Completion ticket in two levels. One counter taken by every workgroup serialises at
+// the memory side (~20 ns per atomic on one address). Here workgroup b counts in at its
+// group's counter (DEC_TG workgroups per group, each counter on a 128-byte line of its
+// own); the group's last arrival counts the group in at the top counter; the top's last
+// arrival is the call's last workgroup. Every arrival has performed its accumulator
+// atomics first, so the last workgroup sees them all; it zeroes the counters it used.
+#define DEC_TG 16
+#define DEC_TLINE 32                          // uint32 per 128-byte line
+#define DEC_TMAX_GROUPS 64                    // larger grids use groups of ceil(W / 64)
+#define DEC_TICKET_WORDS ((DEC_TMAX_GROUPS + 1) * DEC_TLINE)
+__device__ __forceinline__ uint32_t* dec_tickets(dec_acc_t* acc, int hs) {
+  return (uint32_t*)(dec_slots(acc, hs) + DEC_SLOT_REPS * PP_MAX_EXPERTS);
+}
+__device__ __forceinline__ int dec_tgroup_size(int W) {
+  return max(DEC_TG, (W + DEC_TMAX_GROUPS - 1) / DEC_TMAX_GROUPS);
+}
+// thread 0 of each workgroup, after its accumulator atomics are performed: true in the last
+__device__ __forceinline__ bool dec_ticket(uint32_t* tk, int b, int W) {
+  const int tg = dec_tgroup_size(W), grp = b / tg, ngrp = (W + tg - 1) / tg;
+  const uint32_t gsize = (uint32_t)min(tg, W - grp * tg);
+  return add_rlx(tk + (size_t)(grp + 1) * DEC_TLINE, 1u) == gsize - 1u &&
+         add_rlx(tk, 1u) == (uint32_t)ngrp - 1u;
+}
+// by the last workgroup, threads 0 .. ngrp
+__device__ __forceinline__ void dec_ticket_reset(uint32_t* tk, int W, int tid) {
+  const int tg = dec_tgroup_size(W), ngrp = (W + tg - 1) / tg;
+  if (tid <= ngrp) st_rlx(tk + (size_t)tid * DEC_TLINE, 0u);
 }
 
 // Add one partial (fp32) to a fixed-point accumulator; out-of-range partials flag the call.
@@ -296,14 +326,18 @@ __global__ __launch_bounds__(DecNW<CPL>::NT) void decode_kernel(
       sacc = wave_sum(sacc);
       if (lane == 0) red4[wv] = sacc;
       __syncthreads();
-      if (tid == 0) {
+      if (tid < DEC_SLOT_REPS) {  // one copy of the slot per replica, thread r the r-th
         float l = red4[0];
 #pragma unroll
         for (int w = 1; w < NW; ++w) l = __fadd_rn(l, red4[w]);
         if (bias) l = __fadd_rn(l, bias[b]);
-        st_rlx(&slots[b], ((unsigned long long)tag << 32) | __float_as_uint(l));
+        st_rlx(&slots[tid * PP_MAX_EXPERTS + b], ((unsigned long long)tag << 32) | __float_as_uint(l));
       }
     }
+    // this workgroup gathers from replica b % DEC_SLOT_REPS: a slot line is polled by
+    // W / DEC_SLOT_REPS workgroups instead of all of them (reads of one line serialise at
+    // the memory side; one copy for 256 workgroups made the gather ~2.8 us at E = 192)
+    slots += (b % DEC_SLOT_REPS) * PP_MAX_EXPERTS;
     // router workgroup e publishes {tag, logit} in its own 64-bit slot; every workgroup
     // gathers the E slots (bounded spin). No counter is shared while routing (E
     // increments of one address serialise at the memory side).
@@ -465,7 +499,7 @@ __global__ __launch_bounds__(DecNW<CPL>::NT) void decode_kernel(
   }
   vm_wait();  // every wave's accumulator atomics are performed before the ticket
   __syncthreads();
-  if (tid == 0) flag_s = add_rlx(&st->done, 1u) == (uint32_t)(W - 1);
+  if (tid == 0) flag_s = dec_ticket(dec_tickets(acc, hs), b, W);
   __syncthreads();
   if (flag_s) {  // last workgroup: fold copies, write bf16, advance the epoch, reset counters
     // DEC_FOLD_H values of h per thread per pass, every load of a pass issued before
@@ -492,11 +526,8 @@ __global__ __launch_bounds__(DecNW<CPL>::NT) void decode_kernel(
         }
       }
     }
-    if (tid == 0) {
-      st_rlx(&st->router_ticket, epoch + 1u);  // next call: other accumulator set, new slot tag
-      st_rlx(&st->done, 0u);
-      st_rlx(&st->ready, 0u);
-    }
+    dec_ticket_reset(dec_tickets(acc, hs), W, tid);
+    if (tid == 0) st_rlx(&st->router_ticket, epoch + 1u);  // next call: other accumulator set, new slot tag
   }
 }
 
@@ -866,7 +897,7 @@ __global__ __launch_bounds__(64 * NW) void decode16_kernel(
   }
   vm_wait();  // every wave's accumulator atomics are performed before the ticket
   __syncthreads();
-  if (tid == 0) flag_s = add_rlx(&st->done, 1u) == (uint32_t)(W - 1);
+  if (tid == 0) flag_s = dec_ticket(dec_tickets(acc, hs), b, W);
   __syncthreads();
   if (flag_s) {  // last workgroup: fold copies, write bf16, advance the epoch, reset the counter
     // every load of the fold is issued before the first add (one round trip)
@@ -891,10 +922,8 @@ __global__ __launch_bounds__(64 * NW) void decode16_kernel(
         out[h] = failed ? (bf16_t)0x7fc0 : f32_to_bf16(dec_from_fixed(tot));
       }
     }
-    if (tid == 0) {
-      st_rlx(&st->router_ticket, epoch + 1u);
-      st_rlx(&st->done, 0u);
-    }
+    dec_ticket_reset(dec_tickets(acc, hs), W, tid);
+    if (tid == 0) st_rlx(&st->router_ticket, epoch + 1u);
   }
 }
 
@@ -903,10 +932,12 @@ __global__ void decode_ws_clear_kernel(uint32_t* p, size_t n_words) {
     p[i] = 0u;
 }
 
-// state | 2 x DEC_NCOPY x H fixed-point accumulators | PP_MAX_EXPERTS 64-bit logit slots
+// state | 2 x DEC_NCOPY x H fixed-point accumulators | DEC_SLOT_REPS x PP_MAX_EXPERTS 64-bit logit slots |
+// completion-ticket counters
 extern "C" size_t pp_decode_workspace_bytes(int H, int E) {
   (void)E;
-  return dec_acc_offset() + (size_t)2 * DEC_NCOPY * H * sizeof(dec_acc_t) + PP_MAX_EXPERTS * sizeof(unsigned long long);
+  return dec_acc_offset() + (size_t)2 * DEC_NCOPY * H * sizeof(dec_acc_t) +
+         (size_t)DEC_SLOT_REPS * PP_MAX_EXPERTS * sizeof(unsigned long long) + (size_t)DEC_TICKET_WORDS * sizeof(uint32_t);
 }
 
 extern "C" int pp_decode_workspace_init(void* workspace, int H, int E, void* stream) {
@@ -1072,8 +1103,9 @@ extern "C" int pp_moe_decode(const void* x, int x_dtype, int H, const float* rou
 #define PP_DECODE_SCRATCH_HS 4096
 static constexpr size_t kDecScratchBytes =
     dec_acc_offset() + (size_t)2 * DEC_NCOPY * PP_DECODE_SCRATCH_HS * sizeof(dec_acc_t) +
-    PP_MAX_EXPERTS * sizeof(unsigned long long);
-static_assert(kDecScratchBytes == 267520, "decode scratch: 261 KB per GPU (state, int64 accumulators at stride 4096, slots)");
+    (size_t)DEC_SLOT_REPS * PP_MAX_EXPERTS * sizeof(unsigned long long) + (size_t)DEC_TICKET_WORDS * sizeof(uint32_t);
+static_assert(kDecScratchBytes == 306560, "decode scratch: 299 KB per GPU (state, int64 accumulators at stride 4096, "
+                                          "slot replicas, ticket counters)");
 static __device__ __align__(256) unsigned char scratch[kDecScratchBytes];
 
 static std::mutex g_scratch_mu;

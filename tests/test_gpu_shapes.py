@@ -45,6 +45,8 @@ CASES = [
     (4096, 192, 32, 1, 0.7, torch.float32, False),     # decode_kernel with four waves (CPL 8), three key runs
     (3072, 100, 32, 1, 0.7, torch.bfloat16, False),    # four waves (CPL 6); two key runs, the last padded
     (1536, 200, 32, 1, 0.95, torch.float32, True),     # eight waves; four key runs, the last padded; bias
+    (2560, 8, 64, 1, 0.8, torch.float32, True),        # E <= 16 with a router too large to read per workgroup:
+                                                       # the routing kernel's wave selection
 ]
 
 
