@@ -120,28 +120,35 @@ int pp_bucket(const uint8_t* mask, const float* gates, int64_t n_tokens, int E, 
 
 /* ------------------------------------------------------------------------- *
  * Decode (N == 1): one fused kernel -- router GEMV (fp32), selection, gate/up
- * GEMVs over the selected experts' neurons, silu(g)*u*gate, down GEMV and the
- * cross-workgroup reduction in 64-bit fixed point (value * 2^32: the sum does not
- * depend on the order the workgroups finish in, so the bf16 output is the same bits on
- * every call), bf16 output.
+ * GEMVs over the selected experts' neurons, silu(g)*u*gate, down GEMV, bf16 output.
  * Replaces TauSparseMoE.forward_decode with moe_router_select_kernel_decode and
  * moe_decode_swiglu_fused_kernel (src/tl_kernel_optimized_Ultimate_PanGU.py:335-462, 494-530).
+ * Two kernels, by shape:
+ *   E = 16, H % 512 == 0, G <= 512 (the configured shape): two phases in one launch.
+ *     The gate/up records are spread over all workgroups and every act
+ *     silu(g.x)*(u.x)*gate is published to the workspace; each workgroup then writes
+ *     its own rows of the output as a fixed-order sum over the selected experts' down
+ *     rows. Every workgroup waits for acts from all the others, so the grid is clamped
+ *     to the workgroups the device holds at once (occupancy calculator) and to 1024.
+ *   any other shape: each workgroup accumulates its records' act * down into a partial
+ *     output, partials are summed in 64-bit fixed point (value * 2^32) and the last
+ *     workgroup writes bf16. Shapes with (E > 16 or 16*H > 32768) publish each logit
+ *     from its own workgroup and every workgroup waits for all E of them, so the E
+ *     router workgroups must be resident together: checked from the occupancy
+ *     calculator before the launch (PP_ERR_UNSUPPORTED otherwise).
+ * Both sum in an order that does not depend on timing: the bf16 output is the same bits
+ * on every call. A wait that cannot finish (e.g. other work holding the device) ends
+ * after a bounded spin with error bit 1 and NaN outputs, never a hang.
  * The workspace (pp_decode_workspace_bytes) must be zeroed once with
  * pp_decode_workspace_init before the first call; every call leaves it ready for
  * the next one. Calls that share a workspace must be ordered (same stream);
  * overlapping calls on one workspace race. After a call the workspace holds the
  * call's logits, selected experts and gates (struct pp_decode_state below).
  * grid = number of workgroups (0 = automatic).
- * Shapes other than E = 16 with H % 512 == 0 and (E > 16 or 16*H > 32768) publish
- * each logit from its own workgroup and every workgroup waits for all E of them, so
- * the E router workgroups must be resident on the device together: checked from the
- * occupancy calculator before the launch (PP_ERR_UNSUPPORTED otherwise). A wait that
- * still cannot finish (e.g. other work holding the device) ends after a bounded spin
- * with error bit 1 and NaN outputs, never a hang.
  * ------------------------------------------------------------------------- */
 typedef struct pp_decode_state {
-  uint32_t router_ticket; /* internal: call epoch, advanced by one per call */
-  uint32_t ready;         /* internal (unused) */
+  uint32_t router_ticket; /* internal: call epoch of the general kernel, advanced by one per call */
+  uint32_t epoch16;       /* internal: call epoch of the E = 16 kernel, advanced by one per call */
   uint32_t done;          /* internal (unused) */
   uint32_t error;         /* sticky error bits, 0 = none: 1 a logit-slot wait timed out
                              (every later call on the workspace writes NaN), 2 the selection
@@ -165,7 +172,7 @@ int pp_moe_decode(const void* x, int x_dtype, int H, const float* router_packed,
 /* Allocation-free decode. No counterpart in the reference: for callers that cannot
  * allocate device memory (code under hipGraph capture, serving loops or harnesses that
  * forbid hipMalloc). Same arguments and results as pp_moe_decode without the workspace:
- * the library's own 299 KB device array is the workspace (one per GPU, zeroed by a fill
+ * the library's own 564 KB device array is the workspace (one per GPU, zeroed by a fill
  * kernel on the caller's stream at the first call on that GPU, held until the process
  * ends). Limits: H <= 4096, E <= 256 (the library's shape limits; PP_ERR_UNSUPPORTED
  * beyond). Every call on a GPU shares that GPU's array: calls that overlap on one GPU

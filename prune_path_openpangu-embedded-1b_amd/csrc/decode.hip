@@ -5,34 +5,32 @@
 // moe_decode_swiglu_fused_kernel (:385-462). Differences by design: fp32 router, the
 // torch-CPU selection rule (fp64-accumulated cumsum, torch sort order), every neuron of
 // every selected expert computed (the reference's 1-D grid leaves pid_g at 0 and only
-// covers 64 neurons per expert, :398-399, 515), and an fp32 reduction instead of bf16
-// atomics.
+// covers 64 neurons per expert, :398-399, 515), and a reduction whose order does not
+// depend on timing instead of bf16 atomics (the output is the same bits on every call).
 //
-// Routing. When the fp32 router is small (E <= 16 and 16*H*4 <= 128 KB, e.g. E=16 at
-// H=1536) every workgroup computes all logits (fixed reduction order, so every workgroup
-// gets the same bits) and runs the selection itself: no cross-workgroup wait at all.
-// Otherwise workgroup e < E computes logit e and publishes it in a 64-bit slot tagged
-// with the call epoch; every workgroup gathers the E slots (bounded spin on the tag) and
-// runs the selection on its own copy. Workgroups are dispatched in index order, so the
-// producers are resident before any waiter can take their slot; the bound only turns an
-// impossible wait into an error flag instead of a hang.
+// Two kernels, by shape.
 //
-// Work split. The layer's weight bytes are k * G neuron records of 6*H bytes each
-// ({gate row, up row, down column}, see pack.hip). All workgroups share the k*G
-// records evenly; each wave streams whole records with 16-byte loads per lane (the next
-// record's loads are in flight while the current one is reduced), reduces the gate/up
-// dot products across the wave, applies silu(g)*u*gate in registers and accumulates
-// act * down into 8*CPL fp32 registers per lane. The workgroup's partial output goes to
-// one of a few fp32 accumulator copies with float atomics; the last workgroup to finish
-// (ticket) folds the copies, writes the bf16 output, advances the call epoch and resets
-// the counters. Two accumulator sets alternate between calls, and each call clears the
-// set of the previous call early, off its critical path, so no call needs a memset.
+// decode16_kernel (E = 16, H % 512 == 0, G <= 512; the configured shape): every
+// workgroup computes all 16 logits (router 98 KB per workgroup, fixed reduction order,
+// the same bits everywhere), wave 0 selects, and the layer runs in two phases inside
+// the launch. Phase 1: the k*G selected gate/up records are dealt to the streaming
+// waves of the whole grid; each publishes act = silu(g.x) * (u.x) * gate per record to
+// the workspace. Phase 2: workgroup b owns output rows [h0, h1): their down rows
+// (down_t, staged in LDS by DMA while phase 1 runs) times every act, summed in a fixed
+// order, written as bf16. No partial output vectors cross workgroups, so no atomics, no
+// completion ticket and no fold.
 //
-// Cross-workgroup data (logits, selection, counters, accumulators) is only accessed
+// decode_kernel (any other shape, e.g. the checkpoint's E = 192, G = 32): routing in every
+// workgroup (small routers) or one logit per router workgroup published in tagged slots;
+// every workgroup streams whole {gate, up, down} records, accumulates act * down into a
+// partial output, the partials are added in 64-bit fixed point into a few accumulator
+// copies, and the last workgroup (completion ticket) writes bf16.
+//
+// Cross-workgroup data (logits, selection, acts, counters, accumulators) is only accessed
 // with agent-scope atomics, and ordering between them comes from waiting for
 // completion (s_waitcnt vmcnt(0)) before the dependent atomic. Agent-scope fences are
 // avoided on purpose: on gfx950 each one writes back and invalidates the L2, which
-// hundreds of workgroups cannot afford inside a 5 us kernel.
+// hundreds of workgroups cannot afford inside a 10 us kernel.
 #include <mutex>
 
 #include "pp_common.h"
@@ -46,11 +44,6 @@ struct DecNW {
   static constexpr int NT = 64 * NW;
 };
 #define DEC_NCOPY 4   // accumulator copies per set (general kernel; the allocation): 4 beat 8 and 16 at E = 192
-#define DEC16_NCOPY 4 // copies the E = 16 kernel uses (128 workgroups: 32 per address)
-#define DEC16_SPEC(CPL) ((CPL) <= 4)  // speculative top-expert loads (register budget)
-#ifndef DEC16_NW
-#define DEC16_NW 8  // waves per workgroup in the E = 16 kernel
-#endif
 #define DEC_SPIN_LIMIT (1u << 22)
 #define DEC_LOCAL_ROUTER_FLOATS 32768  // Epad*H at or below this: every workgroup routes
 
@@ -589,45 +582,20 @@ __device__ __forceinline__ uint4 load_x8_bf16<bf16_t>(const bf16_t* x, int ch) {
   return *(const uint4*)(x + ch * 8);
 }
 
+// All 16 logits of the token, for the E = 16 kernels: every wave of the workgroup ends with
+// the logit of expert lane & 15 (router and x read once per workgroup, a fixed reduction
+// order, so every workgroup gets the same bits). Wave wv takes the slice
+// [512 CPL wv / NW, 512 CPL (wv + 1) / NW) of x, CPL float4 chunks per lane: lanes form
+// rows of LR = 128 / NW lanes, row rw takes experts rw, rw + NR, ... (NR = 64 / LR rows)
+// and lane cl of the row the chunks cl + LR i. Rows add by DPP; the NW wave partials are
+// added in wave order. part_s: LDS [16 * NW]. Contains a workgroup barrier.
 template <typename XT, int CPL, int NW>
-__global__ __launch_bounds__(64 * NW) void decode16_kernel(
-    const XT* __restrict__ x, const float* __restrict__ router, const float* __restrict__ bias, int G, float tau,
-    const bf16_t* __restrict__ rows, bf16_t* __restrict__ out, pp_decode_state* __restrict__ st,
-    dec_acc_t* __restrict__ acc, int hs, int hclear) {
+__device__ __forceinline__ float dec16_logits(const XT* __restrict__ x, const float* __restrict__ router,
+                                              const float* __restrict__ bias, float* part_s, int lane, int wv) {
   constexpr int H = 512 * CPL;
-  constexpr int HC = H / 8;
-  constexpr int NT = 64 * NW;
-  extern __shared__ __align__(16) float red[];  // [NW][H]
-  __shared__ __align__(16) float part_s[16 * NW];
-  __shared__ __align__(16) float lg_s[16];
-  __shared__ __align__(16) float pg_s[32];
-  __shared__ __align__(16) float srt_s[16];
-  __shared__ int flag_s;
-  __shared__ int k_s;
-  __shared__ int sel_ids_s[16];
-  __shared__ float sel_g_s[16];
-  __shared__ int main_ids_s[16];
-  __shared__ float main_g_s[16];
-  __shared__ int kmain_s, spec_s;
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int W = gridDim.x, b = blockIdx.x;
-  const uint32_t epoch = ld_rlx(&st->router_ticket);  // accumulator set parity
-
-  // x for the stream as packed bf16 (round to nearest even), loaded now so the loads
-  // overlap the routing
-  uint4 xb[CPL];
-#pragma unroll
-  for (int c = 0; c < CPL; ++c) xb[c] = load_x8_bf16<XT>(x, lane + 64 * c);
-  const float bias_j = bias != nullptr ? bias[lane & 15] : 0.0f;
-
-  // ---- logits. Wave wv takes the slice [512 CPL wv / NW, 512 CPL (wv + 1) / NW) of
-  // x, CPL float4 chunks per lane: lanes form rows of LR = 128 / NW lanes, row rw takes
-  // experts rw, rw + NR, ... (NR = 64 / LR rows) and lane cl of the row the chunks
-  // cl + LR i. Loads per workgroup: the router once and x once. Rows add by DPP; wave 0
-  // adds the NW wave partials in wave order. Every workgroup uses the same order, so
-  // every workgroup gets the same logits.
-  static_assert(NW == 8 || NW == 16, "decode16_kernel: 8 or 16 waves");
+  static_assert(NW == 8 || NW == 16, "dec16_logits: 8 or 16 waves");
   constexpr int LR = 128 / NW, NR = 64 / LR, EPL = 16 / NR;
+  const float bias_j = bias != nullptr ? bias[lane & 15] : 0.0f;
   {
     const int rw = lane / LR, cl = lane % LR;
     const int ch0 = (16 * CPL * 8 / NW) * wv + cl;  // float4 chunk index into x / a router row
@@ -655,8 +623,6 @@ __global__ __launch_bounds__(64 * NW) void decode16_kernel(
     }
   }
   __syncthreads();
-
-  // ---- logit of expert j = lane & 15 in every wave: the NW wave partials in wave order
   const int j = lane & 15;
   float xl;
   {
@@ -676,48 +642,121 @@ __global__ __launch_bounds__(64 * NW) void decode16_kernel(
     }
     if (bias != nullptr) xl = __fadd_rn(xl, bias_j);
   }
+  return xl;
+}
+
+
+// ------------------------------------------------------------------ two-phase decode (E = 16)
+// Roles inside a workgroup of eight waves. Wave 0 runs the exact selection alone (the
+// critical path to the first weight byte: 0.7 us after the logits) and publishes it to
+// the other waves through an LDS flag, then DMAs its workgroup's down rows, clears its
+// share of the next call's act bank and, in workgroup 0, advances the epoch. Waves 1..7
+// stream the records.
+// Phase 1 (gate/up): the k*G selected neuron records, in rank order, are dealt to the
+// streaming waves of the grid: record t to wave 1 + t % (7W) / W of workgroup t % W, so
+// consecutive records spread over workgroups and every workgroup gets the same share. A
+// wave issues all its record loads at once, computes act = silu(g.x) * (u.x) * gate per
+// record and publishes each act in its own 32-bit word (DEC2_REPS replicas) of this
+// call's act bank.
+// Phase 2 (down): workgroup b owns output rows [h0, h1) of H; the rows down_t[e][h0..h1)
+// of every selected expert are in LDS (wave 0's DMAs). It waits for all k*G act words and
+// writes out[h] = sum over ranks s of down_t[e_s][h][.] . act_s -- a fixed order: the bf16
+// output is the same bits on every call, with no atomics and no cross-workgroup partial
+// sums.
+// Speculation: rank 0 is the expert with the largest logit unless probabilities tie, so
+// its records and down rows are requested before the cut is known and replaced after it
+// when the guess was wrong. Guessing further ranks does not pay: with the whole layer
+// requested at once the memory pipeline is saturated, a wave stalls at issue, and
+// whatever a guess misses is requested microseconds late.
+// Act words: ~bits(act) with NaN canonical, so 0 never occurs and means "not yet
+// written". Two banks alternate by call epoch; each call clears the other bank (the one
+// the next call uses) early, off its critical path. Every workgroup also marks itself
+// alive in the bank; workgroup 0 advances the epoch once every workgroup has (so no
+// workgroup of the call can read the next epoch). All W workgroups must be resident
+// together (the host clamps W to the device's capacity); waits are bounded: a timeout
+// sets error bit 1 and the workgroup writes NaN.
+#define DEC2_REPS 4            // replicas of the act words (a line is polled by W / DEC2_REPS workgroups)
+#define DEC2_WMAX 1024         // workgroups per call at most (alive words per bank)
+#define DEC2_GMAX 512          // neurons per expert at most (acts of one call fit LDS: 16 * 512 words)
+#define DEC2_RS (16 * DEC2_GMAX)  // words per act replica: a fixed layout, whatever the call's G
+#define DEC2_BANK_WORDS (DEC2_REPS * DEC2_RS + DEC2_WMAX)
+#define DEC2_DOWN_LDS (96 * 1024)  // LDS for the down rows of one pass (16 positions)
+
+// LDS writes of this wave visible to its other lanes (LDS executes a wave's operations in
+// order); unlike a wavefront fence it does not wait for the wave's global loads
+__device__ __forceinline__ void wave_lds_sync() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_wave_barrier();
+}
+
+// 16-byte load with the non-temporal hint (the weight stream is read once per call;
+// keeping it out of the caches leaves room for the router and x)
+typedef unsigned int dec_u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 ld_nt(const uint4* p) {
+  const dec_u32x4 v = __builtin_nontemporal_load((const dec_u32x4*)p);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+__device__ __forceinline__ uint32_t dec2_word(float a) {
+  return ~(a == a ? __float_as_uint(a) : 0x7fc00000u);
+}
+
+template <typename XT, int CPL>
+__global__ __launch_bounds__(512) void decode16_kernel(
+    const XT* __restrict__ x, const float* __restrict__ router, const float* __restrict__ bias, int G, float tau,
+    const bf16_t* __restrict__ gu, int rec_h, const bf16_t* __restrict__ down_t, bf16_t* __restrict__ out,
+    pp_decode_state* __restrict__ st, uint32_t* __restrict__ banks, int rp, int slot_bytes) {
+  constexpr int NW = 8, NT = 512, H = 512 * CPL, HC = H / 8;
+  extern __shared__ __align__(16) unsigned char dn_s[];  // [16][slot_bytes]: down rows of a pass
+  __shared__ __align__(16) float part_s[16 * NW];
+  __shared__ __align__(16) float pg_s[32];
+  __shared__ __align__(16) float srt_s[16];
+  __shared__ __align__(16) float act_s[16 * 512];
+  __shared__ int k_s, fail_s, ready_s;
+  __shared__ int L_s[16];    // selected experts in rank order (the stream order)
+  __shared__ float Lg_s[16];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int W = gridDim.x, b = blockIdx.x;
+  const uint32_t epoch = ld_rlx(&st->epoch16);
+  uint32_t* bank = banks + (size_t)(epoch & 1u) * DEC2_BANK_WORDS;
+  constexpr int AW = DEC2_REPS * DEC2_RS;  // act words per bank (replicas)
+  if (tid == 0) {
+    st_rlx(&bank[AW + b], 1u);  // alive
+    fail_s = (ld_rlx(&st->error) & 1u) != 0u;  // an earlier wait timed out: NaN until re-initialised
+    ready_s = 0;
+  }
+
+  uint4 xb[CPL];
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) xb[c] = load_x8_bf16<XT>(x, lane + 64 * c);
+
+  const int j = lane & 15;
+  const float xl = dec16_logits<XT, CPL, NW>(x, router, bias, part_s, lane, wv);
   const float m = row16_max(xl);
 
-  // ---- speculative top experts. Rank 0 is always selected and is the expert with the
-  // largest logit unless probabilities tie (then the lowest index among equal p); rank 1
-  // usually is too. So while wave 0 runs the selection, waves 1..7 start loading this
-  // workgroup's share of the records of e1 = the lowest index with the largest logit and,
-  // when two shares fit (G <= 3 W), of e2 = the lowest index with the largest logit
-  // among the rest -- one record per wave, e1's share on the first waves. After the
-  // selection barrier a speculative record is used if its expert was selected (then the
-  // main stream skips that expert) and dropped otherwise; either way every selected
-  // record is used exactly once. No speculation for non-finite or NaN logits.
-  // (wave 0 evaluates e1, e2 after its rank step, off its critical path)
-  auto top_experts = [&](int& t1, int& t2) {
-    t1 = t2 = -1;
-    const bool finite = __all(xl == xl) && __fsub_rn(m, m) == 0.0f;
-    if (!(DEC16_SPEC(CPL) && finite && G <= 7 * W)) return;
-    t1 = __builtin_amdgcn_readfirstlane(row16_min_i(xl == m ? j : 16));
-    if (G > 3 * W) return;
-    const float m2 = row16_max(j != t1 ? xl : -__builtin_inff());
-    t2 = __builtin_amdgcn_readfirstlane(row16_min_i((j != t1 && xl == m2) ? j : 16));
+  int h0, h1;  // output rows of this workgroup
+  pp_split((uint32_t)H, (uint32_t)W, (uint32_t)b, h0, h1);
+  const int cpr = G >> 3;  // 16-byte chunks per down row
+  auto dma_rows = [&](int s, int e, int r0, int r1) {  // down_t[e][r0..r1) -> slot s (one wave)
+    const int nch = (r1 - r0) * cpr;
+    const unsigned char* src = (const unsigned char*)(down_t + ((int64_t)e * H + r0) * G);
+    unsigned char* dst = dn_s + s * slot_bytes;
+    for (int c0 = 0; c0 < nch; c0 += 64)
+      __builtin_amdgcn_global_load_lds(src + 16 * min(c0 + lane, nch - 1),
+                                       (__attribute__((address_space(3))) void*)(dst + 16 * c0), 16, 0, 2 /* nt */);
   };
-  int e1 = -1, e2 = -1;
-  // ---- selection (wave 0), same arithmetic as select_small. Lane (g, j) = 16 g + j
-  // serves expert j; the critical path is short dependent chains, so the four 16-lane
-  // groups split the work instead of repeating it:
-  // * one exp / one division for both outputs: group 1 evaluates the gate
-  //   1 / (exp(0 - x_j) + 1) while group 0 evaluates p_j = exp(x_j - max) * (1 / S);
-  //   max and S are the xor butterfly i^8, i^4, i^2, i^1 (torch's reduce_all order);
-  // * group g compares key_j with the keys of experts 4g .. 4g+3 (64-bit rank keys:
-  //   NaN first, then descending p, equal p by index = torch's stable descending sort)
-  //   and sums the p of those ranked before j; two xor steps combine the groups;
-  // * when every p is 0 or >= 2^-29 each partial sum (< 2) is a multiple of 2^-52 and
-  //   exact in double, so {p_q : rank_q <= rank_j} summed in any order equals the fp64
-  //   running sum at rank_j; otherwise (or for NaN) the sequential running sum.
+  const int p0_end = min(h1, h0 + rp);
+  constexpr int NS = NW - 1;                          // streaming waves 1 .. NW-1
+
   if (wv == 0) {
+    // ---- exact selection, alone on this wave (the decode16 arithmetic); published to
+    // the other waves through an LDS flag, no barrier
     const int grp = lane >> 4;
-    if (lane < 16) lg_s[j] = xl;  // telemetry
     const float e = pp_expf_u10(grp == 1 ? __fsub_rn(0.0f, xl) : __fsub_rn(xl, m));
     const float S = row16_sum(e);
     const float r = __fdiv_rn(1.0f, grp == 1 ? __fadd_rn(e, 1.0f) : S);
     if (lane < 32) pg_s[lane] = grp == 1 ? r : __fmul_rn(e, r);  // [p_0..15 | gate_0..15]
-    wave_sync_lds();
+    wave_lds_sync();
     const float p = pg_s[j];
     const float4 p4 = *(const float4*)&pg_s[4 * grp];
     const float pq[4] = {p4.x, p4.y, p4.z, p4.w};
@@ -729,7 +768,7 @@ __global__ __launch_bounds__(64 * NW) void decode16_kernel(
       const bool before = sel_key(pq[i], 4 * grp + i) < kj;
       rank += before ? 1 : 0;
       cum += before ? (double)pq[i] : 0.0;
-      exact &= (int)(pq[i] == 0.0f) | (int)(pq[i] >= 0x1p-29f);  // NaN fails both
+      exact &= (int)(pq[i] == 0.0f) | (int)(pq[i] >= 0x1p-29f);
     }
     rank += __shfl_xor(rank, 16, PP_WAVE);
     cum += __shfl_xor(cum, 16, PP_WAVE);
@@ -743,187 +782,206 @@ __global__ __launch_bounds__(64 * NW) void decode16_kernel(
       k = __popcll(__ballot(sel) & 0xffffull);
     } else {
       if (lane < 16) srt_s[rank] = p;
-      wave_sync_lds();
+      wave_lds_sync();
       k = tau_cut([&](int q) { return srt_s[q]; }, 16, tau);
       sel = rank < k;
     }
-    // full selection in rank order (telemetry), and the main stream's list: the same
-    // without e1 / e2 when selected (their records come from the speculative loads)
-    top_experts(e1, e2);
-    const unsigned long long selm = __ballot(sel);
-    const bool e1_sel = e1 >= 0 && ((selm >> e1) & 1ull);
-    const bool e2_sel = e2 >= 0 && ((selm >> e2) & 1ull);
-    const int rank_e1 = e1 >= 0 ? __builtin_amdgcn_readlane(rank, e1) : 0;
-    const int rank_e2 = e2 >= 0 ? __builtin_amdgcn_readlane(rank, e2) : 0;
     if (lane < 16 && sel) {
-      sel_ids_s[rank] = j;
-      sel_g_s[rank] = pg_s[16 + j];
-      if (!(e1_sel && j == e1) && !(e2_sel && j == e2)) {
-        const int mi = rank - ((e1_sel && rank > rank_e1) ? 1 : 0) - ((e2_sel && rank > rank_e2) ? 1 : 0);
-        main_ids_s[mi] = j;
-        main_g_s[mi] = pg_s[16 + j];
+      L_s[rank] = j;
+      Lg_s[rank] = pg_s[16 + j];
+    }
+    if (lane == 0) k_s = k;
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    if (lane == 0) __hip_atomic_store(&ready_s, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    // the first pass's down rows of every selected position, DMA'd by this wave (the
+    // streaming waves then wait on their own record loads only) -- except position 0 when
+    // no logit is NaN: wave NW-1 requests it before the cut and corrects it after
+    // the first pass's down rows of every selected position, DMA'd by this wave (the
+    // streaming waves then wait on their own record loads only; a wave that issued DMAs
+    // ahead of its records would hold each act until its down rows had landed) --
+    // except position 0 when no logit is NaN: wave NW-1 requests it before the cut and
+    // corrects it after
+    if (h0 < h1)
+      for (int s = __all(xl == xl) ? 1 : 0; s < k; ++s) dma_rows(s, L_s[s], h0, p0_end);
+    if (b == 0) {  // telemetry for the caller
+      if (lane < 16) st_rlx(&st->logits[lane], xl);
+      if (lane < k) {
+        st_rlx(&st->sel_ids[lane], L_s[lane]);
+        st_rlx(&st->sel_gates[lane], Lg_s[lane]);
       }
+      if (lane == 0) st_rlx(&st->k, k);
     }
-    if (lane == 0) {
-      k_s = k;
-      kmain_s = k - (e1_sel ? 1 : 0) - (e2_sel ? 1 : 0);
-      spec_s = (e1_sel ? 1 : 0) | (e2_sel ? 2 : 0);
-    }
-  }
-  // wave wv >= 1 loads speculative record wv - 1 of this workgroup's shares: e1's share
-  // [s0, s1) first, then e2's
-  int s0 = 0, s1 = 0, es = -1, ebit = 0, rs = 0;
-  if (wv != 0) {
-    top_experts(e1, e2);
-    if (e1 >= 0) {
-      pp_split((uint32_t)G, (uint32_t)W, (uint32_t)b, s0, s1);
-      const int q = wv - 1, nsh = s1 - s0;
-      if (q < nsh) {
-        es = e1, ebit = 1, rs = s0 + q;
-      } else if (e2 >= 0 && q < 2 * nsh) {
-        es = e2, ebit = 2, rs = s0 + q - nsh;
+    // the other bank (the next call's): this workgroup's share of clearing it
+    uint32_t* nb = banks + (size_t)((epoch + 1u) & 1u) * DEC2_BANK_WORDS;
+    int lo_w, hi_w;
+    pp_split((uint32_t)DEC2_BANK_WORDS, (uint32_t)W, (uint32_t)b, lo_w, hi_w);
+    for (int i = lo_w + lane; i < hi_w; i += 64) st_rlx(&nb[i], 0u);
+    if (b == 0) {
+      // once every workgroup of the call has marked itself alive (so has read the epoch),
+      // advance the epoch: the next call uses the other bank
+      bool ok = true;
+      for (int i = lane; i < W; i += 64) {
+        uint32_t n = 0;
+        while (ld_rlx(&bank[AW + i]) == 0u) {
+          __builtin_amdgcn_s_sleep(8);
+          if (++n > DEC_SPIN_LIMIT) {
+            ok = false;
+            break;
+          }
+        }
       }
+      if (!__all(ok) && lane == 0) {
+        __hip_atomic_fetch_or(&st->error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        st_rlx(&st->error_call, epoch + 1u);
+      }
+      if (lane == 0) st_rlx(&st->epoch16, epoch + 1u);
     }
-  }
-  const bool have_spec = es >= 0;
-  uint4 sg[CPL], su[CPL], sd[CPL];
-  if (have_spec) {
-    const uint4* rec = (const uint4*)(rows + ((int64_t)es * G + rs) * 3 * H);
-#pragma unroll
-    for (int c = 0; c < CPL; ++c) {
-      sg[c] = rec[lane + 64 * c];
-      su[c] = rec[HC + lane + 64 * c];
-      sd[c] = rec[2 * HC + lane + 64 * c];
-    }
-  }
-
-  wg_lds_barrier();  // LDS only: the speculative loads stay in flight
-  const int k = k_s;
-  if (b == 0) {  // telemetry for the caller
-    if (tid < 16) st_rlx(&st->logits[tid], lg_s[tid]);
-    if (tid < k) {
-      st_rlx(&st->sel_ids[tid], sel_ids_s[tid]);
-      st_rlx(&st->sel_gates[tid], sel_g_s[tid]);
-    }
-    if (tid == 0) st_rlx(&st->k, k);
-  }
-
-  dec_clear_previous(acc, hs, hclear, epoch, b, W, tid, NT, DEC16_NCOPY);
-
-  // ---- stream the selected neuron records (as decode_kernel)
-  const bool spec_used = spec_s != 0;
-  const int T = kmain_s * G;
-  int v0, v1;
-  pp_split((uint32_t)T, (uint32_t)W, (uint32_t)b, v0, v1);
-  const int n = v1 - v0;
-  int r = v0 + (n * wv) / NW;
-  const int r_end = v0 + (n * (wv + 1)) / NW;
-  float oacc[CPL][8];
-#pragma unroll
-  for (int c = 0; c < CPL; ++c)
-#pragma unroll
-    for (int i = 0; i < 8; ++i) oacc[c][i] = 0.0f;
-  // one record: gate/up dots over the wave, silu(g) * u * gate, acc += act * down
-  auto process = [&](const uint4(&g2)[CPL], const uint4(&u2)[CPL], const uint4(&d2)[CPL], float gwt) {
-    float gs = 0.0f, us = 0.0f;
-#pragma unroll
-    for (int c = 0; c < CPL; ++c) {
-      gs = dot8_bf16(g2[c], xb[c], gs);
-      us = dot8_bf16(u2[c], xb[c], us);
-    }
-    gs = wave_sum_dpp(gs);
-    us = wave_sum_dpp(us);
-    const float av = pp_silu(gs) * us * gwt;
-#pragma unroll
-    for (int c = 0; c < CPL; ++c) axpy8(av, d2[c], oacc[c]);
-  };
-  uint4 gq[CPL], uq[CPL], dq[CPL];
-  int s_cur = 0, g_cur = 0;
-  if (r < r_end) {
-    s_cur = (int)((uint32_t)r / (uint32_t)G);
-    g_cur = r - s_cur * G;
-    const uint4* rec = (const uint4*)(rows + ((int64_t)main_ids_s[s_cur] * G + g_cur) * 3 * H);
-#pragma unroll
-    for (int c = 0; c < CPL; ++c) {
-      gq[c] = rec[lane + 64 * c];
-      uq[c] = rec[HC + lane + 64 * c];
-      dq[c] = rec[2 * HC + lane + 64 * c];
-    }
-  }
-  // the speculative record (loaded before the selection) with its expert's gate
-  if (have_spec && (spec_s & ebit)) process(sg, su, sd, pg_s[16 + es]);
-  for (; r < r_end; ++r) {
-    uint4 g2[CPL], u2[CPL], d2[CPL];
-#pragma unroll
-    for (int c = 0; c < CPL; ++c) { g2[c] = gq[c]; u2[c] = uq[c]; d2[c] = dq[c]; }
-    const float gwt = main_g_s[s_cur];
-    if (r + 1 < r_end) {
-      if (++g_cur == G) { g_cur = 0; ++s_cur; }
-      const uint4* rec = (const uint4*)(rows + ((int64_t)main_ids_s[s_cur] * G + g_cur) * 3 * H);
+  } else {
+    // ---- waves 1 .. NW-1: once the selection is published, every load of the wave is
+    // issued at once (its records and the first pass's down rows of its positions), then
+    // the records are reduced and published as they arrive. (Loads issued before the cut
+    // on a guess do not pay: with the whole layer requested at once the memory pipeline
+    // is saturated and a wave stalls at issue, so whatever a guess misses is requested
+    // microseconds late.)
+    const int Q = W * NS;
+    const int t0 = (wv - 1) * W + b, t1 = t0 + Q;
+    uint4 ga[CPL], ua[CPL], gb[CPL], ub[CPL];
+    auto load_rec = [&](uint4 (&gq)[CPL], uint4 (&uq)[CPL], int t) {
+      const int s = t / G;
+      const uint4* rec = (const uint4*)(gu + ((int64_t)L_s[s] * G + (t - s * G)) * rec_h * H);
 #pragma unroll
       for (int c = 0; c < CPL; ++c) {
-        gq[c] = rec[lane + 64 * c];
-        uq[c] = rec[HC + lane + 64 * c];
-        dq[c] = rec[2 * HC + lane + 64 * c];
+        gq[c] = ld_nt(&rec[lane + 64 * c]);
+        uq[c] = ld_nt(&rec[HC + lane + 64 * c]);
+      }
+    };
+    auto dots_publish = [&](const uint4 (&gq)[CPL], const uint4 (&uq)[CPL], int t) {
+      float gs = 0.0f, us = 0.0f;
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) {
+        gs = dot8_bf16(gq[c], xb[c], gs);
+        us = dot8_bf16(uq[c], xb[c], us);
+      }
+      gs = wave_sum_dpp(gs);
+      us = wave_sum_dpp(us);
+      if (lane < DEC2_REPS) st_rlx(&bank[lane * DEC2_RS + t], dec2_word(pp_silu(gs) * us * Lg_s[t / G]));
+    };
+    // Position 0 (rank 0) is always selected and is the expert with the largest logit
+    // unless probabilities tie: its records and down rows are requested before the cut is
+    // known (one sixth of the layer's bytes at tau 0.70, in flight during the selection);
+    // after the cut they are used if rank 0 is that expert, requested again otherwise.
+    const bool spec_ok = __all(xl == xl);
+    const int e_top = (int)__builtin_ctz((uint32_t)(__ballot(xl == m) & 0xffffull) | 0x8000u);
+    const bool sp_rec = spec_ok && t0 < G, sp_dma = spec_ok && wv == NW - 1 && h0 < h1;
+    if (sp_rec) {
+      const uint4* rec = (const uint4*)(gu + ((int64_t)e_top * G + t0) * rec_h * H);
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) {
+        ga[c] = ld_nt(&rec[lane + 64 * c]);
+        ua[c] = ld_nt(&rec[HC + lane + 64 * c]);
       }
     }
-    process(g2, u2, d2, gwt);
+    if (sp_dma) dma_rows(0, e_top, h0, p0_end);
+    while (__hip_atomic_load(&ready_s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) == 0) __builtin_amdgcn_s_sleep(1);
+    asm volatile("" ::: "memory");
+    const int k = k_s;
+    const int T = k * G;
+    const bool top_ok = L_s[0] == e_top;
+    if ((sp_rec || sp_dma) && !top_ok) vm_wait();  // a wrong guess has landed before it is replaced
+    if (sp_dma && !top_ok) dma_rows(0, L_s[0], h0, p0_end);
+    if (t0 < T && !(sp_rec && top_ok)) load_rec(ga, ua, t0);
+    if (t1 < T) load_rec(gb, ub, t1);
+    for (int t = t0; t < T; t += 2 * Q) {
+      dots_publish(ga, ua, t);
+      const int ta = t + 2 * Q, tb = t + Q;
+      if (ta < T) load_rec(ga, ua, ta);
+      if (tb < T) {
+        dots_publish(gb, ub, tb);
+        if (tb + 2 * Q < T) load_rec(gb, ub, tb + 2 * Q);
+      }
+    }
   }
 
-  // ---- workgroup reduction -> one of DEC16_NCOPY fp32 accumulators
-  // every wave parks its partials in its LDS slot, then every thread folds the slots in
-  // wave order for contiguous h and adds to the copy (uniform over the workgroup:
-  // whether it has records of a speculated expert, from the same split)
-  const bool spec_wg = spec_used && ((uint32_t)G / (uint32_t)W > 0u || (uint32_t)b < (uint32_t)G % (uint32_t)W);
-  if (n > 0 || spec_wg) {
+  // ---- phase 2: every act word of the call into LDS (bounded wait; replica b % DEC2_REPS),
+  // then the rows. Polling starts once this workgroup's own records are published (its
+  // polls would otherwise compete with the record stream at the memory side). Wave 0,
+  // idle during the stream, first runs this code once dry (one poll round, no waits, no
+  // output): the instruction cache is cold at each launch, and the dry pass brings the
+  // code in before the real pass needs it.
+  const int k = k_s;
+  const int T = k * G;
+  const uint32_t* rbank = bank + (b % DEC2_REPS) * DEC2_RS;
+#pragma nounroll
+  for (int pass = wv == 0 ? 0 : 1; pass < 2; ++pass) {
+    const bool dry = pass == 0;
+    if (!dry) __syncthreads();
+    // every word of this thread loaded at once (T <= 16 * G <= 16 * NT), then the words
+    // still 0 re-polled together: one memory round trip per round
+    bool fail = false;
+    uint32_t v[16];
 #pragma unroll
-    for (int c = 0; c < CPL; ++c) {
-      float4* dst = (float4*)(red + wv * H + (lane + 64 * c) * 8);
-      dst[0] = make_float4(oacc[c][0], oacc[c][1], oacc[c][2], oacc[c][3]);
-      dst[1] = make_float4(oacc[c][4], oacc[c][5], oacc[c][6], oacc[c][7]);
+    for (int u = 0; u < 16; ++u) {
+      const int i = tid + NT * u;
+      v[u] = i < T ? ld_rlx(&rbank[i]) : 1u;
     }
-    __syncthreads();
-    dec_acc_t* accc = dec_acc_set(acc, hs, epoch) + (b % DEC16_NCOPY) * hs;
+    uint32_t n = 0;
+    while (!dry && !fail) {
+      bool pending = false;
 #pragma unroll
-    for (int i = 0; i < (H + NT - 1) / NT; ++i) {
-      const int h = tid + NT * i;
-      if (h < H) {
-        float v = red[h];
-#pragma unroll
-        for (int w = 1; w < NW; ++w) v += red[w * H + h];
-        dec_acc_add(accc + h, v, st, epoch);
-      }
-    }
-  }
-  vm_wait();  // every wave's accumulator atomics are performed before the ticket
-  __syncthreads();
-  if (tid == 0) flag_s = dec_ticket(dec_tickets(acc, hs), b, W);
-  __syncthreads();
-  if (flag_s) {  // last workgroup: fold copies, write bf16, advance the epoch, reset the counter
-    // every load of the fold is issued before the first add (one round trip)
-    constexpr int HPT = (H + NT - 1) / NT;
-    const dec_acc_t* accs = dec_acc_set(acc, hs, epoch);
-    const bool failed = ld_rlx(&st->error_call) == epoch + 1u || (ld_rlx(&st->error) & 1u) != 0u;
-    dec_acc_t sv[HPT][DEC16_NCOPY];
-#pragma unroll
-    for (int i = 0; i < HPT; ++i)
-#pragma unroll
-      for (int c = 0; c < DEC16_NCOPY; ++c) {
-        const int h = tid + NT * i;
-        sv[i][c] = h < H ? ld_rlx(accs + c * hs + h) : (dec_acc_t)0;
+      for (int u = 0; u < 16; ++u) pending |= v[u] == 0u;
+      if (!pending) break;
+      __builtin_amdgcn_s_sleep(4);
+      if (++n > DEC_SPIN_LIMIT) {
+        fail = true;
+        break;
       }
 #pragma unroll
-    for (int i = 0; i < HPT; ++i) {
-      const int h = tid + NT * i;
-      if (h < H) {
-        dec_acc_t tot = 0;
+      for (int u = 0; u < 16; ++u)
+        if (v[u] == 0u) v[u] = ld_rlx(&rbank[tid + NT * u]);
+    }
 #pragma unroll
-        for (int c = 0; c < DEC16_NCOPY; ++c) tot += sv[i][c];
-        out[h] = failed ? (bf16_t)0x7fc0 : f32_to_bf16(dec_from_fixed(tot));
+    for (int u = 0; u < 16; ++u) {
+      const int i = tid + NT * u;
+      if (i < T) act_s[i] = __uint_as_float(~v[u]);
+    }
+    bool failed = false;
+    if (!dry) {
+      if (fail) fail_s = 1;
+      vm_wait();  // this wave's down-row DMAs have landed
+      __syncthreads();
+      failed = fail_s != 0;
+      if (failed && tid == 0) {
+        __hip_atomic_fetch_or(&st->error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        st_rlx(&st->error_call, epoch + 1u);
       }
     }
-    dec_ticket_reset(dec_tickets(acc, hs), W, tid);
-    if (tid == 0) st_rlx(&st->router_ticket, epoch + 1u);
+    for (int r0 = h0; r0 < h1; r0 += rp) {
+      const int r1 = min(h1, r0 + rp);
+      if (r0 != h0) {  // later passes (grids smaller than H / rp): DMA, then compute
+        if (dry) break;
+        __syncthreads();
+        for (int s = wv; s < k; s += NW) dma_rows(s, L_s[s], r0, r1);
+        vm_wait();
+        __syncthreads();
+      }
+      const int r = r0 + wv;  // wave wv: one row of the pass, lane: one 16-byte chunk
+      if (r < r1) {
+        float acc = 0.0f;
+        if (lane < cpr) {
+          const unsigned char* dp = dn_s + (size_t)(wv * G + 8 * lane) * 2;
+          const float* ap = act_s + 8 * lane;
+#pragma unroll 4
+          for (int s = 0; s < k; ++s) {
+            const uint4 w = *(const uint4*)(dp + (size_t)s * slot_bytes);
+            const float4 a0 = *(const float4*)(ap + s * G), a1 = *(const float4*)(ap + s * G + 4);
+            const float av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+            acc += dot8(w, av);
+          }
+        }
+        acc = wave_sum_dpp(acc);
+        if (lane == 0 && !dry) out[r] = failed ? (bf16_t)0x7fc0 : f32_to_bf16(acc);
+      }
+    }
   }
 }
 
@@ -932,12 +990,20 @@ __global__ void decode_ws_clear_kernel(uint32_t* p, size_t n_words) {
     p[i] = 0u;
 }
 
-// state | 2 x DEC_NCOPY x H fixed-point accumulators | DEC_SLOT_REPS x PP_MAX_EXPERTS 64-bit logit slots |
-// completion-ticket counters
+// Workspace: state | general kernel: 2 x DEC_NCOPY x hs fixed-point accumulators,
+// DEC_SLOT_REPS x PP_MAX_EXPERTS 64-bit logit slots, completion-ticket counters | E = 16
+// kernel: two act banks of DEC2_BANK_WORDS words (E = 16 only). The two kernels keep
+// separate epochs (router_ticket, epoch16), so calls of either kind may follow each other
+// on one workspace.
+static constexpr size_t dec_general_bytes(int hs) {
+  return (size_t)2 * DEC_NCOPY * hs * sizeof(dec_acc_t) + (size_t)DEC_SLOT_REPS * PP_MAX_EXPERTS * sizeof(unsigned long long) +
+         (size_t)DEC_TICKET_WORDS * sizeof(uint32_t);
+}
+static constexpr size_t dec_banks_offset(int hs) { return (dec_acc_offset() + dec_general_bytes(hs) + 255) / 256 * 256; }
+static constexpr size_t dec_banks_bytes() { return (size_t)2 * DEC2_BANK_WORDS * sizeof(uint32_t); }
+
 extern "C" size_t pp_decode_workspace_bytes(int H, int E) {
-  (void)E;
-  return dec_acc_offset() + (size_t)2 * DEC_NCOPY * H * sizeof(dec_acc_t) +
-         (size_t)DEC_SLOT_REPS * PP_MAX_EXPERTS * sizeof(unsigned long long) + (size_t)DEC_TICKET_WORDS * sizeof(uint32_t);
+  return E == 16 ? dec_banks_offset(H) + dec_banks_bytes() : dec_acc_offset() + dec_general_bytes(H);
 }
 
 extern "C" int pp_decode_workspace_init(void* workspace, int H, int E, void* stream) {
@@ -1034,25 +1100,38 @@ static int decode_check_args(const void* x, int x_dtype, int H, const float* rou
 // each copy of the previous call's set to clear.
 static int decode_dispatch(const void* x, int x_dtype, int H, const float* router_packed, const float* bias,
                            int E, int G, float tau, const void* packed, void* out_bf16, pp_decode_state* st,
-                           dec_acc_t* acc, int hs, int hclear, int grid, hipStream_t s) {
+                           dec_acc_t* acc, int hs, int hclear, uint32_t* banks, int grid, hipStream_t s) {
   const int grid_in = grid;
   if (grid == 0) grid = pp_device_cus();
   if (grid < E) grid = E;  // every expert has its router workgroup
   const int cpl = (H / 8 + 63) / 64;  // 16-byte chunks per lane per row (H <= 4096 -> <= 8)
-  if (E == 16 && H % 512 == 0) {
-    const int c = H / 512;
-    const size_t smem16 = (size_t)DEC16_NW * H * sizeof(float);
-    if (grid_in == 0) grid = pp_device_cus() / 2;  // measured best: one 8-wave workgroup per two CUs
-#define PP_DEC16_CASE(C)                                                                                     \
-  case C:                                                                                                    \
-    if (x_dtype == PP_DTYPE_F32)                                                                             \
-      decode16_kernel<float, C, DEC16_NW><<<grid, 64 * DEC16_NW, smem16, s>>>((const float*)x, router_packed, bias, G, tau, \
-                                                               (const bf16_t*)packed, (bf16_t*)out_bf16, st, acc, hs, hclear); \
-    else                                                                                                     \
-      decode16_kernel<bf16_t, C, DEC16_NW><<<grid, 64 * DEC16_NW, smem16, s>>>((const bf16_t*)x, router_packed, bias, G, tau, \
-                                                                (const bf16_t*)packed, (bf16_t*)out_bf16, st, acc, hs, hclear); \
-    break;
-    switch (c) {
+  if (E == 16 && H % 512 == 0 && G <= DEC2_GMAX) {
+    // the two-phase kernel: every workgroup waits for acts from all the others, so the
+    // grid is clamped to what the device holds at once (and to DEC2_WMAX); rows of the
+    // output per workgroup are handled rp at a time, their down rows staged in LDS
+    PP_REQUIRE(banks != nullptr, PP_ERR_INVALID, "pp_moe_decode: workspace without the E = 16 act banks");
+    int W = min(grid_in == 0 ? pp_device_cus() : grid_in, DEC2_WMAX);
+    const int nh = (H + W - 1) / W;
+    const int rp = max(1, min(min(8, nh), DEC2_DOWN_LDS / (16 * G * 2)));
+    const int slot_bytes = (rp * G * 2 + 1023) / 1024 * 1024;
+    const size_t smem = (size_t)16 * slot_bytes;
+    const bf16_t* gu = (const bf16_t*)packed;
+    const bf16_t* down_t = gu + (size_t)16 * G * 3 * H;
+#define PP_DEC16_CASE(C)                                                                                        \
+  case C: {                                                                                                     \
+    const void* kf = x_dtype == PP_DTYPE_F32 ? (const void*)decode16_kernel<float, C>                          \
+                                             : (const void*)decode16_kernel<bf16_t, C>;                         \
+    const int cap = dec_capacity(kf, 512, smem);                                                               \
+    PP_REQUIRE(cap >= 1, PP_ERR_UNSUPPORTED, "pp_moe_decode: the E = 16 kernel does not fit the device");     \
+    W = min(W, cap);                                                                                            \
+    if (x_dtype == PP_DTYPE_F32)                                                                                \
+      decode16_kernel<float, C><<<W, 512, smem, s>>>((const float*)x, router_packed, bias, G, tau, gu, 3, down_t,  \
+                                                     (bf16_t*)out_bf16, st, banks, rp, slot_bytes);            \
+    else                                                                                                        \
+      decode16_kernel<bf16_t, C><<<W, 512, smem, s>>>((const bf16_t*)x, router_packed, bias, G, tau, gu, 3, down_t, \
+                                                      (bf16_t*)out_bf16, st, banks, rp, slot_bytes);           \
+  } break;
+    switch (H / 512) {
       PP_DEC16_CASE(1)
       PP_DEC16_CASE(2)
       PP_DEC16_CASE(3)
@@ -1088,7 +1167,8 @@ extern "C" int pp_moe_decode(const void* x, int x_dtype, int H, const float* rou
   PP_REQUIRE(workspace, PP_ERR_INVALID, "pp_moe_decode: null workspace");
   pp_decode_state* st = (pp_decode_state*)workspace;
   dec_acc_t* acc = (dec_acc_t*)((char*)workspace + dec_acc_offset());
-  return decode_dispatch(x, x_dtype, H, router_packed, bias, E, G, tau, packed, out_bf16, st, acc, H, H, grid,
+  uint32_t* banks = E == 16 ? (uint32_t*)((char*)workspace + dec_banks_offset(H)) : nullptr;
+  return decode_dispatch(x, x_dtype, H, router_packed, bias, E, G, tau, packed, out_bf16, st, acc, H, H, banks, grid,
                          (hipStream_t)stream);
 }
 
@@ -1101,11 +1181,9 @@ extern "C" int pp_moe_decode(const void* x, int x_dtype, int H, const float* rou
 // passes `scratch` itself (in host code it names a host-side stand-in, not device
 // memory): the device address comes from hipGetSymbolAddress, once per device.
 #define PP_DECODE_SCRATCH_HS 4096
-static constexpr size_t kDecScratchBytes =
-    dec_acc_offset() + (size_t)2 * DEC_NCOPY * PP_DECODE_SCRATCH_HS * sizeof(dec_acc_t) +
-    (size_t)DEC_SLOT_REPS * PP_MAX_EXPERTS * sizeof(unsigned long long) + (size_t)DEC_TICKET_WORDS * sizeof(uint32_t);
-static_assert(kDecScratchBytes == 306560, "decode scratch: 299 KB per GPU (state, int64 accumulators at stride 4096, "
-                                          "slot replicas, ticket counters)");
+static constexpr size_t kDecScratchBytes = dec_banks_offset(PP_DECODE_SCRATCH_HS) + dec_banks_bytes();
+static_assert(kDecScratchBytes == 577024, "decode scratch: 564 KB per GPU (state, int64 accumulators at stride 4096, "
+                                          "slot replicas, ticket counters, the E = 16 kernel's act banks)");
 static __device__ __align__(256) unsigned char scratch[kDecScratchBytes];
 
 static std::mutex g_scratch_mu;
@@ -1146,6 +1224,7 @@ extern "C" int pp_moe_decode_noalloc(const void* x, int x_dtype, int H, const fl
   if (rc) return rc;
   pp_decode_state* st = (pp_decode_state*)ptr;
   dec_acc_t* acc = (dec_acc_t*)((char*)ptr + dec_acc_offset());
+  uint32_t* banks = (uint32_t*)((char*)ptr + dec_banks_offset(PP_DECODE_SCRATCH_HS));
   return decode_dispatch(x, x_dtype, H, router_packed, bias, E, G, tau, packed, out_bf16, st, acc,
-                         PP_DECODE_SCRATCH_HS, PP_DECODE_SCRATCH_HS, grid, s);
+                         PP_DECODE_SCRATCH_HS, PP_DECODE_SCRATCH_HS, banks, grid, s);
 }

@@ -49,11 +49,12 @@ def test_decode_c1_vs_fixture(pkg, c1, ti):
     epoch = None
     for t in range(x.shape[0]):
         out, st = _decode_one(pkg, m, x[t])
-        assert st["error"] == 0 and st["ready"] == 0 and st["done"] == 0
-        # the call epoch (accumulator set parity) advances by one per call
+        assert st["error"] == 0 and st["done"] == 0
+        # the E = 16 kernel's call epoch (act bank parity) advances by one per call; the
+        # general kernel's epoch is left alone
         if epoch is not None:
-            assert st["router_ticket"] == epoch + 1
-        epoch = st["router_ticket"]
+            assert st["epoch16"] == epoch[0] + 1 and st["router_ticket"] == epoch[1]
+        epoch = (st["epoch16"], st["router_ticket"])
         lg = st["logits"].numpy()
         np.testing.assert_allclose(lg, z["logits"][t], rtol=1e-5, atol=1e-5)
         sel = oracle.select(lg[None], tau)
@@ -385,14 +386,14 @@ def test_prefill_expert_with_129_pairs(pkg):
 
 @pytest.mark.parametrize("tau,want", [(0.2, [1]), (0.7, [1, 3, 0, 2, 4, 5, 6])])
 def test_decode_top_expert_speculation(pkg, tau, want):
-    """E = 16 decode loads the records of the largest-logit expert before the selection
-    is known. With an identity router the logits are x[:16]: experts 1 and 3 get logits
-    one ulp apart at 1e-4 (the other 14 at -2), so exp(x - max) is exactly 1 for both,
-    their probabilities tie and rank 0 is expert 1 (lower index) although expert 3 has
-    the larger logit. tau=0.2 selects only expert 1 (the speculative loads of expert 3
-    must be dropped); tau=0.7 selects expert 3 at rank 1 (from the speculative loads) and
-    the rest from the main stream. Output vs the fp64 sparse reference on the oracle's
-    selection."""
+    """E = 16 decode requests the records and down rows of the largest-logit expert (as
+    rank 0) before the selection is known. With an identity router the logits are
+    x[:16]: experts 1 and 3 get logits one ulp apart at 1e-4 (the other 14 at -2), so
+    exp(x - max) is exactly 1 for both, their probabilities tie and rank 0 is expert 1
+    (lower index) although expert 3 has the larger logit: the speculative loads (expert
+    3) must be replaced by expert 1's. tau=0.2 selects only expert 1; tau=0.7 selects
+    expert 3 at rank 1 and five more. Twice in a row (both act banks). Output vs the fp64
+    sparse reference on the oracle's selection."""
     E, H, G = 16, 1536, 384
     w = np.zeros((E, H), np.float32)
     w[np.arange(E), np.arange(E)] = 1.0
@@ -410,7 +411,7 @@ def test_decode_top_expert_speculation(pkg, tau, want):
     x[:E] = -2.0
     x[3] = np.float32(1e-4)
     x[1] = np.nextafter(x[3], np.float32(-np.inf))
-    for _ in range(2):  # both accumulator sets
+    for _ in range(2):  # both act banks
         out = pkg.ops.moe_decode(to_gpu(x), rp, None, E, G, tau, packed, ws)
         st = pkg.ops.decode_state(ws, E)
         assert st["error"] == 0

@@ -4,10 +4,10 @@ Every kernel variant the library dispatches by shape gets at least one case, eac
 checked against the float64 sparse restatement on the same bf16 operands (rtol 2e-2 /
 atol 2e-3) with the selection bit-exact against the oracle on the kernel's own logits:
 
-* decode: decode16_kernel (E = 16, H % 512 == 0; with and without the speculative
-  loads, CPL <= 4 / CPL = 8) and decode_kernel (any other E or H; eight waves for
-  H <= 2560, four above; the workgroup selection's rank merge over one to four 64-key
-  runs, with and without a padded last run);
+* decode: decode16_kernel (E = 16, H % 512 == 0, G <= 512; CPL 1, 3 and 8, G = 512 at
+  its limit) and decode_kernel (any other E, H or G, E = 16 with G > 512 among them;
+  eight waves for H <= 2560, four above; the workgroup selection's rank merge over one
+  to four 64-key runs, with and without a padded last run);
 * prefill routing: route16_few_kernel (E = 16, N <= 64, H % 512 == 0, H <= 2048),
   route16_kernel (other E = 16 cases) and route_kernel (E != 16);
 * prefill GEMMs: gemm_s_kernel (N <= 64, G % 64 == 0, H >= 384), gemm_v3_kernel
@@ -29,7 +29,9 @@ CASES = [
     (128, 16, 32, 3, 0.7, torch.float32, False),       # smallest H; G % 64 == 32 GEMMs; route16_few
     (640, 16, 64, 1, 0.7, torch.float32, False),       # E = 16 but H % 512 != 0: decode_kernel
     (640, 16, 64, 70, 0.7, torch.float32, True),       # route16 with H % 512 != 0 and a bias; gemm_v3 at N = 70
-    (4096, 16, 128, 1, 0.7, torch.float32, False),     # decode16 at CPL = 8 (no speculative loads)
+    (4096, 16, 128, 1, 0.7, torch.float32, False),     # decode16 at CPL = 8 (two passes of output rows per workgroup)
+    (512, 16, 512, 1, 0.9, torch.bfloat16, False),     # decode16 at CPL = 1 and its G limit (512)
+    (2048, 16, 1024, 1, 0.7, torch.float32, True),     # E = 16 with G > 512: decode_kernel (local logits)
     (4096, 16, 128, 40, 0.5, torch.bfloat16, False),   # H > 2048: route16 at N <= 64; short tiles
     (2048, 16, 64, 64, 0.95, torch.float32, True),     # route16_few at CPL = 4 with a bias; short tiles at N = 64
     (1024, 8, 96, 33, 0.9, torch.float32, False),      # route_kernel (E = 8); gateup/down kernels (G = 96)
