@@ -679,7 +679,10 @@ __device__ __forceinline__ float dec16_logits(const XT* __restrict__ x, const fl
 #define DEC2_WMAX 1024         // workgroups per call at most (alive words per bank)
 #define DEC2_GMAX 512          // neurons per expert at most (acts of one call fit LDS: 16 * 512 words)
 #define DEC2_RS (16 * DEC2_GMAX)  // words per act replica: a fixed layout, whatever the call's G
-#define DEC2_BANK_WORDS (DEC2_REPS * DEC2_RS + DEC2_WMAX)
+#define DEC2_LREPS 16          // replicas of the published logit words (decode2p_kernel)
+#define DEC2_LOGITS (DEC2_REPS * DEC2_RS)                    // bank offset of the logit words
+#define DEC2_ALIVE (DEC2_LOGITS + DEC2_LREPS * PP_MAX_EXPERTS)  // bank offset of the alive marks
+#define DEC2_BANK_WORDS (DEC2_ALIVE + DEC2_WMAX)
 #define DEC2_DOWN_LDS (96 * 1024)  // LDS for the down rows of one pass (16 positions)
 
 // LDS writes of this wave visible to its other lanes (LDS executes a wave's operations in
@@ -719,9 +722,8 @@ __global__ __launch_bounds__(512) void decode16_kernel(
   const int W = gridDim.x, b = blockIdx.x;
   const uint32_t epoch = ld_rlx(&st->epoch16);
   uint32_t* bank = banks + (size_t)(epoch & 1u) * DEC2_BANK_WORDS;
-  constexpr int AW = DEC2_REPS * DEC2_RS;  // act words per bank (replicas)
   if (tid == 0) {
-    st_rlx(&bank[AW + b], 1u);  // alive
+    st_rlx(&bank[DEC2_ALIVE + b], 1u);  // alive
     fail_s = (ld_rlx(&st->error) & 1u) != 0u;  // an earlier wait timed out: NaN until re-initialised
     ready_s = 0;
   }
@@ -822,7 +824,7 @@ __global__ __launch_bounds__(512) void decode16_kernel(
       bool ok = true;
       for (int i = lane; i < W; i += 64) {
         uint32_t n = 0;
-        while (ld_rlx(&bank[AW + i]) == 0u) {
+        while (ld_rlx(&bank[DEC2_ALIVE + i]) == 0u) {
           __builtin_amdgcn_s_sleep(8);
           if (++n > DEC_SPIN_LIMIT) {
             ok = false;
@@ -985,16 +987,289 @@ __global__ __launch_bounds__(512) void decode16_kernel(
   }
 }
 
+// ------------------------------------------------------------------ two-phase decode, any E
+// decode2p_kernel: the two phases of decode16_kernel for the other shapes with E*G <= 8192
+// and G <= 512 (the checkpoint's E = 192, G = 32 among them). Routing as decode_kernel:
+// every workgroup routes when the router is small (E <= 16 and 16*H <= 32768); otherwise
+// workgroup e < E computes logit e and publishes it as a word (~bits, 0 = not yet written)
+// in DEC2_LREPS replicas kept in this call's act bank, and every workgroup gathers the E
+// words of replica b % DEC2_LREPS (the bank is cleared by the previous call, so no tags).
+// Selection by wave 0 (E <= 16) or by the whole workgroup. No speculation. The down rows
+// of the k selected experts are one flat list of 16-byte chunks, DMA'd by wave 0 into
+// contiguous LDS (a G = 32 row is only 64 bytes); phase 2 sums each output row over
+// (rank, chunk) items spread over the lanes, in a fixed order.
+template <typename XT, int CPL, bool LOCAL>
+__global__ __launch_bounds__(512) void decode2p_kernel(
+    const XT* __restrict__ x, int H, const float* __restrict__ router, const float* __restrict__ bias, int E,
+    int G, float tau, const bf16_t* __restrict__ gu, const bf16_t* __restrict__ down_t, bf16_t* __restrict__ out,
+    pp_decode_state* __restrict__ st, uint32_t* __restrict__ banks, int rp) {
+  constexpr int NW = 8, NT = 512, NS = NW - 1;
+  extern __shared__ __align__(16) unsigned char dn_s[];  // down rows of a pass: [rank][row][G] bf16
+  __shared__ __align__(16) float act_s[DEC2_RS];
+  __shared__ SelScratch ss;
+  __shared__ unsigned long long keys_s[PP_MAX_EXPERTS];
+  __shared__ float lg_s[PP_MAX_EXPERTS];
+  __shared__ float red_s[NW];
+  __shared__ int L_s[PP_MAX_EXPERTS];
+  __shared__ float Lg_s[PP_MAX_EXPERTS];
+  __shared__ int fail_s;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int W = gridDim.x, b = blockIdx.x;
+  const int HC = H >> 3;
+  const uint32_t epoch = ld_rlx(&st->epoch16);
+  uint32_t* bank = banks + (size_t)(epoch & 1u) * DEC2_BANK_WORDS;
+  if (tid == 0) {
+    st_rlx(&bank[DEC2_ALIVE + b], 1u);
+    fail_s = (ld_rlx(&st->error) & 1u) != 0u;  // an earlier wait timed out: NaN until re-initialised
+  }
+  const uint4 zero4 = make_uint4(0, 0, 0, 0);
+  uint4 xb[CPL];  // x as packed bf16 for the records
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) xb[c] = lane + 64 * c < HC ? load_x8_bf16<XT>(x, lane + 64 * c) : zero4;
+
+  // ---- logits
+  if (LOCAL) {
+    local_logits<XT, CPL>(x, H, router, bias, E, lg_s, tid);
+  } else {
+    uint32_t* lw = bank + DEC2_LOGITS;  // [DEC2_LREPS][PP_MAX_EXPERTS]
+    if (b < E) {  // logit b: every element loaded before the first FMA, added in k order
+      constexpr int KPT = 4096 / NT;
+      float xv[KPT], wr[KPT];
+#pragma unroll
+      for (int i = 0; i < KPT; ++i) {
+        const int kk = tid + i * NT;
+        xv[i] = kk < H ? load_as_f32<XT>(x, kk) : 0.0f;
+        wr[i] = kk < H ? router[(int64_t)b * H + kk] : 0.0f;
+      }
+      float sacc = 0.0f;
+#pragma unroll
+      for (int i = 0; i < KPT; ++i)
+        if (tid + i * NT < H) sacc = __builtin_fmaf(xv[i], wr[i], sacc);
+      sacc = wave_sum(sacc);
+      if (lane == 0) red_s[wv] = sacc;
+      __syncthreads();
+      if (tid < DEC2_LREPS) {
+        float l = red_s[0];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) l = __fadd_rn(l, red_s[w]);
+        if (bias) l = __fadd_rn(l, bias[b]);
+        st_rlx(&lw[tid * PP_MAX_EXPERTS + b], dec2_word(l));
+      }
+    }
+    const uint32_t* rl = lw + (b % DEC2_LREPS) * PP_MAX_EXPERTS;
+    if (tid < E) {  // E <= 256 < NT: one word per thread, bounded wait
+      uint32_t v = ld_rlx(&rl[tid]), n = 0;
+      while (v == 0u) {
+        __builtin_amdgcn_s_sleep(1);
+        if (++n > DEC_SPIN_LIMIT) {
+          fail_s = 1;
+          v = 0x803fffffu;  // ~NaN
+          break;
+        }
+        v = ld_rlx(&rl[tid]);
+      }
+      lg_s[tid] = __uint_as_float(~v);
+    }
+    __syncthreads();
+  }
+
+  // ---- selection (rank order, gates)
+  if (E <= 16) {
+    if (wv == 0) select_one_token([&](int j) { return lg_s[j]; }, E, tau, &ss, lane);
+    __syncthreads();
+  } else {
+    select_one_token_wg([&](int j) { return lg_s[j]; }, E, tau, &ss, keys_s, red_s, tid, NT);
+  }
+  // a selection that is not a permutation of the experts (a broken sort; never, for a
+  // correct one) streams nothing and raises the error flag: the output is NaN
+  const bool bad = E > 16 && ss.bad;
+  const int k = bad ? 0 : ss.k;
+  for (int q = tid; q < k; q += NT) {
+    const int e = ss.order[q];
+    L_s[q] = e;
+    Lg_s[q] = pp_sigmoid(lg_s[e]);
+  }
+  if (tid == 0 && bad) {
+    fail_s = 1;
+    __hip_atomic_fetch_or(&st->error, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    st_rlx(&st->error_call, epoch + 1u);
+  }
+  __syncthreads();
+  const int T = k * G;
+  if (b == 0) {  // telemetry for the caller: logits and selection of this call
+    for (int j = tid; j < E; j += NT) st_rlx(&st->logits[j], lg_s[j]);
+    for (int q = tid; q < k; q += NT) {
+      st_rlx(&st->sel_ids[q], L_s[q]);
+      st_rlx(&st->sel_gates[q], Lg_s[q]);
+    }
+    if (tid == 0) st_rlx(&st->k, k);
+  }
+  {  // this workgroup's share of clearing the other bank (the next call's)
+    uint32_t* nb = banks + (size_t)((epoch + 1u) & 1u) * DEC2_BANK_WORDS;
+    int lo_w, hi_w;
+    pp_split((uint32_t)DEC2_BANK_WORDS, (uint32_t)W, (uint32_t)b, lo_w, hi_w);
+    for (int i = lo_w + tid; i < hi_w; i += NT) st_rlx(&nb[i], 0u);
+  }
+
+  int h0, h1;  // output rows of this workgroup
+  pp_split((uint32_t)H, (uint32_t)W, (uint32_t)b, h0, h1);
+  const int cpr = G >> 3;  // 16-byte chunks per down row
+  // down rows [r0, r1) of ranks 0 .. k-1 -> LDS: chunk q = (rank, row, chunk) at q * 16 (one wave)
+  auto dma_rows = [&](int r0, int r1) {
+    const int per = (r1 - r0) * cpr, nq = k * per;
+    int s = lane / per, rem = lane - s * per;  // position of chunk c0 + lane
+    for (int c0 = 0; c0 < nq; c0 += 64) {
+      const int q = min(c0 + lane, nq - 1);
+      const int sq = q == c0 + lane ? s : k - 1, rq = q == c0 + lane ? rem : per - 1;
+      const unsigned char* src = (const unsigned char*)(down_t + ((int64_t)L_s[sq] * H + r0) * G) + 16 * rq;
+      __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(dn_s + 16 * c0), 16, 0, 2);
+      rem += 64;
+      while (rem >= per) {
+        rem -= per;
+        ++s;
+      }
+    }
+  };
+  if (wv == 0) {
+    if (b == 0) {
+      // once every workgroup of the call has marked itself alive (so has read the epoch),
+      // advance the epoch: the next call uses the other bank
+      bool ok = true;
+      for (int i = lane; i < W; i += 64) {
+        uint32_t n = 0;
+        while (ld_rlx(&bank[DEC2_ALIVE + i]) == 0u) {
+          __builtin_amdgcn_s_sleep(8);
+          if (++n > DEC_SPIN_LIMIT) {
+            ok = false;
+            break;
+          }
+        }
+      }
+      if (!__all(ok) && lane == 0) {
+        __hip_atomic_fetch_or(&st->error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        st_rlx(&st->error_call, epoch + 1u);
+      }
+      if (lane == 0) st_rlx(&st->epoch16, epoch + 1u);
+    }
+    if (h0 < h1 && k > 0) dma_rows(h0, min(h1, h0 + rp));
+  } else {
+    // ---- phase 1 (waves 1 .. NW-1): records t0, t0 + Q, ... of the k*G selected ones
+    const int Q = W * NS;
+    const int t0 = (wv - 1) * W + b, t1 = t0 + Q;
+    uint4 ga[CPL], ua[CPL], gb[CPL], ub[CPL];
+    auto load_rec = [&](uint4 (&gq)[CPL], uint4 (&uq)[CPL], int t) {
+      const int s = t / G;
+      const uint4* rec = (const uint4*)(gu + ((int64_t)L_s[s] * G + (t - s * G)) * 3 * H);
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) {
+        const int ch = lane + 64 * c;
+        gq[c] = ch < HC ? ld_nt(&rec[ch]) : zero4;
+        uq[c] = ch < HC ? ld_nt(&rec[HC + ch]) : zero4;
+      }
+    };
+    auto dots_publish = [&](const uint4 (&gq)[CPL], const uint4 (&uq)[CPL], int t) {
+      float gs = 0.0f, us = 0.0f;
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) {
+        gs = dot8_bf16(gq[c], xb[c], gs);
+        us = dot8_bf16(uq[c], xb[c], us);
+      }
+      gs = wave_sum_dpp(gs);
+      us = wave_sum_dpp(us);
+      if (lane < DEC2_REPS) st_rlx(&bank[lane * DEC2_RS + t], dec2_word(pp_silu(gs) * us * Lg_s[t / G]));
+    };
+    if (t0 < T) load_rec(ga, ua, t0);
+    if (t1 < T) load_rec(gb, ub, t1);
+    for (int t = t0; t < T; t += 2 * Q) {
+      dots_publish(ga, ua, t);
+      const int ta = t + 2 * Q, tb = t + Q;
+      if (ta < T) load_rec(ga, ua, ta);
+      if (tb < T) {
+        dots_publish(gb, ub, tb);
+        if (tb + 2 * Q < T) load_rec(gb, ub, tb + 2 * Q);
+      }
+    }
+  }
+
+  // ---- phase 2: every act word of the call into LDS (replica b % DEC2_REPS, bounded
+  // wait), then the rows
+  __syncthreads();
+  const uint32_t* rbank = bank + (b % DEC2_REPS) * DEC2_RS;
+  {
+    bool fail = false;
+    uint32_t v[16];  // T <= E*G <= 16 * NT
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const int i = tid + NT * u;
+      v[u] = i < T ? ld_rlx(&rbank[i]) : 1u;
+    }
+    uint32_t n = 0;
+    while (!fail) {
+      bool pending = false;
+#pragma unroll
+      for (int u = 0; u < 16; ++u) pending |= v[u] == 0u;
+      if (!pending) break;
+      __builtin_amdgcn_s_sleep(4);
+      if (++n > DEC_SPIN_LIMIT) {
+        fail = true;
+        break;
+      }
+#pragma unroll
+      for (int u = 0; u < 16; ++u)
+        if (v[u] == 0u) v[u] = ld_rlx(&rbank[tid + NT * u]);
+    }
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const int i = tid + NT * u;
+      if (i < T) act_s[i] = __uint_as_float(~v[u]);
+    }
+    if (fail) fail_s = 1;
+  }
+  vm_wait();  // wave 0's down-row DMAs have landed
+  __syncthreads();
+  const bool failed = fail_s != 0;
+  if (failed && tid == 0) {
+    __hip_atomic_fetch_or(&st->error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    st_rlx(&st->error_call, epoch + 1u);
+  }
+  // lanes: (sub, chunk) with sub = lane / cpr when cpr divides 64 (spl ranks per wave
+  // pass), else one rank at a time; row r0 + wv of the pass on wave wv
+  const int spl = (64 % cpr == 0) ? 64 / cpr : 1;
+  const int sub = lane / cpr, cc = lane - sub * cpr;
+  for (int r0 = h0; r0 < h1; r0 += rp) {
+    const int r1 = min(h1, r0 + rp), nr = r1 - r0;
+    if (r0 != h0) {  // later passes (grids smaller than H / rp): DMA, then compute
+      __syncthreads();
+      if (wv == 0 && k > 0) dma_rows(r0, r1);
+      vm_wait();
+      __syncthreads();
+    }
+    if (wv < nr) {
+      float acc = 0.0f;
+      if (sub < spl) {
+        for (int s = sub; s < k; s += spl) {
+          const uint4 w = *(const uint4*)(dn_s + 16 * ((s * nr + wv) * cpr + cc));
+          const float4 a0 = *(const float4*)(act_s + s * G + 8 * cc), a1 = *(const float4*)(act_s + s * G + 8 * cc + 4);
+          const float av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+          acc += dot8(w, av);
+        }
+      }
+      acc = wave_sum_dpp(acc);
+      if (lane == 0) out[r0 + wv] = failed ? (bf16_t)0x7fc0 : f32_to_bf16(acc);
+    }
+  }
+}
+
 __global__ void decode_ws_clear_kernel(uint32_t* p, size_t n_words) {
   for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n_words; i += (size_t)gridDim.x * blockDim.x)
     p[i] = 0u;
 }
 
-// Workspace: state | general kernel: 2 x DEC_NCOPY x hs fixed-point accumulators,
-// DEC_SLOT_REPS x PP_MAX_EXPERTS 64-bit logit slots, completion-ticket counters | E = 16
-// kernel: two act banks of DEC2_BANK_WORDS words (E = 16 only). The two kernels keep
-// separate epochs (router_ticket, epoch16), so calls of either kind may follow each other
-// on one workspace.
+// Workspace: state | decode_kernel: 2 x DEC_NCOPY x hs fixed-point accumulators,
+// DEC_SLOT_REPS x PP_MAX_EXPERTS 64-bit logit slots, completion-ticket counters | the
+// two-phase kernels: two act banks of DEC2_BANK_WORDS words. The two families keep separate
+// epochs (router_ticket, epoch16), so calls of either kind may follow each other on one
+// workspace.
 static constexpr size_t dec_general_bytes(int hs) {
   return (size_t)2 * DEC_NCOPY * hs * sizeof(dec_acc_t) + (size_t)DEC_SLOT_REPS * PP_MAX_EXPERTS * sizeof(unsigned long long) +
          (size_t)DEC_TICKET_WORDS * sizeof(uint32_t);
@@ -1003,7 +1278,8 @@ static constexpr size_t dec_banks_offset(int hs) { return (dec_acc_offset() + de
 static constexpr size_t dec_banks_bytes() { return (size_t)2 * DEC2_BANK_WORDS * sizeof(uint32_t); }
 
 extern "C" size_t pp_decode_workspace_bytes(int H, int E) {
-  return E == 16 ? dec_banks_offset(H) + dec_banks_bytes() : dec_acc_offset() + dec_general_bytes(H);
+  (void)E;
+  return dec_banks_offset(H) + dec_banks_bytes();
 }
 
 extern "C" int pp_decode_workspace_init(void* workspace, int H, int E, void* stream) {
@@ -1145,6 +1421,55 @@ static int decode_dispatch(const void* x, int x_dtype, int H, const float* route
     return pp_check_launch("pp_moe_decode");
   }
   const bool local = E <= 16 && (int64_t)16 * H <= DEC_LOCAL_ROUTER_FLOATS;
+  if (E * G <= DEC2_RS && G <= DEC2_GMAX) {
+    // two phases, routing as decode_kernel (every workgroup routes for small routers up to
+    // H = 1536, where the router rows fit the registers); every workgroup waits for the
+    // others' acts (and, with published logits, for the E router workgroups), so the grid
+    // is at least E and at most what the device holds at once
+    PP_REQUIRE(banks != nullptr, PP_ERR_INVALID, "pp_moe_decode: workspace without the act banks");
+    int W = max(min(grid_in == 0 ? pp_device_cus() : grid_in, DEC2_WMAX), E);
+    const int nh = (H + W - 1) / W;
+    const int rp = max(1, min(min(8, nh), DEC2_DOWN_LDS / (E * G * 2)));
+    const size_t smem = (size_t)((E * rp * (G / 8) + 63) / 64 * 64) * 16;
+    const bf16_t* gu = (const bf16_t*)packed;
+    const bf16_t* down_t = gu + (size_t)E * G * 3 * H;
+    bf16_t* o = (bf16_t*)out_bf16;
+    int rc = PP_OK;
+    auto launch = [&](auto kern, auto xp) {
+      const int cap = dec_capacity((const void*)kern, 512, smem);
+      W = min(W, cap);
+      if (W < E || W < 1) {
+        pp_set_error("pp_moe_decode: the device holds %d decode workgroups at once, fewer than the %d experts' "
+                     "router workgroups", cap, E);
+        rc = PP_ERR_UNSUPPORTED;
+        return;
+      }
+      kern<<<W, 512, smem, s>>>(xp, H, router_packed, bias, E, G, tau, gu, down_t, o, st, banks, rp);
+    };
+#define PP_DEC2P_CASE(C)                                                                                           \
+  case C:                                                                                                          \
+    if (x_dtype == PP_DTYPE_F32) {                                                                                 \
+      if (local && C <= 3) launch(decode2p_kernel<float, (C <= 3 ? C : 3), true>, (const float*)x);                \
+      else launch(decode2p_kernel<float, C, false>, (const float*)x);                                              \
+    } else {                                                                                                       \
+      if (local && C <= 3) launch(decode2p_kernel<bf16_t, (C <= 3 ? C : 3), true>, (const bf16_t*)x);              \
+      else launch(decode2p_kernel<bf16_t, C, false>, (const bf16_t*)x);                                            \
+    }                                                                                                              \
+    break;
+    switch (cpl) {
+      PP_DEC2P_CASE(1)
+      PP_DEC2P_CASE(2)
+      PP_DEC2P_CASE(3)
+      PP_DEC2P_CASE(4)
+      PP_DEC2P_CASE(5)
+      PP_DEC2P_CASE(6)
+      PP_DEC2P_CASE(7)
+      PP_DEC2P_CASE(8)
+    }
+#undef PP_DEC2P_CASE
+    if (rc) return rc;
+    return pp_check_launch("pp_moe_decode");
+  }
   const bf16_t* rows = (const bf16_t*)packed;
   bf16_t* o = (bf16_t*)out_bf16;
   int rc;
@@ -1167,7 +1492,7 @@ extern "C" int pp_moe_decode(const void* x, int x_dtype, int H, const float* rou
   PP_REQUIRE(workspace, PP_ERR_INVALID, "pp_moe_decode: null workspace");
   pp_decode_state* st = (pp_decode_state*)workspace;
   dec_acc_t* acc = (dec_acc_t*)((char*)workspace + dec_acc_offset());
-  uint32_t* banks = E == 16 ? (uint32_t*)((char*)workspace + dec_banks_offset(H)) : nullptr;
+  uint32_t* banks = (uint32_t*)((char*)workspace + dec_banks_offset(H));
   return decode_dispatch(x, x_dtype, H, router_packed, bias, E, G, tau, packed, out_bf16, st, acc, H, H, banks, grid,
                          (hipStream_t)stream);
 }
@@ -1182,8 +1507,8 @@ extern "C" int pp_moe_decode(const void* x, int x_dtype, int H, const float* rou
 // memory): the device address comes from hipGetSymbolAddress, once per device.
 #define PP_DECODE_SCRATCH_HS 4096
 static constexpr size_t kDecScratchBytes = dec_banks_offset(PP_DECODE_SCRATCH_HS) + dec_banks_bytes();
-static_assert(kDecScratchBytes == 577024, "decode scratch: 564 KB per GPU (state, int64 accumulators at stride 4096, "
-                                          "slot replicas, ticket counters, the E = 16 kernel's act banks)");
+static_assert(kDecScratchBytes == 609792, "decode scratch: 596 KB per GPU (state, int64 accumulators at stride 4096, "
+                                          "slot replicas, ticket counters, the two-phase kernels' act banks)");
 static __device__ __align__(256) unsigned char scratch[kDecScratchBytes];
 
 static std::mutex g_scratch_mu;
