@@ -796,9 +796,6 @@ __global__ __launch_bounds__(512) void decode16_kernel(
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     if (lane == 0) __hip_atomic_store(&ready_s, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     // the first pass's down rows of every selected position, DMA'd by this wave (the
-    // streaming waves then wait on their own record loads only) -- except position 0 when
-    // no logit is NaN: wave NW-1 requests it before the cut and corrects it after
-    // the first pass's down rows of every selected position, DMA'd by this wave (the
     // streaming waves then wait on their own record loads only; a wave that issued DMAs
     // ahead of its records would hold each act until its down rows had landed) --
     // except position 0 when no logit is NaN: wave NW-1 requests it before the cut and
@@ -995,8 +992,8 @@ __global__ __launch_bounds__(512) void decode16_kernel(
 // in DEC2_LREPS replicas kept in this call's act bank, and every workgroup gathers the E
 // words of replica b % DEC2_LREPS (the bank is cleared by the previous call, so no tags).
 // Selection by wave 0 (E <= 16) or by the whole workgroup. No speculation. The down rows
-// of the k selected experts are one flat list of 16-byte chunks, DMA'd by wave 0 into
-// contiguous LDS (a G = 32 row is only 64 bytes); phase 2 sums each output row over
+// of the k selected experts are one flat list of 16-byte chunks, DMA'd by the streaming
+// waves into contiguous LDS (a G = 32 row is only 64 bytes); phase 2 sums each output row over
 // (rank, chunk) items spread over the lanes, in a fixed order.
 template <typename XT, int CPL, bool LOCAL>
 __global__ __launch_bounds__(512) void decode2p_kernel(
@@ -1004,8 +1001,8 @@ __global__ __launch_bounds__(512) void decode2p_kernel(
     int G, float tau, const bf16_t* __restrict__ gu, const bf16_t* __restrict__ down_t, bf16_t* __restrict__ out,
     pp_decode_state* __restrict__ st, uint32_t* __restrict__ banks, int rp) {
   constexpr int NW = 8, NT = 512, NS = NW - 1;
-  extern __shared__ __align__(16) unsigned char dn_s[];  // down rows of a pass: [rank][row][G] bf16
-  __shared__ __align__(16) float act_s[DEC2_RS];
+  extern __shared__ __align__(16) unsigned char dn_s[];  // down rows of a pass: [rank][row][G] bf16 + one pad chunk per rank
+  __shared__ __align__(16) float act_s[DEC2_RS + 4 * PP_MAX_EXPERTS];  // [rank][G + 4]: padded rows
   __shared__ SelScratch ss;
   __shared__ unsigned long long keys_s[PP_MAX_EXPERTS];
   __shared__ float lg_s[PP_MAX_EXPERTS];
@@ -1114,18 +1111,23 @@ __global__ __launch_bounds__(512) void decode2p_kernel(
   int h0, h1;  // output rows of this workgroup
   pp_split((uint32_t)H, (uint32_t)W, (uint32_t)b, h0, h1);
   const int cpr = G >> 3;  // 16-byte chunks per down row
-  // down rows [r0, r1) of ranks 0 .. k-1 -> LDS: chunk q = (rank, row, chunk) at q * 16 (one wave)
-  auto dma_rows = [&](int r0, int r1) {
-    const int per = (r1 - r0) * cpr, nq = k * per;
-    int s = lane / per, rem = lane - s * per;  // position of chunk c0 + lane
-    for (int c0 = 0; c0 < nq; c0 += 64) {
-      const int q = min(c0 + lane, nq - 1);
-      const int sq = q == c0 + lane ? s : k - 1, rq = q == c0 + lane ? rem : per - 1;
+  // down rows [r0, r1) of ranks 0 .. k-1 -> LDS, one wave: rank s's (row, chunk) c at LDS chunk
+  // s * (per + 1) + c; the chunk after each rank is padding (it fetches the rank's last
+  // chunk again), so ranks sit an odd number of chunks apart and the row sums' reads of
+  // consecutive ranks fall in different LDS banks
+  // (instructions part, part + nparts, ... of the list: the waves 1..NW-1 share it)
+  auto dma_rows = [&](int r0, int r1, int part, int nparts) {
+    const int per = (r1 - r0) * cpr, pp = per + 1, nq = k * pp, step = 64 * nparts;
+    const int first = 64 * part + lane;
+    int s = first / pp, rem = first - s * pp;  // LDS chunk c0 + lane = (rank s, chunk rem)
+    for (int c0 = 64 * part; c0 < nq; c0 += step) {
+      const bool in = c0 + lane < nq;
+      const int sq = in ? s : k - 1, rq = in ? min(rem, per - 1) : per - 1;
       const unsigned char* src = (const unsigned char*)(down_t + ((int64_t)L_s[sq] * H + r0) * G) + 16 * rq;
       __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(dn_s + 16 * c0), 16, 0, 2);
-      rem += 64;
-      while (rem >= per) {
-        rem -= per;
+      rem += step;
+      while (rem >= pp) {
+        rem -= pp;
         ++s;
       }
     }
@@ -1151,7 +1153,6 @@ __global__ __launch_bounds__(512) void decode2p_kernel(
       }
       if (lane == 0) st_rlx(&st->epoch16, epoch + 1u);
     }
-    if (h0 < h1 && k > 0) dma_rows(h0, min(h1, h0 + rp));
   } else {
     // ---- phase 1 (waves 1 .. NW-1): records t0, t0 + Q, ... of the k*G selected ones
     const int Q = W * NS;
@@ -1178,6 +1179,9 @@ __global__ __launch_bounds__(512) void decode2p_kernel(
       us = wave_sum_dpp(us);
       if (lane < DEC2_REPS) st_rlx(&bank[lane * DEC2_RS + t], dec2_word(pp_silu(gs) * us * Lg_s[t / G]));
     };
+    // this wave's share of the first pass's down rows, then its records (loads complete
+    // in issue order, so the records' waits do not hold the DMAs back)
+    if (h0 < h1 && k > 0) dma_rows(h0, min(h1, h0 + rp), wv - 1, NS);
     if (t0 < T) load_rec(ga, ua, t0);
     if (t1 < T) load_rec(gb, ub, t1);
     for (int t = t0; t < T; t += 2 * Q) {
@@ -1218,10 +1222,20 @@ __global__ __launch_bounds__(512) void decode2p_kernel(
       for (int u = 0; u < 16; ++u)
         if (v[u] == 0u) v[u] = ld_rlx(&rbank[tid + NT * u]);
     }
+    // act of (rank s, neuron g) to act_s[s * (G + 4) + g]: rows padded so the row sums'
+    // reads of consecutive ranks fall in different banks; word tid + NT u walks (s, g)
+    // by NT per step
+    int sa = tid / G, ga = tid - sa * G;
+    const int ds = NT / G, dg = NT - ds * G;
 #pragma unroll
     for (int u = 0; u < 16; ++u) {
-      const int i = tid + NT * u;
-      if (i < T) act_s[i] = __uint_as_float(~v[u]);
+      if (tid + NT * u < T) act_s[sa * (G + 4) + ga] = __uint_as_float(~v[u]);
+      sa += ds;
+      ga += dg;
+      if (ga >= G) {
+        ga -= G;
+        ++sa;
+      }
     }
     if (fail) fail_s = 1;
   }
@@ -1240,7 +1254,7 @@ __global__ __launch_bounds__(512) void decode2p_kernel(
     const int r1 = min(h1, r0 + rp), nr = r1 - r0;
     if (r0 != h0) {  // later passes (grids smaller than H / rp): DMA, then compute
       __syncthreads();
-      if (wv == 0 && k > 0) dma_rows(r0, r1);
+      if (wv == 0 && k > 0) dma_rows(r0, r1, 0, 1);
       vm_wait();
       __syncthreads();
     }
@@ -1248,8 +1262,9 @@ __global__ __launch_bounds__(512) void decode2p_kernel(
       float acc = 0.0f;
       if (sub < spl) {
         for (int s = sub; s < k; s += spl) {
-          const uint4 w = *(const uint4*)(dn_s + 16 * ((s * nr + wv) * cpr + cc));
-          const float4 a0 = *(const float4*)(act_s + s * G + 8 * cc), a1 = *(const float4*)(act_s + s * G + 8 * cc + 4);
+          const uint4 w = *(const uint4*)(dn_s + 16 * (s * (nr * cpr + 1) + wv * cpr + cc));
+          const float4 a0 = *(const float4*)(act_s + s * (G + 4) + 8 * cc);
+          const float4 a1 = *(const float4*)(act_s + s * (G + 4) + 8 * cc + 4);
           const float av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
           acc += dot8(w, av);
         }
@@ -1429,8 +1444,11 @@ static int decode_dispatch(const void* x, int x_dtype, int H, const float* route
     PP_REQUIRE(banks != nullptr, PP_ERR_INVALID, "pp_moe_decode: workspace without the act banks");
     int W = max(min(grid_in == 0 ? pp_device_cus() : grid_in, DEC2_WMAX), E);
     const int nh = (H + W - 1) / W;
-    const int rp = max(1, min(min(8, nh), DEC2_DOWN_LDS / (E * G * 2)));
-    const size_t smem = (size_t)((E * rp * (G / 8) + 63) / 64 * 64) * 16;
+    // rows per pass: the largest rp <= 8 whose LDS (E ranks x (rp rows x G / 8 chunks + one
+    // pad chunk), rounded up to whole DMA instructions) fits DEC2_DOWN_LDS
+    int rp = min(8, nh);
+    while (rp > 1 && (size_t)((E * (rp * (G / 8) + 1) + 63) / 64 * 64) * 16 > DEC2_DOWN_LDS) --rp;
+    const size_t smem = (size_t)((E * (rp * (G / 8) + 1) + 63) / 64 * 64) * 16;
     const bf16_t* gu = (const bf16_t*)packed;
     const bf16_t* down_t = gu + (size_t)E * G * 3 * H;
     bf16_t* o = (bf16_t*)out_bf16;
