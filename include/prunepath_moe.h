@@ -172,7 +172,7 @@ int pp_moe_decode(const void* x, int x_dtype, int H, const float* router_packed,
 /* Allocation-free decode. No counterpart in the reference: for callers that cannot
  * allocate device memory (code under hipGraph capture, serving loops or harnesses that
  * forbid hipMalloc). Same arguments and results as pp_moe_decode without the workspace:
- * the library's own 564 KB device array is the workspace (one per GPU, zeroed by a fill
+ * the library's own 596 KB device array is the workspace (one per GPU, zeroed by a fill
  * kernel on the caller's stream at the first call on that GPU, held until the process
  * ends). Limits: H <= 4096, E <= 256 (the library's shape limits; PP_ERR_UNSUPPORTED
  * beyond). Every call on a GPU shares that GPU's array: calls that overlap on one GPU
@@ -187,7 +187,11 @@ int pp_moe_decode_noalloc(const void* x, int x_dtype, int H, const float* router
  * epilogue (bf16 MFMA) -> grouped down GEMM -> per-token combine in fp32 -> bf16.
  * Replaces TauSparseMoE.forward_prefill (src/tl_kernel_optimized_Ultimate_PanGU.py:532-604)
  * and moe_fused_expert_kernel (:271-328). No host synchronisation.
- * workspace: pp_prefill_workspace_bytes(N, H, E, G) bytes of device scratch.
+ * workspace: pp_prefill_workspace_bytes(N, H, E, G) bytes of device scratch. The pair
+ * buffers are sized for every token selecting every expert, so the call runs in
+ * consecutive passes of at most max(64, 512 MiB / (E * H * 4)) tokens (2048 tokens in one
+ * pass at E = 16, H = 1536; 455 a pass at E = 192) and the workspace stays bounded for
+ * any N; the output is the same as one pass over all N.
  * ------------------------------------------------------------------------- */
 size_t pp_prefill_workspace_bytes(int64_t n_tokens, int H, int E, int G);
 int pp_moe_prefill(const void* x, int x_dtype, int64_t n_tokens, int H,

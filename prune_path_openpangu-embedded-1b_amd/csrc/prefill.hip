@@ -1057,22 +1057,27 @@ static PrefillWs prefill_layout(int64_t N, int H, int E, int G) {
   return L;
 }
 
-extern "C" size_t pp_prefill_workspace_bytes(int64_t n_tokens, int H, int E, int G) {
-  return prefill_layout(n_tokens, H, E, G).total;
+// Tokens per pass. The pair buffers are sized for the worst case, every token selecting
+// every expert (P = N * E pairs: fp32 y [P][H], bf16 act [P][G], the CSR), since the
+// actual P is only known on the device; a pass covers at most as many tokens as keep
+// that y within PF_PASS_Y_BYTES (2048 tokens at E = 16, H = 1536 in one pass; 455
+// tokens a pass at the checkpoint's E = 192), so the workspace stays bounded for any
+// N and E. Longer inputs run in consecutive passes on the same workspace.
+#define PF_PASS_Y_BYTES ((int64_t)512 << 20)
+static int64_t prefill_pass_tokens(int64_t N, int H, int E) {
+  const int64_t per_token = (int64_t)E * H * 4;
+  return min(N, max((int64_t)64, PF_PASS_Y_BYTES / per_token));
 }
 
-extern "C" int pp_moe_prefill(const void* x, int x_dtype, int64_t n_tokens, int H, const float* router_packed,
-                              const float* bias, int E, int G, float tau, const void* packed, void* out_bf16,
-                              void* workspace, void* stream) {
-  int rc = pp_check_shape(H, E, G);
-  if (rc) return rc;
-  PP_REQUIRE(n_tokens >= 0 && n_tokens <= (int64_t)0x7fffffff / PP_MAX_EXPERTS, PP_ERR_UNSUPPORTED,
-             "pp_moe_prefill: n_tokens %lld out of range", (long long)n_tokens);
-  PP_REQUIRE(x_dtype == PP_DTYPE_F32 || x_dtype == PP_DTYPE_BF16, PP_ERR_INVALID, "pp_moe_prefill: x_dtype %d",
-             x_dtype);
-  if (n_tokens == 0) return PP_OK;
-  PP_REQUIRE(x && router_packed && packed && out_bf16 && workspace, PP_ERR_INVALID, "pp_moe_prefill: null pointer");
-  hipStream_t st = (hipStream_t)stream;
+extern "C" size_t pp_prefill_workspace_bytes(int64_t n_tokens, int H, int E, int G) {
+  return prefill_layout(prefill_pass_tokens(n_tokens, H, E), H, E, G).total;
+}
+
+// One pass over n_tokens tokens (at most prefill_pass_tokens) on the workspace.
+static int prefill_pass(const void* x, int x_dtype, int64_t n_tokens, int H, const float* router_packed,
+                        const float* bias, int E, int G, float tau, const void* packed, void* out_bf16,
+                        void* workspace, hipStream_t st) {
+  int rc;
   const PrefillWs L = prefill_layout(n_tokens, H, E, G);
   char* ws = (char*)workspace;
   float* gates = (float*)(ws + L.gates);
@@ -1113,4 +1118,26 @@ extern "C" int pp_moe_prefill(const void* x, int x_dtype, int64_t n_tokens, int 
   const bf16_t* down_t = (const bf16_t*)packed + (int64_t)E * G * 3 * H;
   if ((rc = down_launch(act, H, G, down_t, tiles, meta, mt, y, gws, st, short_tiles))) return rc;
   return combine_launch(y, token_pairs, count, n_tokens, H, E, (bf16_t*)out_bf16, st);
+}
+
+extern "C" int pp_moe_prefill(const void* x, int x_dtype, int64_t n_tokens, int H, const float* router_packed,
+                              const float* bias, int E, int G, float tau, const void* packed, void* out_bf16,
+                              void* workspace, void* stream) {
+  int rc = pp_check_shape(H, E, G);
+  if (rc) return rc;
+  PP_REQUIRE(n_tokens >= 0 && n_tokens <= (int64_t)0x7fffffff / PP_MAX_EXPERTS, PP_ERR_UNSUPPORTED,
+             "pp_moe_prefill: n_tokens %lld out of range", (long long)n_tokens);
+  PP_REQUIRE(x_dtype == PP_DTYPE_F32 || x_dtype == PP_DTYPE_BF16, PP_ERR_INVALID, "pp_moe_prefill: x_dtype %d",
+             x_dtype);
+  if (n_tokens == 0) return PP_OK;
+  PP_REQUIRE(x && router_packed && packed && out_bf16 && workspace, PP_ERR_INVALID, "pp_moe_prefill: null pointer");
+  const int64_t nc = prefill_pass_tokens(n_tokens, H, E);
+  const size_t xs = x_dtype == PP_DTYPE_BF16 ? 2 : 4;
+  for (int64_t n0 = 0; n0 < n_tokens; n0 += nc) {
+    const int64_t nt = min(nc, n_tokens - n0);
+    if ((rc = prefill_pass((const char*)x + (size_t)n0 * H * xs, x_dtype, nt, H, router_packed, bias, E, G, tau,
+                           packed, (bf16_t*)out_bf16 + (size_t)n0 * H, workspace, (hipStream_t)stream)))
+      return rc;
+  }
+  return PP_OK;
 }

@@ -195,6 +195,25 @@ def test_prefill_stages_vs_oracle(pkg):
     np.testing.assert_array_equal(out.float().cpu().numpy(), full)
 
 
+def test_prefill_in_passes_e192(pkg):
+    """A prefill longer than one pass (the worst-case pair buffers of a pass are bounded:
+    455 tokens a pass at E = 192, H = 1536), here 1000 tokens in three passes on a
+    workspace sized for one: every row vs the float64 reference, selection bit-exact, and
+    the output identical to the same tokens run as separate calls."""
+    E, G, N = 192, 32, 1000
+    assert pkg.ops.prefill_workspace_bytes(N, 1536, E, G) == pkg.ops.prefill_workspace_bytes(455, 1536, E, G)
+    w = gi.layer_weights(41, E=E)
+    m = make_module(pkg, w, 0.7)
+    x = gi.tokens(42, N)
+    out = m(to_gpu(x[None])).float().cpu().numpy()[0]
+    res = pkg.ops.route(to_gpu(x), m.router_packed, E, 0.7)
+    sel = oracle.select(res["logits"].cpu().numpy(), 0.7)
+    np.testing.assert_array_equal(res["mask"].cpu().numpy(), sel.mask)
+    assert_close(out, sparse_expected_gpu(x, w, sel.gates), what="E=192 prefill in passes")
+    parts = [m(to_gpu(x[None, a:b])).float().cpu().numpy()[0] for a, b in ((0, 455), (455, 910), (910, N))]
+    np.testing.assert_array_equal(np.concatenate(parts), out)
+
+
 def test_real_checkpoint_shape_e192_g32(pkg):
     """E=192 experts of G=32 neurons with a reference cluster map (layer 3)."""
     ids = np.load(os.path.join(GOLDEN, "pangu_clusters_k32.npz"))["expert_ids"][3].astype(np.int32)
