@@ -149,7 +149,7 @@ int pp_bucket(const uint8_t* mask, const float* gates, int64_t n_tokens, int E, 
 typedef struct pp_decode_state {
   uint32_t router_ticket; /* internal: call epoch of the general kernel, advanced by one per call */
   uint32_t epoch16;       /* internal: call epoch of the E = 16 kernel, advanced by one per call */
-  uint32_t done;          /* internal (unused) */
+  uint32_t epochb;        /* internal: call epoch of the batch kernel (pp_moe_decode_batch) */
   uint32_t error;         /* sticky error bits, 0 = none: 1 a logit-slot wait timed out
                              (every later call on the workspace writes NaN), 2 the selection
                              was not a permutation of the experts, 4 a workgroup partial sum
@@ -181,6 +181,30 @@ int pp_moe_decode(const void* x, int x_dtype, int H, const float* router_packed,
 int pp_moe_decode_noalloc(const void* x, int x_dtype, int H, const float* router_packed,
                           const float* bias, int E, int G, float tau, const void* packed,
                           void* out_bf16, int grid, void* stream);
+
+/* Small-batch decode: 1 <= N <= 64 tokens in one launch. Replaces, for such batches,
+ * TauSparseMoE.forward_prefill (src/tl_kernel_optimized_Ultimate_PanGU.py:532-604: route,
+ * bucket, fused expert kernel, scatter-add), which the reference forward takes for every
+ * N > 1 (:606-615); same selection and output semantics as pp_moe_prefill on the same
+ * tokens, for the E = 16 family (E == 16, H % 512 == 0, G <= 512; PP_ERR_UNSUPPORTED
+ * otherwise, so a caller can fall back to pp_moe_prefill). Every token's routing, the
+ * gate/up MFMA over the union of the selected experts, the down projection and the fold
+ * run in one kernel whose workgroups exchange data through the two workspaces:
+ * workspace is a decode workspace (pp_decode_workspace_bytes, zeroed once by
+ * pp_decode_workspace_init; it carries the call epoch and the per-workgroup flags and may
+ * be the one the layer's pp_moe_decode calls use), batch_workspace
+ * pp_decode_batch_workspace_bytes(H, E, G) bytes needing no initialisation. Calls that
+ * share either must be ordered on one stream. logits_out ([N][16] fp32) and mask_out
+ * ([N][16] uint8) receive the routing when not null. The output is the same bits on
+ * every call (fixed summation orders). Error reporting as pp_moe_decode (error bit 1: a
+ * wait timed out, every later call writes NaN until pp_decode_workspace_init).
+ * grid = number of workgroups (0 = automatic; rounded down to a multiple of 16 and to
+ * what the device holds at once). */
+size_t pp_decode_batch_workspace_bytes(int H, int E, int G);
+int pp_moe_decode_batch(const void* x, int x_dtype, int64_t n_tokens, int H, const float* router_packed,
+                        const float* bias, int E, int G, float tau, const void* packed, void* out_bf16,
+                        float* logits_out, uint8_t* mask_out, void* workspace, void* batch_workspace,
+                        int grid, void* stream);
 
 /* ------------------------------------------------------------------------- *
  * Prefill / N > 1: route -> bucket -> grouped gate/up GEMM with fused SwiGLU

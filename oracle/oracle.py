@@ -24,12 +24,18 @@ reference repository root):
   all neurons, router, tau mask, ``intermediate * (gates @ experts_masks)``,
   down projection.
 * ``sparse_moe_from_selection`` -- the same layer evaluated sparsely from a
-  given selection, in float64, on caller-given (e.g. bf16-rounded) weights.
+  given selection, in float64, on caller-given (e.g. bf16-rounded) weights;
+  optionally with the acts rounded to bf16 before the down projection, the
+  rounding point of the reference's fused expert kernel
+  (src/tl_kernel_optimized_Ultimate_PanGU.py:318).
+* ``bf16_rne`` -- float32 to bfloat16, round to nearest even (torch's conversion).
 
 Pinning (tests/test_oracle.py): softmax/select bits against torch CPU ops in the
 container (same torch 2.10 the reference pins, requirements.txt:3) and against
 committed golden fixtures; bucket against brute force; masked MLP against the
-sparse form and against a float64 direct sum; the permutation against the
+sparse form and against a float64 direct sum; bf16_rne against torch's conversion
+(ties, subnormals, overflow, NaN) and the bf16-act form against the exact one within
+the half-ulp bound; the permutation against the
 reference-held cluster maps (src/Pangu_Clusters/*.txt).
 """
 from __future__ import annotations
@@ -210,12 +216,25 @@ def masked_moe_mlp(x, w_gate, w_up, w_down, w_router, expert_ids, tau, bias=None
     return out, sel
 
 
-def sparse_moe_from_selection(x, gate_rows, up_rows, down_cols, gates, G):
+def bf16_rne(a) -> np.ndarray:
+    """float32 values rounded to bfloat16 (round to nearest, ties to even; NaN stays a
+    quiet NaN), returned as float32 -- torch's ``.to(torch.bfloat16)``."""
+    f = np.ascontiguousarray(a, np.float32)
+    u = f.view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000).astype(np.uint32)
+    r = np.where(np.isnan(f), np.uint32(0x7FC00000), r)
+    return r.view(np.float32)
+
+
+def sparse_moe_from_selection(x, gate_rows, up_rows, down_cols, gates, G, act_bf16=False):
     """Sparse evaluation of the same layer in float64 from a given selection.
 
     x [n,H]; gate_rows/up_rows [I,H] rearranged (expert e owns rows e*G:(e+1)*G);
     down_cols [I,H] rearranged down weights (row j = column j of down_proj);
     gates [n,E] (0 where not selected). Returns out [n,H] float64.
+    act_bf16: round each act = silu(g) * u * gate to bfloat16 before the down projection,
+    as the reference's fused expert kernel does (``acc_gate.to(tl.bfloat16)``,
+    src/tl_kernel_optimized_Ultimate_PanGU.py:318).
     """
     x64 = np.asarray(x, np.float64)
     g = np.asarray(gates, np.float64)
@@ -232,5 +251,7 @@ def sparse_moe_from_selection(x, gate_rows, up_rows, down_cols, gates, G):
         sl = slice(e * G, (e + 1) * G)
         xe = x64[toks]
         act = _silu64(xe @ Wg[sl].T) * (xe @ Wu[sl].T) * g[toks, e][:, None]
+        if act_bf16:
+            act = bf16_rne(act.astype(np.float32)).astype(np.float64)
         out[toks] += act @ Wd[sl]
     return out

@@ -52,6 +52,9 @@ SIGNATURES = {
                               c_void_p, c_void_p, c_int, c_void_p]),
     "pp_moe_decode_noalloc": (c_int, [c_void_p, c_int, c_int, c_void_p, c_void_p, c_int, c_int, c_float,
                                       c_void_p, c_void_p, c_int, c_void_p]),
+    "pp_decode_batch_workspace_bytes": (c_size_t, [c_int, c_int, c_int]),
+    "pp_moe_decode_batch": (c_int, [c_void_p, c_int, c_int64, c_int, c_void_p, c_void_p, c_int, c_int, c_float,
+                                    c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_void_p]),
     "pp_prefill_workspace_bytes": (c_size_t, [c_int64, c_int, c_int, c_int]),
     "pp_moe_prefill": (c_int, [c_void_p, c_int, c_int64, c_int, c_void_p, c_void_p, c_int, c_int, c_float,
                                c_void_p, c_void_p, c_void_p, c_void_p]),

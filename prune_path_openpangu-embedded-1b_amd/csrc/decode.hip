@@ -704,6 +704,57 @@ __device__ __forceinline__ uint32_t dec2_word(float a) {
   return ~(a == a ? __float_as_uint(a) : 0x7fc00000u);
 }
 
+// Exact tau selection of one token over 16 experts, on one wave: xl = logit of expert
+// j = lane & 15 (every lane), m = the largest of the 16 logits. pg_s[0..15] receives the
+// probabilities, pg_s[16..31] the gates (sigmoid of the logit). Returns, in every lane,
+// whether expert j is selected, with its rank (descending probability, ties by index) and
+// the number k of selected experts. When every probability is 0 or >= 2^-29 the fp64
+// running sums are exact in any order, so each lane sums the probabilities ranked before
+// its own; otherwise the sorted probabilities go through tau_cut's sequential sum.
+// srt_s: LDS [16] of this wave. LDS traffic only (no barrier).
+__device__ __forceinline__ bool sel16_wave(float xl, float m, float tau, float* pg_s, float* srt_s, int lane,
+                                           int& rank_out, int& k_out) {
+  const int j = lane & 15;
+  const int grp = lane >> 4;
+  const float e = pp_expf_u10(grp == 1 ? __fsub_rn(0.0f, xl) : __fsub_rn(xl, m));
+  const float S = row16_sum(e);
+  const float r = __fdiv_rn(1.0f, grp == 1 ? __fadd_rn(e, 1.0f) : S);
+  if (lane < 32) pg_s[lane] = grp == 1 ? r : __fmul_rn(e, r);  // [p_0..15 | gate_0..15]
+  wave_lds_sync();
+  const float p = pg_s[j];
+  const float4 p4 = *(const float4*)&pg_s[4 * grp];
+  const float pq[4] = {p4.x, p4.y, p4.z, p4.w};
+  const unsigned long long kj = sel_key(p, j);
+  int rank = 0, exact = 1;
+  double cum = 0.0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const bool before = sel_key(pq[i], 4 * grp + i) < kj;
+    rank += before ? 1 : 0;
+    cum += before ? (double)pq[i] : 0.0;
+    exact &= (int)(pq[i] == 0.0f) | (int)(pq[i] >= 0x1p-29f);
+  }
+  rank += __shfl_xor(rank, 16, PP_WAVE);
+  cum += __shfl_xor(cum, 16, PP_WAVE);
+  rank += __shfl_xor(rank, 32, PP_WAVE);
+  cum += __shfl_xor(cum, 32, PP_WAVE);
+  const float tau32 = tau;
+  int k;
+  bool sel;
+  if (__all(exact)) {
+    sel = rank == 0 || (float)(cum + (double)p) < tau32;
+    k = __popcll(__ballot(sel) & 0xffffull);
+  } else {
+    if (lane < 16) srt_s[rank] = p;
+    wave_lds_sync();
+    k = tau_cut([&](int q) { return srt_s[q]; }, 16, tau);
+    sel = rank < k;
+  }
+  rank_out = rank;
+  k_out = k;
+  return sel;
+}
+
 template <typename XT, int CPL>
 __global__ __launch_bounds__(512) void decode16_kernel(
     const XT* __restrict__ x, const float* __restrict__ router, const float* __restrict__ bias, int G, float tau,
@@ -751,43 +802,10 @@ __global__ __launch_bounds__(512) void decode16_kernel(
   constexpr int NS = NW - 1;                          // streaming waves 1 .. NW-1
 
   if (wv == 0) {
-    // ---- exact selection, alone on this wave (the decode16 arithmetic); published to
-    // the other waves through an LDS flag, no barrier
-    const int grp = lane >> 4;
-    const float e = pp_expf_u10(grp == 1 ? __fsub_rn(0.0f, xl) : __fsub_rn(xl, m));
-    const float S = row16_sum(e);
-    const float r = __fdiv_rn(1.0f, grp == 1 ? __fadd_rn(e, 1.0f) : S);
-    if (lane < 32) pg_s[lane] = grp == 1 ? r : __fmul_rn(e, r);  // [p_0..15 | gate_0..15]
-    wave_lds_sync();
-    const float p = pg_s[j];
-    const float4 p4 = *(const float4*)&pg_s[4 * grp];
-    const float pq[4] = {p4.x, p4.y, p4.z, p4.w};
-    const unsigned long long kj = sel_key(p, j);
-    int rank = 0, exact = 1;
-    double cum = 0.0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const bool before = sel_key(pq[i], 4 * grp + i) < kj;
-      rank += before ? 1 : 0;
-      cum += before ? (double)pq[i] : 0.0;
-      exact &= (int)(pq[i] == 0.0f) | (int)(pq[i] >= 0x1p-29f);
-    }
-    rank += __shfl_xor(rank, 16, PP_WAVE);
-    cum += __shfl_xor(cum, 16, PP_WAVE);
-    rank += __shfl_xor(rank, 32, PP_WAVE);
-    cum += __shfl_xor(cum, 32, PP_WAVE);
-    const float tau32 = tau;
-    int k;
-    bool sel;
-    if (__all(exact)) {
-      sel = rank == 0 || (float)(cum + (double)p) < tau32;
-      k = __popcll(__ballot(sel) & 0xffffull);
-    } else {
-      if (lane < 16) srt_s[rank] = p;
-      wave_lds_sync();
-      k = tau_cut([&](int q) { return srt_s[q]; }, 16, tau);
-      sel = rank < k;
-    }
+    // ---- exact selection, alone on this wave; published to the other waves through an
+    // LDS flag, no barrier
+    int rank, k;
+    const bool sel = sel16_wave(xl, m, tau, pg_s, srt_s, lane, rank, k);
     if (lane < 16 && sel) {
       L_s[rank] = j;
       Lg_s[rank] = pg_s[16 + j];
@@ -1275,6 +1293,366 @@ __global__ __launch_bounds__(512) void decode2p_kernel(
   }
 }
 
+// ------------------------------------------------------------------ batch decode (E = 16)
+// decodeb_kernel: one launch for 1 <= N <= 64 tokens (small-batch decode), every workgroup
+// resident at once, three exchanges through the batch workspace:
+// A. workgroup b < N routes token b (dec16_logits, sel16_wave on wave 0) and publishes its
+//    16 gates (exactly -1: expert not selected; a selected gate is a sigmoid, or NaN) and
+//    x as bf16;
+// B. every workgroup reads the N x 16 gates; the union of the selected experts, ascending,
+//    gives T = nu * G union neurons, union neuron q being neuron q % G of expert
+//    U[q / G];
+// C. gate/up: workgroup b takes union neurons [q0, q1) of an even split of T, all N
+//    tokens, K = H split over the eight waves (32x32x16 MFMA: tokens x neurons, each lane
+//    streaming 64 contiguous bytes of its row per four k-steps); the eight partials are
+//    added in a fixed tree; act[t][q] = silu(g) * u * gate(t, e) (0 where token t did not
+//    select e) goes to the workspace as bf16;
+// D. down: workgroup b = 16 r + s takes the rows of row group r (8-row blocks of H split
+//    over W / 16 groups) and the union neurons of slice s (16-neuron blocks of T split
+//    over 16 slices; with all 16 experts hit, slice s is expert s): its down rows are
+//    staged in LDS during C, and MFMA (rows x tokens) over the slice writes a partial
+//    [row][token] sum in fp32;
+// E. fold: the 8-row block u of H is summed over the 16 slices in slice order by
+//    workgroup u % W, so the bf16 output is the same bits on every call.
+// Exchanges: data written with coherent (sc1) stores, then a per-workgroup flag word set
+// to the call's tag (epochb + 1) once those stores completed; readers wait for the
+// flags of the workgroups they read from, then load with sc1 (a workgroup whose wait
+// timed out publishes NaN acts and partial sums, so every output it feeds is NaN). Tags
+// grow by one per call, so flags need no clearing; workgroup 0 advances epochb once every
+// workgroup has set its last flag. Every wait is bounded: a timeout sets error bit 1 and the workgroup writes
+// NaN. Workspace reads and writes go through buffer descriptors sized to their region.
+#define DECB_MAXN 64               // tokens per call at most
+#define DECB_S 16                  // neuron slices of the down projection
+#define DECB_RED_BYTES (32 * 1024)  // LDS of the gate/up K-split reduction (four waves' partials)
+#define DECB_DOWN_LDS (96 * 1024)   // LDS of the down rows of one pass
+#define DECB_FLAG_WORDS (3 * DEC2_WMAX)  // route, act and partial flags, one word per workgroup
+
+struct DecbLayout {
+  size_t selg, xbf, act, part, total;
+};
+// batch workspace: gates [64][16] fp32 | x [64][H] bf16 | act [64][16 G] bf16 |
+// partial sums [16][H][64] fp32
+__host__ __device__ __forceinline__ DecbLayout decb_layout(int H, int G) {
+  DecbLayout L;
+  size_t o = 0;
+  L.selg = o;
+  o += (size_t)DECB_MAXN * 16 * 4;
+  L.xbf = o;
+  o += (size_t)DECB_MAXN * H * 2;
+  L.act = o;
+  o += (size_t)DECB_MAXN * 16 * G * 2;
+  L.part = o;
+  o += (size_t)DECB_S * H * DECB_MAXN * 4;
+  L.total = o;
+  return L;
+}
+
+typedef __amdgpu_buffer_rsrc_t decb_rsrc_t;
+__device__ __forceinline__ decb_rsrc_t decb_rsrc(const void* p, size_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, (int)bytes, 0x00020000);
+}
+#define DECB_SC1 16  // cache policy: coherent across the device's L2s
+#define DECB_NT 2    // cache policy: non-temporal
+template <int AUX>
+__device__ __forceinline__ uint4 decb_ld16(decb_rsrc_t r, uint32_t off) {
+  const dec_u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, AUX);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ void decb_st16(decb_rsrc_t r, uint32_t off, uint4 v) {
+  const dec_u32x4 u = {v.x, v.y, v.z, v.w};
+  __builtin_amdgcn_raw_buffer_store_b128(u, r, off, 0, DECB_SC1);
+}
+
+// bounded wait for a flag word to hold `tag`; false on timeout
+__device__ __forceinline__ bool decb_wait(const uint32_t* f, uint32_t tag) {
+  uint32_t n = 0;
+  while (ld_rlx(f) != tag) {
+    __builtin_amdgcn_s_sleep(2);
+    if (++n > DEC_SPIN_LIMIT) return false;
+  }
+  return true;
+}
+
+template <typename XT, int CPL, int TB>
+__global__ __launch_bounds__(512) void decodeb_kernel(
+    const XT* __restrict__ x, int N, const float* __restrict__ router, const float* __restrict__ bias, int G,
+    float tau, const bf16_t* __restrict__ gu, const bf16_t* __restrict__ down_t, bf16_t* __restrict__ out,
+    float* __restrict__ logits_out, uint8_t* __restrict__ mask_out, pp_decode_state* __restrict__ st,
+    uint32_t* __restrict__ flags, unsigned char* __restrict__ bw, int rows_pp) {
+  constexpr int NW = 8, NT = 512, H = 512 * CPL, HC = H / 8;
+  extern __shared__ __align__(16) unsigned char smem[];  // [reduction | down rows of a pass]
+  float* red_s = (float*)smem;
+  unsigned char* dn_s = smem + DECB_RED_BYTES;
+  __shared__ __align__(16) float part_s[16 * NW];
+  __shared__ __align__(16) float pg_s[32];
+  __shared__ __align__(16) float srt_s[16];
+  __shared__ __align__(16) float sg_s[DECB_MAXN * 16];  // gate of (token, expert); -1: not selected
+  __shared__ int ul_s[16];                              // the union of the selected experts, ascending
+  __shared__ int nu_s;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int W = gridDim.x, b = blockIdx.x;
+  const uint32_t tag = ld_rlx(&st->epochb) + 1u;
+  bool fail = (ld_rlx(&st->error) & 1u) != 0u;  // an earlier wait timed out: NaN until re-initialised
+  const DecbLayout Lb = decb_layout(H, G);
+  const int TS = 16 * G;  // act row stride (elements)
+  const decb_rsrc_t r_selg = decb_rsrc(bw + Lb.selg, Lb.xbf - Lb.selg);
+  const decb_rsrc_t r_xbf = decb_rsrc(bw + Lb.xbf, Lb.act - Lb.xbf);
+  const decb_rsrc_t r_act = decb_rsrc(bw + Lb.act, Lb.part - Lb.act);
+  const decb_rsrc_t r_part = decb_rsrc(bw + Lb.part, Lb.total - Lb.part);
+  const decb_rsrc_t r_gu = decb_rsrc(gu, (size_t)16 * G * 3 * H * 2);
+  uint32_t* rflag = flags;
+  uint32_t* aflag = flags + DEC2_WMAX;
+  uint32_t* pflag = flags + 2 * DEC2_WMAX;
+
+  // ---- A: routing of token b
+  if (b < N) {
+    const XT* xt = x + (size_t)b * H;
+    const float xl = dec16_logits<XT, CPL, NW>(xt, router, bias, part_s, lane, wv);
+    for (int c = tid; c < HC; c += NT) decb_st16(r_xbf, (uint32_t)(b * H + 8 * c) * 2, load_x8_bf16<XT>(xt, c));
+    if (wv == 0) {
+      const float m = row16_max(xl);
+      int rank, k;
+      const bool sel = sel16_wave(xl, m, tau, pg_s, srt_s, lane, rank, k);
+      if (lane < 16) {
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(sel ? pg_s[16 + lane] : -1.0f), r_selg,
+                                              (b * 16 + lane) * 4, 0, DECB_SC1);
+        if (logits_out != nullptr) logits_out[b * 16 + lane] = xl;
+        if (mask_out != nullptr) mask_out[b * 16 + lane] = sel ? 1 : 0;
+      }
+    }
+    vm_wait();
+    __syncthreads();
+    if (tid == 0) st_rlx(&rflag[b], tag);
+  }
+
+  // ---- B: every token's gates; the union of the selected experts
+  if (tid < N && !decb_wait(&rflag[tid], tag)) fail = true;
+  fail = __syncthreads_or(fail);  // from here on a failed workgroup publishes NaN
+  for (int i = tid; i < N * 16; i += NT)
+    sg_s[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r_selg, i * 4, 0, DECB_SC1));
+  __syncthreads();
+  if (wv == 0) {
+    bool hit = false;
+    if (lane < 16)
+      for (int t = 0; t < N; ++t) hit |= sg_s[t * 16 + lane] != -1.0f;
+    const unsigned long long bal = __ballot(hit);
+    if (hit) ul_s[__popcll(bal & ((1ull << lane) - 1ull))] = lane;
+    if (lane == 0) nu_s = __popcll(bal);
+  }
+  __syncthreads();
+  const int T = nu_s * G;
+  const int jn = lane & 31, kh = lane >> 5;  // TB: token blocks of 32 (N <= 32 TB)
+
+  // rows and slice of phase D (known now: its down rows are fetched during C)
+  const int R = W / DECB_S, s = b % DECB_S, r = b / DECB_S;
+  int rb0, rb1, sb0, sb1;
+  pp_split((uint32_t)(H / 8), (uint32_t)R, (uint32_t)r, rb0, rb1);
+  pp_split((uint32_t)(T / 16), (uint32_t)DECB_S, (uint32_t)s, sb0, sb1);
+  const int hr0 = 8 * rb0, hr1 = 8 * rb1;
+  const int a0 = 16 * sb0, nk = 16 * (sb1 - sb0);
+  const int cpr = nk / 8, RSB = 16 * (cpr + 1);  // staged row: cpr chunks + one pad chunk
+  // down rows [p0, p0 + nr) of the slice -> LDS: row rho at rho * RSB, chunk c (8 union
+  // neurons a0 + 8c ..) at + 16 c; the pad chunk fetches the row's last chunk again.
+  // Instructions part, part + nparts, ... of the flat list (64 chunks each).
+  auto dma_rows = [&](int p0, int nr, int part, int nparts) {
+    if (cpr == 0) return;
+    const int total = nr * (cpr + 1);
+    for (int i0 = 64 * part; i0 < total; i0 += 64 * nparts) {
+      const int f = min(i0 + lane, total - 1);
+      const int rho = f / (cpr + 1);
+      const int c = min(f - rho * (cpr + 1), cpr - 1);
+      const int q = a0 + 8 * c;
+      const int e = ul_s[q / G], g = q - (q / G) * G;
+      const bf16_t* src = down_t + ((size_t)e * H + p0 + rho) * G + g;
+      __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(dn_s + 16 * i0), 16, 0,
+                                       DECB_NT);
+    }
+  };
+
+  // ---- C: gate/up of union neurons [q0, q1)
+  int q0, q1;
+  pp_split((uint32_t)T, (uint32_t)W, (uint32_t)b, q0, q1);
+  for (int nb0 = q0; nb0 < q1; nb0 += 32) {
+    const int qn = min(nb0 + jn, q1 - 1);  // this lane's neuron (B column)
+    const int eg = qn / G;
+    const uint32_t grow = (uint32_t)(((ul_s[eg] * G + qn - eg * G) * 3) * H) * 2;  // gate row; up row + 2H
+    uint32_t xrow[TB];
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb) xrow[tb] = (uint32_t)(min(tb * 32 + jn, N - 1) * H) * 2;  // A row (token)
+    f32x16_t ag[TB], au[TB];
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb)
+#pragma unroll
+      for (int q = 0; q < 16; ++q) ag[tb][q] = au[tb][q] = 0.0f;
+    // wave wv: K range [64 CPL wv, 64 CPL (wv + 1)); per macro-step of 64 elements, lane
+    // (., kh) holds elements 32 kh .. 32 kh + 31 of its rows, k-step i taking its 8
+    // elements 8i ..; DP macro-steps in flight (registers: DP (32 + 16 TB) + 32 TB)
+    constexpr int DP = TB == 1 ? 3 : 2;
+    uint4 g4[DP][4], u4[DP][4], x4[DP][TB][4];
+    auto issue = [&](int m) {
+      const int sl = m % DP;
+      const uint32_t ko = (uint32_t)(64 * CPL * wv + 64 * m + 32 * kh) * 2;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        g4[sl][i] = decb_ld16<DECB_NT>(r_gu, grow + ko + 16 * i);
+        u4[sl][i] = decb_ld16<DECB_NT>(r_gu, grow + 2 * H + ko + 16 * i);
+      }
+#pragma unroll
+      for (int tb = 0; tb < TB; ++tb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) x4[sl][tb][i] = decb_ld16<DECB_SC1>(r_xbf, xrow[tb] + ko + 16 * i);
+    };
+#pragma unroll
+    for (int m = 0; m < DP - 1 && m < CPL; ++m) issue(m);
+#pragma unroll
+    for (int m = 0; m < CPL; ++m) {
+      if (m + DP - 1 < CPL) issue(m + DP - 1);
+      asm volatile("" ::: "memory");  // keeps later stages' loads from being hoisted here
+      const int sl = m % DP;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int tb = 0; tb < TB; ++tb) {
+          ag[tb] = mfma32(x4[sl][tb][i], g4[sl][i], ag[tb]);
+          au[tb] = mfma32(x4[sl][tb][i], u4[sl][i], au[tb]);
+        }
+    }
+    if (nb0 == q0 && wv > 0) dma_rows(hr0, min(rows_pp, hr1 - hr0), wv - 1, NW - 1);
+    // the eight K partials, added in a fixed tree: w += w + 4, then w += w + 2, then w += w + 1
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb) {
+      for (int half = 4; half >= 1; half >>= 1) {
+        if (wv >= half && wv < 2 * half) {
+          float* d = red_s + (wv - half) * 2048;
+#pragma unroll
+          for (int q = 0; q < 16; ++q) {
+            d[q * 64 + lane] = ag[tb][q];
+            d[1024 + q * 64 + lane] = au[tb][q];
+          }
+        }
+        wg_lds_barrier();
+        if (wv < half) {
+          const float* d = red_s + wv * 2048;
+#pragma unroll
+          for (int q = 0; q < 16; ++q) {
+            ag[tb][q] += d[q * 64 + lane];
+            au[tb][q] += d[1024 + q * 64 + lane];
+          }
+        }
+        wg_lds_barrier();
+      }
+    }
+    if (wv == 0) {  // act[t][nb0 + jn] of every token
+      const int qq = nb0 + jn;
+      const int e = qq < q1 ? ul_s[qq / G] : 0;
+#pragma unroll
+      for (int tb = 0; tb < TB; ++tb) {
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+          const int t = tb * 32 + mfma32_row(q, lane);
+          if (t < N && qq < q1) {
+            const float gt = sg_s[t * 16 + e];
+            const float a = fail ? __int_as_float(0x7fc00000) : gt != -1.0f ? pp_silu(ag[tb][q]) * au[tb][q] * gt : 0.0f;
+            __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16(a), r_act, (uint32_t)(t * TS + qq) * 2, 0, DECB_SC1);
+          }
+        }
+      }
+    }
+  }
+  if (q0 >= q1 && wv > 0) dma_rows(hr0, min(rows_pp, hr1 - hr0), wv - 1, NW - 1);
+  if (wv == 0) {  // this workgroup's acts are stored (only wave 0 stores them)
+    vm_wait();
+    if (lane == 0) st_rlx(&aflag[b], tag);
+  }
+
+  // ---- D: partial sums of rows [hr0, hr1) over slice s
+  {
+    // the acts of [a0, a0 + nk) come from the workgroups whose [q0, q1) meet it
+    for (int p = tid; p < W; p += NT) {
+      int lo, hi;
+      pp_split((uint32_t)T, (uint32_t)W, (uint32_t)p, lo, hi);
+      if (lo < hi && lo < a0 + nk && hi > a0 && !decb_wait(&aflag[p], tag)) fail = true;
+    }
+    vm_wait();  // the first pass's down rows
+    fail = __syncthreads_or(fail);
+    for (int p0 = hr0; p0 < hr1; p0 += rows_pp) {
+      const int nr = min(rows_pp, hr1 - p0);
+      if (p0 != hr0) {  // later passes (row groups beyond rows_pp rows)
+        wg_lds_barrier();
+        dma_rows(p0, nr, wv, NW);
+        vm_wait();
+        __syncthreads();
+      }
+      const int nrb = (nr + 31) >> 5;
+      for (int tile = wv; tile < nrb * TB; tile += NW) {
+        const int rbk = tile / TB, tb = tile - rbk * TB;
+        const int rho = min(rbk * 32 + jn, nr - 1);  // A row: down row of the pass
+        const int tk = min(tb * 32 + jn, N - 1);     // B column: token
+        const unsigned char* arow = dn_s + rho * RSB + 16 * kh;
+        const uint32_t boff = (uint32_t)(tk * TS + a0 + 8 * kh) * 2;
+        // every act fragment of the tile requested at once (nk <= G <= DEC2_GMAX), then the
+        // MFMAs: one memory round trip per tile
+        const int nks = nk / 16;
+        uint4 bv[DEC2_GMAX / 16];
+#pragma unroll
+        for (int ks = 0; ks < DEC2_GMAX / 16; ++ks)
+          if (ks < nks) bv[ks] = decb_ld16<DECB_SC1>(r_act, boff + 32 * ks);
+        f32x16_t acc;
+#pragma unroll
+        for (int q = 0; q < 16; ++q) acc[q] = 0.0f;
+#pragma unroll
+        for (int ks = 0; ks < DEC2_GMAX / 16; ++ks)
+          if (ks < nks) acc = mfma32(*(const uint4*)(arow + 32 * ks), bv[ks], acc);
+        // D: lane l, element q -> row rbk * 32 + mfma32_row(q, l), token tb * 32 + l % 32
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+          const int rr = rbk * 32 + mfma32_row(q, lane);
+          if (rr < nr)
+            __builtin_amdgcn_raw_buffer_store_b32(fail ? 0x7fc00000u : __float_as_uint(acc[q]), r_part,
+                                                  (uint32_t)(((s * H + p0 + rr) * DECB_MAXN + tb * 32 + jn) * 4), 0,
+                                                  DECB_SC1);
+        }
+      }
+    }
+    vm_wait();
+    __syncthreads();
+    if (tid == 0) st_rlx(&pflag[b], tag);
+  }
+
+  // ---- E: fold of the 8-row blocks u = b, b + W, ... over the 16 slices, in slice order
+  for (int u = b; u < H / 8; u += W) {
+    int rg = 0;  // the row group holding block u
+    for (int i = 0; i < R; ++i) {
+      int lo, hi;
+      pp_split((uint32_t)(H / 8), (uint32_t)R, (uint32_t)i, lo, hi);
+      if (u >= lo && u < hi) rg = i;
+    }
+    if (tid < DECB_S && !decb_wait(&pflag[rg * DECB_S + tid], tag)) fail = true;
+    const bool failed = __syncthreads_or(fail);
+    const int t = tid >> 3, hh = tid & 7;
+    if (t < N) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int sl = 0; sl < DECB_S; ++sl)
+        acc += __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+            r_part, (uint32_t)(((sl * H + 8 * u + hh) * DECB_MAXN + t) * 4), 0, DECB_SC1));
+      out[(size_t)t * H + 8 * u + hh] = failed ? (bf16_t)0x7fc0 : f32_to_bf16(acc);
+    }
+  }
+
+  if (b == 0)  // once every workgroup has set its last flag (so has read the tag), advance
+    for (int p = tid; p < W; p += NT)
+      if (!decb_wait(&pflag[p], tag)) fail = true;
+  const bool failed = __syncthreads_or(fail);
+  if (tid == 0) {
+    if (failed) {
+      __hip_atomic_fetch_or(&st->error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      st_rlx(&st->error_call, tag);
+    }
+    if (b == 0) st_rlx(&st->epochb, tag);
+  }
+}
+
 __global__ void decode_ws_clear_kernel(uint32_t* p, size_t n_words) {
   for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n_words; i += (size_t)gridDim.x * blockDim.x)
     p[i] = 0u;
@@ -1282,7 +1660,7 @@ __global__ void decode_ws_clear_kernel(uint32_t* p, size_t n_words) {
 
 // Workspace: state | decode_kernel: 2 x DEC_NCOPY x hs fixed-point accumulators,
 // DEC_SLOT_REPS x PP_MAX_EXPERTS 64-bit logit slots, completion-ticket counters | the
-// two-phase kernels: two act banks of DEC2_BANK_WORDS words. The two families keep separate
+// two-phase kernels: two act banks of DEC2_BANK_WORDS words | the batch kernel: its flags. The two families keep separate
 // epochs (router_ticket, epoch16), so calls of either kind may follow each other on one
 // workspace.
 static constexpr size_t dec_general_bytes(int hs) {
@@ -1292,9 +1670,12 @@ static constexpr size_t dec_general_bytes(int hs) {
 static constexpr size_t dec_banks_offset(int hs) { return (dec_acc_offset() + dec_general_bytes(hs) + 255) / 256 * 256; }
 static constexpr size_t dec_banks_bytes() { return (size_t)2 * DEC2_BANK_WORDS * sizeof(uint32_t); }
 
+// the batch kernel's flags follow the banks (the allocation-free scratch stops before them)
+static constexpr size_t dec_bflags_offset(int hs) { return dec_banks_offset(hs) + dec_banks_bytes(); }
+
 extern "C" size_t pp_decode_workspace_bytes(int H, int E) {
   (void)E;
-  return dec_banks_offset(H) + dec_banks_bytes();
+  return dec_bflags_offset(H) + (size_t)DECB_FLAG_WORDS * sizeof(uint32_t);
 }
 
 extern "C" int pp_decode_workspace_init(void* workspace, int H, int E, void* stream) {
@@ -1513,6 +1894,74 @@ extern "C" int pp_moe_decode(const void* x, int x_dtype, int H, const float* rou
   uint32_t* banks = (uint32_t*)((char*)workspace + dec_banks_offset(H));
   return decode_dispatch(x, x_dtype, H, router_packed, bias, E, G, tau, packed, out_bf16, st, acc, H, H, banks, grid,
                          (hipStream_t)stream);
+}
+
+// ------------------------------------------------------------------ batch entry
+extern "C" size_t pp_decode_batch_workspace_bytes(int H, int E, int G) {
+  (void)E;
+  return decb_layout(H, G).total;
+}
+
+extern "C" int pp_moe_decode_batch(const void* x, int x_dtype, int64_t n_tokens, int H, const float* router_packed,
+                                   const float* bias, int E, int G, float tau, const void* packed, void* out_bf16,
+                                   float* logits_out, uint8_t* mask_out, void* workspace, void* batch_workspace,
+                                   int grid, void* stream) {
+  int rc = decode_check_args(x, x_dtype, H, router_packed, E, G, packed, out_bf16, grid);
+  if (rc) return rc;
+  PP_REQUIRE(workspace && batch_workspace, PP_ERR_INVALID, "pp_moe_decode_batch: null workspace");
+  PP_REQUIRE(n_tokens >= 1 && n_tokens <= DECB_MAXN, PP_ERR_UNSUPPORTED,
+             "pp_moe_decode_batch: n_tokens %lld unsupported (1..%d)", (long long)n_tokens, DECB_MAXN);
+  PP_REQUIRE(E == 16 && H % 512 == 0 && G <= DEC2_GMAX, PP_ERR_UNSUPPORTED,
+             "pp_moe_decode_batch: H=%d E=%d G=%d unsupported (E = 16, H %% 512 == 0, G <= %d)", H, E, G, DEC2_GMAX);
+  const int N = (int)n_tokens;
+  hipStream_t s = (hipStream_t)stream;
+  pp_decode_state* st = (pp_decode_state*)workspace;
+  uint32_t* flags = (uint32_t*)((char*)workspace + dec_bflags_offset(H));
+  const bf16_t* gu = (const bf16_t*)packed;
+  const bf16_t* down_t = gu + (size_t)16 * G * 3 * H;
+  // W: a multiple of DECB_S, at least N, at most what the device holds at once (every
+  // workgroup waits for others); rows per pass: a row group's rows as far as LDS allows
+  int W = min(grid == 0 ? pp_device_cus() : grid, DEC2_WMAX) / DECB_S * DECB_S;
+  const int R0 = max(W / DECB_S, 1);
+  int rp = 8 * ((H / 8 + R0 - 1) / R0);
+  auto lds_rows = [&](int rows) { return (size_t)((rows * (G / 8 + 1) + 63) / 64 * 64) * 16; };
+  while (rp > 1 && lds_rows(rp) > DECB_DOWN_LDS) --rp;
+  const size_t smem = DECB_RED_BYTES + lds_rows(rp);
+  auto launch = [&](auto kern, auto xp) {
+    const int cap = dec_capacity((const void*)kern, 512, smem);
+    W = min(W, cap) / DECB_S * DECB_S;
+    if (W < max(N, DECB_S)) {
+      pp_set_error("pp_moe_decode_batch: %d workgroups resident at once, the batch kernel needs %d", W,
+                   max(N, DECB_S));
+      rc = PP_ERR_UNSUPPORTED;
+      return;
+    }
+    kern<<<W, 512, smem, s>>>(xp, N, router_packed, bias, G, tau, gu, down_t, (bf16_t*)out_bf16, logits_out, mask_out,
+                              st, flags, (unsigned char*)batch_workspace, rp);
+  };
+#define PP_DECB_CASE(C)                                                                      \
+  case C:                                                                                    \
+    if (x_dtype == PP_DTYPE_F32) {                                                           \
+      if (N <= 32) launch(decodeb_kernel<float, C, 1>, (const float*)x);                     \
+      else launch(decodeb_kernel<float, C, 2>, (const float*)x);                             \
+    } else {                                                                                 \
+      if (N <= 32) launch(decodeb_kernel<bf16_t, C, 1>, (const bf16_t*)x);                   \
+      else launch(decodeb_kernel<bf16_t, C, 2>, (const bf16_t*)x);                           \
+    }                                                                                        \
+    break;
+  switch (H / 512) {
+    PP_DECB_CASE(1)
+    PP_DECB_CASE(2)
+    PP_DECB_CASE(3)
+    PP_DECB_CASE(4)
+    PP_DECB_CASE(5)
+    PP_DECB_CASE(6)
+    PP_DECB_CASE(7)
+    PP_DECB_CASE(8)
+  }
+#undef PP_DECB_CASE
+  if (rc) return rc;
+  return pp_check_launch("pp_moe_decode_batch");
 }
 
 // ------------------------------------------------------------------ allocation-free entry

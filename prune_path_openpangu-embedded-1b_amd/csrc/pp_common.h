@@ -47,6 +47,16 @@ __device__ __forceinline__ float bf16_to_f32(bf16_t v) {
 // size is part of their latency.
 __device__ __forceinline__ bf16_t f32_to_bf16(float f) { return __builtin_bit_cast(bf16_t, (__bf16)f); }
 
+// ---------------------------------------------------------------- MFMA
+__device__ __forceinline__ bf16x8_t as_bf16x8(uint4 u) { return __builtin_bit_cast(bf16x8_t, u); }
+
+// v_mfma_f32_32x32x16_bf16: A lane l holds row l % 32, k = 8 (l / 32) .. + 7; B lane l
+// holds column l % 32, the same k; D lane l, element q is row mfma32_row(q, l), column l % 32.
+__device__ __forceinline__ f32x16_t mfma32(const uint4 a, const uint4 b, f32x16_t c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
+}
+__device__ __forceinline__ int mfma32_row(int q, int lane) { return (q >> 2) * 8 + (lane >> 5) * 4 + (q & 3); }
+
 __host__ __device__ __forceinline__ int pp_ceil_div(int a, int b) { return (a + b - 1) / b; }
 
 // Balanced contiguous split of [0, T) into W parts: part b is [lo, hi). One 32-bit

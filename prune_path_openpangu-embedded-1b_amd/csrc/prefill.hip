@@ -23,15 +23,6 @@
 #define GM_LDK (GM_BK + 8)  // padded LDS row (bf16 elements)
 #define GM_BM 128
 
-__device__ __forceinline__ bf16x8_t as_bf16x8(uint4 u) { return __builtin_bit_cast(bf16x8_t, u); }
-
-__device__ __forceinline__ f32x16_t mfma32(const uint4 a, const uint4 b, f32x16_t c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
-}
-
-// D layout of the 32x32 MFMA: lane l, element q -> row (q/4)*8 + (l/32)*4 + q%4, col l%32.
-__device__ __forceinline__ int mfma32_row(int q, int lane) { return (q >> 2) * 8 + (lane >> 5) * 4 + (q & 3); }
-
 typedef bf16_t lds_row_t[GM_LDK];
 
 // Chunk i of a thread covers tile row (tid >> 3) + 32 * i, columns kcol .. kcol + 7.

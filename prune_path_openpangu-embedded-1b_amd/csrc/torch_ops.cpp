@@ -14,6 +14,8 @@
 //   pack_experts,
 //   pack_router           physical_reorder_for_inference (src/openpangu_moe.py:212-256)
 //   moe_decode(_into)     TauSparseMoE.forward_decode (:494-530)
+//   moe_decode_batch(_into)  TauSparseMoE.forward_prefill (:532-604) for 1 <= N <= 64
+//                         tokens (the reference takes it for every N > 1, :606-615)
 //   moe_prefill(_into)    TauSparseMoE.forward_prefill (:532-604)
 #include <ATen/ATen.h>
 #include <c10/core/DeviceGuard.h>
@@ -286,6 +288,60 @@ Tensor moe_decode_meta(const Tensor& x, const Tensor&, const optional<Tensor>&, 
   return at::empty_symint({c10::SymInt(1), x.sym_numel()}, x.options().dtype(at::kBFloat16));
 }
 
+// ------------------------------------------------------------------ small-batch decode
+void decode_batch_into(const Tensor& x, const Tensor& router_packed, const optional<Tensor>& bias, int64_t E,
+                       int64_t G, double tau, const Tensor& packed, const Tensor& workspace,
+                       const Tensor& batch_workspace, const Tensor& out, const optional<Tensor>& logits_out,
+                       const optional<Tensor>& mask_out, int64_t grid) {
+  TORCH_CHECK(x.dim() == 2, "prunepath.moe_decode_batch: x must be [N, H]");
+  const int64_t N = x.size(0), H = x.size(1);
+  check_bias(bias, E, "moe_decode_batch");
+  TORCH_CHECK(workspace.scalar_type() == at::kByte &&
+                  workspace.numel() >= (int64_t)pp_decode_workspace_bytes((int)H, (int)E),
+              "prunepath.moe_decode_batch: uint8 workspace of pp_decode_workspace_bytes(H, E) required");
+  TORCH_CHECK(batch_workspace.scalar_type() == at::kByte &&
+                  batch_workspace.numel() >= (int64_t)pp_decode_batch_workspace_bytes((int)H, (int)E, (int)G),
+              "prunepath.moe_decode_batch: uint8 batch_workspace of pp_decode_batch_workspace_bytes(H, E, G) required");
+  TORCH_CHECK(out.scalar_type() == at::kBFloat16 && out.numel() == N * H && out.is_contiguous(),
+              "prunepath.moe_decode_batch: out must be contiguous bf16 [N, H]");
+  if (logits_out.has_value())
+    TORCH_CHECK(logits_out->scalar_type() == at::kFloat && logits_out->numel() == N * E && logits_out->is_contiguous(),
+                "prunepath.moe_decode_batch: logits_out must be contiguous fp32 [N, E]");
+  if (mask_out.has_value())
+    TORCH_CHECK(mask_out->scalar_type() == at::kByte && mask_out->numel() == N * E && mask_out->is_contiguous(),
+                "prunepath.moe_decode_batch: mask_out must be contiguous uint8 [N, E]");
+  need_gpu("moe_decode_batch", x,
+           {&x, &router_packed, bias.has_value() ? &*bias : nullptr, &packed, &workspace, &batch_workspace, &out,
+            logits_out.has_value() ? &*logits_out : nullptr, mask_out.has_value() ? &*mask_out : nullptr});
+  const c10::DeviceGuard g(x.device());
+  check_rc(pp_moe_decode_batch(x.data_ptr(), x_code(x, "moe_decode_batch"), N, (int)H,
+                               router_packed.data_ptr<float>(), (const float*)ptr(bias), (int)E, (int)G, (float)tau,
+                               packed.data_ptr(), out.data_ptr(),
+                               logits_out.has_value() ? logits_out->data_ptr<float>() : nullptr,
+                               mask_out.has_value() ? mask_out->data_ptr<uint8_t>() : nullptr, workspace.data_ptr(),
+                               batch_workspace.data_ptr(), (int)grid, stream_of(x)),
+           "moe_decode_batch");
+}
+
+Tensor moe_decode_batch_gpu(const Tensor& x, const Tensor& router_packed, const optional<Tensor>& bias, int64_t E,
+                            int64_t G, double tau, const Tensor& packed, const Tensor& workspace,
+                            const Tensor& batch_workspace, int64_t grid) {
+  TORCH_CHECK(x.dim() == 2, "prunepath.moe_decode_batch: x must be [N, H]");
+  Tensor out = at::empty({x.size(0), x.size(1)}, x.options().dtype(at::kBFloat16));
+  decode_batch_into(x, router_packed, bias, E, G, tau, packed, workspace, batch_workspace, out, c10::nullopt,
+                    c10::nullopt, grid);
+  return out;
+}
+
+Tensor moe_decode_batch_meta(const Tensor& x, const Tensor&, const optional<Tensor>&, int64_t, int64_t, double,
+                             const Tensor&, const Tensor&, const Tensor&, int64_t) {
+  return at::empty_symint(x.sym_sizes(), x.options().dtype(at::kBFloat16));
+}
+
+void moe_decode_batch_into_meta(const Tensor&, const Tensor&, const optional<Tensor>&, int64_t, int64_t, double,
+                                const Tensor&, const Tensor&, const Tensor&, const Tensor&, const optional<Tensor>&,
+                                const optional<Tensor>&, int64_t) {}
+
 // ------------------------------------------------------------------ prefill
 void prefill_into(const Tensor& x, const Tensor& router_packed, const optional<Tensor>& bias, int64_t E, int64_t G,
                   double tau, const Tensor& packed, const Tensor& workspace, const Tensor& out) {
@@ -345,6 +401,11 @@ TORCH_LIBRARY(prunepath, m) {
         "Tensor(a!) workspace, int grid=0) -> Tensor");
   m.def("moe_decode_into(Tensor x, Tensor router_packed, Tensor? bias, int E, int G, float tau, Tensor packed, "
         "Tensor(a!) workspace, Tensor(b!) out, int grid=0) -> ()");
+  m.def("moe_decode_batch(Tensor x, Tensor router_packed, Tensor? bias, int E, int G, float tau, Tensor packed, "
+        "Tensor(a!) workspace, Tensor(b!) batch_workspace, int grid=0) -> Tensor");
+  m.def("moe_decode_batch_into(Tensor x, Tensor router_packed, Tensor? bias, int E, int G, float tau, Tensor packed, "
+        "Tensor(a!) workspace, Tensor(b!) batch_workspace, Tensor(c!) out, Tensor(d!)? logits_out=None, "
+        "Tensor(e!)? mask_out=None, int grid=0) -> ()");
   m.def("moe_prefill(Tensor x, Tensor router_packed, Tensor? bias, int E, int G, float tau, Tensor packed) -> Tensor");
   m.def("moe_prefill_into(Tensor x, Tensor router_packed, Tensor? bias, int E, int G, float tau, Tensor packed, "
         "Tensor(a!) workspace, Tensor(b!) out) -> ()");
@@ -359,6 +420,8 @@ TORCH_LIBRARY_IMPL(prunepath, CUDA, m) {
   m.impl("decode_workspace_init", &decode_workspace_init_gpu);
   m.impl("moe_decode", &moe_decode_gpu);
   m.impl("moe_decode_into", &decode_into);
+  m.impl("moe_decode_batch", &moe_decode_batch_gpu);
+  m.impl("moe_decode_batch_into", &decode_batch_into);
   m.impl("moe_prefill", &moe_prefill_gpu);
   m.impl("moe_prefill_into", &prefill_into);
 }
@@ -372,12 +435,15 @@ TORCH_LIBRARY_IMPL(prunepath, Meta, m) {
   m.impl("decode_workspace_init", &decode_workspace_init_meta);
   m.impl("moe_decode", &moe_decode_meta);
   m.impl("moe_decode_into", &moe_decode_into_meta);
+  m.impl("moe_decode_batch", &moe_decode_batch_meta);
+  m.impl("moe_decode_batch_into", &moe_decode_batch_into_meta);
   m.impl("moe_prefill", &moe_prefill_meta);
   m.impl("moe_prefill_into", &moe_prefill_into_meta);
 }
 
 TORCH_LIBRARY_IMPL(prunepath, CPU, m) {
   for (const char* name : {"route", "route_logits", "bucket", "pack_experts", "pack_router", "decode_workspace_init",
-                           "moe_decode", "moe_decode_into", "moe_prefill", "moe_prefill_into"})
+                           "moe_decode", "moe_decode_into", "moe_decode_batch", "moe_decode_batch_into",
+                           "moe_prefill", "moe_prefill_into"})
     m.impl(name, torch::CppFunction::makeFromBoxedFunction<&refuse_cpu>());
 }

@@ -133,7 +133,7 @@ def decode_state(ws: torch.Tensor, E: int) -> dict:
     ids = body[1024:2048].view(torch.int32)[:k].clone()
     gts = body[2048:3072].view(torch.float32)[:k].clone()
     return {"error": int(u32[3]), "k": k, "logits": logits, "sel_ids": ids, "sel_gates": gts,
-            "router_ticket": int(u32[0]), "epoch16": int(u32[1]), "done": int(u32[2])}
+            "router_ticket": int(u32[0]), "epoch16": int(u32[1]), "epochb": int(u32[2])}
 
 
 def moe_decode(x: torch.Tensor, router_packed: torch.Tensor, bias: Optional[torch.Tensor], E: int, G: int,
@@ -147,6 +147,41 @@ def moe_decode(x: torch.Tensor, router_packed: torch.Tensor, bias: Optional[torc
     if out is None:
         return L.torch_ops().moe_decode(x, router_packed, bias, E, G, float(tau), packed, workspace, int(grid))
     L.torch_ops().moe_decode_into(x, router_packed, bias, E, G, float(tau), packed, workspace, out, int(grid))
+    return out
+
+
+# ----------------------------------------------------------------------------- small-batch decode
+DECODE_BATCH_MAX = 64
+
+
+def decode_batch_workspace_bytes(H: int, E: int, G: int) -> int:
+    return int(L.lib().pp_decode_batch_workspace_bytes(H, E, G))
+
+
+def decode_batch_supported(N: int, H: int, E: int, G: int) -> bool:
+    """Shapes the one-launch small-batch kernel takes (the rest go through prefill)."""
+    return 1 <= N <= DECODE_BATCH_MAX and E == 16 and H % 512 == 0 and 512 <= H <= 4096 and G % 32 == 0 and G <= 512
+
+
+def moe_decode_batch(x: torch.Tensor, router_packed: torch.Tensor, bias: Optional[torch.Tensor], E: int, G: int,
+                     tau: float, packed: torch.Tensor, workspace: torch.Tensor, batch_workspace: torch.Tensor,
+                     grid: int = 0, out: Optional[torch.Tensor] = None, logits_out: Optional[torch.Tensor] = None,
+                     mask_out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Small-batch MoE-MLP layer in one launch (``torch.ops.prunepath.moe_decode_batch``,
+    or ``moe_decode_batch_into`` writing ``out`` and, when given, the routing: logits
+    [N,E] fp32 and mask [N,E] uint8). x [N,H] with N <= 64; ``workspace`` a decode
+    workspace (``decode_workspace``), ``batch_workspace`` of
+    ``decode_batch_workspace_bytes(H, E, G)`` bytes. Returns bf16 [N,H]."""
+    if x.dtype not in (torch.float32, torch.bfloat16):
+        x = x.float()
+    ops = L.torch_ops()
+    if out is None and logits_out is None and mask_out is None:
+        return ops.moe_decode_batch(x, router_packed, bias, E, G, float(tau), packed, workspace, batch_workspace,
+                                    int(grid))
+    if out is None:
+        out = torch.empty(x.shape[0], x.shape[1], dtype=torch.bfloat16, device=x.device)
+    ops.moe_decode_batch_into(x, router_packed, bias, E, G, float(tau), packed, workspace, batch_workspace, out,
+                              logits_out, mask_out, int(grid))
     return out
 
 

@@ -23,6 +23,10 @@ Differences by design (each a documented build choice, not an omission):
   calls ``total_tiles.item()``, :581).
 * Every neuron of every selected expert is computed (the reference decode grid
   covers only 64 neurons per expert, :398-399, 515).
+* Small batches (2 <= N <= ``batch_max`` tokens, 32 by default and at most 64, at E = 16
+  with H % 512 == 0 and G <= 512) run the one-launch batch kernel (``ops.moe_decode_batch``) instead of the prefill pipeline the
+  reference uses for every N > 1: same routing and output within the north-star
+  tolerance, one kernel instead of five. Its batch workspace is allocated on first use.
 * Decode failures are not silent (the reference has no failure reporting): a decode
   call whose selection is inconsistent or whose reduction leaves the fixed-point range
   writes NaN outputs, and one whose cross-workgroup wait times out writes NaN from then
@@ -67,8 +71,11 @@ class TauSparseMoE(nn.Module):
         self.register_buffer("packed_experts", None, persistent=False)
         self.register_buffer("router_packed", None, persistent=False)
         self.register_buffer("decode_workspace", None, persistent=False)
+        self.register_buffer("batch_workspace", None, persistent=False)
         self._packed_key = None
         self.checked = False
+        # token counts up to which forward() takes the one-launch batch kernel
+        self.batch_max = 32
 
     # ------------------------------------------------------------------ packing
     def _weights_key(self):
@@ -162,6 +169,18 @@ class TauSparseMoE(nn.Module):
             self.check_decode()
         return out.view(B, L, H)
 
+    def forward_decode_batch(self, x_flat: torch.Tensor, B: int, L: int, H: int) -> torch.Tensor:
+        E, G = self.num_experts, self.group_size
+        nb = ops.decode_batch_workspace_bytes(H, E, G)
+        if self.batch_workspace is None or self.batch_workspace.device != x_flat.device or \
+                self.batch_workspace.numel() < nb:
+            self.batch_workspace = torch.empty(nb, dtype=torch.uint8, device=x_flat.device)
+        out = ops.moe_decode_batch(x_flat, self.router_packed, self.router_bias, E, G, self.tau,
+                                   self.packed_experts, self.decode_workspace, self.batch_workspace)
+        if self.checked:
+            self.check_decode()
+        return out.view(B, L, H)
+
     def forward_prefill(self, N: int, x_flat: torch.Tensor, B: int, L: int, H: int) -> torch.Tensor:
         out = ops.moe_prefill(x_flat, self.router_packed, self.router_bias, self.num_experts, self.group_size,
                               self.tau, self.packed_experts)
@@ -181,4 +200,6 @@ class TauSparseMoE(nn.Module):
             return torch.empty(B, L, H, dtype=torch.bfloat16, device=x.device)
         if N == 1:
             return self.forward_decode(x_flat, B, L, H)
+        if N <= self.batch_max and ops.decode_batch_supported(N, H, self.num_experts, self.group_size):
+            return self.forward_decode_batch(x_flat, B, L, H)
         return self.forward_prefill(N, x_flat, B, L, H)

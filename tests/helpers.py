@@ -54,16 +54,17 @@ def make_module(pkg, w: dict, tau: float, bias=None):
     return m
 
 
-def sparse_expected(x: np.ndarray, w: dict, gates: np.ndarray) -> np.ndarray:
+def sparse_expected(x: np.ndarray, w: dict, gates: np.ndarray, act_bf16: bool = False) -> np.ndarray:
     """float64 layer output from a given selection, on bf16-rounded x and weights
-    (what the kernels consume)."""
+    (what the kernels consume); act_bf16 rounds the acts to bf16 before the down
+    projection, as the reference's fused expert kernel does."""
     E = w["w_router"].shape[0]
     I = w["w_gate"].shape[0]
     G = I // E
     perm = oracle.pack_permutation(w["expert_ids"])
     return oracle.sparse_moe_from_selection(bf16_round(x), bf16_round(w["w_gate"])[perm],
                                             bf16_round(w["w_up"])[perm], bf16_round(w["w_down"])[:, perm].T,
-                                            gates, G)
+                                            gates, G, act_bf16=act_bf16)
 
 
 def sparse_expected_gpu(x: np.ndarray, w: dict, gates: np.ndarray) -> np.ndarray:

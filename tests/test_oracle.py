@@ -278,6 +278,46 @@ def test_masked_equals_sparse_form(oracle):
         np.testing.assert_allclose(out2, out, rtol=0, atol=0)
 
 
+def test_bf16_rne_matches_torch(oracle):
+    rng = np.random.default_rng(5)
+    a = np.concatenate([rng.standard_normal(20000).astype(np.float32) * 10.0 ** rng.integers(-40, 39, 20000),
+                        np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 3.4e38, -3.4e38, 1e-45, 1.0 + 2.0 ** -8,
+                                  1.0 + 3 * 2.0 ** -8, 1.0 + 2.0 ** -8 + 2.0 ** -20], np.float32)])
+    # exact ties: mantissas ending in 0x8000 with an even and an odd kept bit
+    ties = (np.arange(1, 2001, dtype=np.uint32) << 16 | 0x8000).view(np.float32)
+    a = np.concatenate([a.astype(np.float32), ties, -ties])
+    got = oracle.bf16_rne(a)
+    ref = torch.from_numpy(a).to(torch.bfloat16).float().numpy()
+    np.testing.assert_array_equal(np.isnan(got), np.isnan(ref))
+    ok = ~np.isnan(ref)
+    np.testing.assert_array_equal(got[ok].view(np.uint32), ref[ok].view(np.uint32))
+
+
+def test_sparse_bf16_act_within_half_ulp(oracle):
+    """The bf16-act form differs from the exact one by at most the acts' half-ulp
+    rounding carried through the down projection, and does differ (the rounding is
+    applied)."""
+    z, w, x = _c1("c1_layer")
+    perm = oracle.pack_permutation(w["expert_ids"])
+    sel = oracle.select(z["logits"], 0.7)
+    args = (x, w["w_gate"][perm], w["w_up"][perm], w["w_down"][:, perm].T, sel.gates, gi.G)
+    ex = oracle.sparse_moe_from_selection(*args)
+    rb = oracle.sparse_moe_from_selection(*args, act_bf16=True)
+    # bound: sum over neurons of |act| 2^-8 |down|, per (token, column)
+    Wg, Wu, Wd = (np.asarray(a, np.float64) for a in args[1:4])
+    bound = np.zeros_like(ex)
+    for e in range(sel.gates.shape[1]):
+        t = np.nonzero(sel.gates[:, e] != 0)[0]
+        if t.size == 0:
+            continue
+        sl = slice(e * gi.G, (e + 1) * gi.G)
+        g = x[t].astype(np.float64) @ Wg[sl].T
+        act = g / (1 + np.exp(-g)) * (x[t].astype(np.float64) @ Wu[sl].T) * sel.gates[t, e][:, None]
+        bound[t] += np.abs(act) * 2.0 ** -8 @ np.abs(Wd[sl])
+    assert np.all(np.abs(rb - ex) <= bound * (1 + 1e-9) + 1e-12)
+    assert np.abs(rb - ex).max() > 0
+
+
 def test_pack_permutation_vs_cluster_maps(oracle):
     ids = np.load(os.path.join(GOLDEN, "pangu_clusters_k32.npz"))["expert_ids"]
     assert ids.shape == (26, 6144)

@@ -15,7 +15,7 @@ import torch
 from conftest import import_pkg
 
 OPS = ["route", "route_logits", "bucket", "pack_experts", "pack_router", "decode_workspace_init", "moe_decode",
-       "moe_decode_into", "moe_prefill", "moe_prefill_into"]
+       "moe_decode_into", "moe_decode_batch", "moe_decode_batch_into", "moe_prefill", "moe_prefill_into"]
 
 
 @pytest.fixture(scope="module")
@@ -54,6 +54,9 @@ def test_meta_shapes(P):
     assert P.moe_decode(x[0], rp, None, E, G, 0.7, packed, ws).shape == (1, H)
     y = P.moe_prefill(x, rp, None, E, G, 0.7, packed)
     assert y.shape == (N, H) and y.dtype == torch.bfloat16
+    bws = torch.empty(lib.pp_decode_batch_workspace_bytes(H, E, G), dtype=torch.uint8, device=m)
+    yb = P.moe_decode_batch(x, rp, None, E, G, 0.7, packed, ws, bws)
+    assert yb.shape == (N, H) and yb.dtype == torch.bfloat16
 
 
 def test_meta_symbolic_sizes(P):
@@ -104,6 +107,10 @@ def test_opcheck_all_ops(P):
     out1 = torch.empty(1, H, dtype=torch.bfloat16, device=x.device)
     wsp = torch.empty(pkg.ops.prefill_workspace_bytes(x.shape[0], H, E, G), dtype=torch.uint8, device=x.device)
     outp = torch.empty(x.shape[0], H, dtype=torch.bfloat16, device=x.device)
+    bws = torch.empty(pkg.ops.decode_batch_workspace_bytes(H, E, G), dtype=torch.uint8, device=x.device)
+    outb = torch.empty(x.shape[0], H, dtype=torch.bfloat16, device=x.device)
+    lgb = torch.empty(x.shape[0], E, dtype=torch.float32, device=x.device)
+    mkb = torch.empty(x.shape[0], E, dtype=torch.uint8, device=x.device)
     cases = [
         (P.route, (x, rp, None, E, 0.7)),
         (P.route_logits, (logits, 0.7)),
@@ -113,6 +120,8 @@ def test_opcheck_all_ops(P):
         (P.decode_workspace_init, (ws, H, E)),
         (P.moe_decode, (x[0], rp, None, E, G, 0.7, packed, ws, 0)),
         (P.moe_decode_into, (x[0], rp, None, E, G, 0.7, packed, ws, out1, 0)),
+        (P.moe_decode_batch, (x, rp, None, E, G, 0.7, packed, ws, bws, 0)),
+        (P.moe_decode_batch_into, (x, rp, None, E, G, 0.7, packed, ws, bws, outb, lgb, mkb, 0)),
         (P.moe_prefill, (x, rp, None, E, G, 0.7, packed)),
         (P.moe_prefill_into, (x, rp, None, E, G, 0.7, packed, wsp, outp)),
     ]
