@@ -191,9 +191,10 @@ int pp_moe_decode_noalloc(const void* x, int x_dtype, int H, const float* router
  * gate/up MFMA over the union of the selected experts, the down projection and the fold
  * run in one kernel whose workgroups exchange data through the two workspaces:
  * workspace is a decode workspace (pp_decode_workspace_bytes, zeroed once by
- * pp_decode_workspace_init; it carries the call epoch and the per-workgroup flags and may
- * be the one the layer's pp_moe_decode calls use), batch_workspace
- * pp_decode_batch_workspace_bytes(H, E, G) bytes needing no initialisation. Calls that
+ * pp_decode_workspace_init; it carries the call epoch, the tagged gates and the
+ * per-workgroup flags, and may be the one the layer's pp_moe_decode calls use),
+ * batch_workspace pp_decode_batch_workspace_bytes(H, E, G) bytes needing no initialisation
+ * (untagged data only: one batch workspace may serve several decode workspaces). Calls that
  * share either must be ordered on one stream. logits_out ([N][16] fp32) and mask_out
  * ([N][16] uint8) receive the routing when not null. The output is the same bits on
  * every call (fixed summation orders). Error reporting as pp_moe_decode (error bit 1: a

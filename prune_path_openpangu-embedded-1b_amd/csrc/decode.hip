@@ -1295,56 +1295,74 @@ __global__ __launch_bounds__(512) void decode2p_kernel(
 
 // ------------------------------------------------------------------ batch decode (E = 16)
 // decodeb_kernel: one launch for 1 <= N <= 64 tokens (small-batch decode), every workgroup
-// resident at once, three exchanges through the batch workspace:
-// A. workgroup b < N routes token b (dec16_logits, sel16_wave on wave 0) and publishes its
-//    16 gates (exactly -1: expert not selected; a selected gate is a sigmoid, or NaN) and
-//    x as bf16;
-// B. every workgroup reads the N x 16 gates; the union of the selected experts, ascending,
-//    gives T = nu * G union neurons, union neuron q being neuron q % G of expert
-//    U[q / G];
-// C. gate/up: workgroup b takes union neurons [q0, q1) of an even split of T, all N
-//    tokens, K = H split over the eight waves (32x32x16 MFMA: tokens x neurons, each lane
-//    streaming 64 contiguous bytes of its row per four k-steps); the eight partials are
-//    added in a fixed tree; act[t][q] = silu(g) * u * gate(t, e) (0 where token t did not
-//    select e) goes to the workspace as bf16;
+// resident at once, exchanging data through the batch workspace:
+// A. workgroup b < N routes token b (dec16_logits, sel16_wave on wave 0), writes x as bf16
+//    in MFMA-fragment order and then publishes its 16 gates as tagged words (gate bits,
+//    exactly -1 for an expert not selected; a selected gate is a sigmoid, or NaN);
+// B. every workgroup polls the N x 16 tagged gates; the union of the selected experts,
+//    ascending, gives T = nu * G union neurons, union neuron q being neuron q % G of
+//    expert U[q / G];
+// C. gate/up: workgroup b takes union neurons [q0, q1) of an even split of T in groups of
+//    8, in blocks of at most 24 neurons, all N tokens. K = H is split over the eight
+//    waves (wave w takes the 64-element K-blocks w, w + 8, ...): a wave DMAs the gate and
+//    up rows of each of its K-blocks into its own LDS ring of three stages (whole 128-byte
+//    lines per request, chunks XOR-swizzled by row) and loads the x fragments into
+//    registers (1 KB contiguous per request); 32x32x16 MFMA, tokens x neurons. The eight
+//    partials are added in a fixed tree; act[t][q] = silu(g) * u * gate(t, e) (0 where
+//    token t did not select e) is published as bf16 in MFMA-fragment order;
 // D. down: workgroup b = 16 r + s takes the rows of row group r (8-row blocks of H split
 //    over W / 16 groups) and the union neurons of slice s (16-neuron blocks of T split
 //    over 16 slices; with all 16 experts hit, slice s is expert s): its down rows are
-//    staged in LDS during C, and MFMA (rows x tokens) over the slice writes a partial
-//    [row][token] sum in fp32;
+//    DMA'd to LDS once its gate/up work is done, and MFMA (rows x tokens) over the slice
+//    writes a partial [row][token] sum in fp32;
 // E. fold: the 8-row block u of H is summed over the 16 slices in slice order by
 //    workgroup u % W, so the bf16 output is the same bits on every call.
-// Exchanges: data written with coherent (sc1) stores, then a per-workgroup flag word set
-// to the call's tag (epochb + 1) once those stores completed; readers wait for the
-// flags of the workgroups they read from, then load with sc1 (a workgroup whose wait
-// timed out publishes NaN acts and partial sums, so every output it feeds is NaN). Tags
-// grow by one per call, so flags need no clearing; workgroup 0 advances epochb once every
-// workgroup has set its last flag. Every wait is bounded: a timeout sets error bit 1 and the workgroup writes
+// Exchanges: data written with coherent (sc1) stores, then made visible by a tag (the
+// call's epochb + 1): the gates carry it in their upper word, the acts and partial sums
+// by a per-workgroup flag word set once those stores completed; readers wait for the tags
+// they depend on, then load with sc1 (a workgroup whose wait timed out publishes NaN acts
+// and partial sums, so every output it feeds is NaN). Tags grow by one per call, so
+// nothing needs clearing; workgroup 0 advances epochb once every workgroup has set its
+// last flag. Every wait is bounded: a timeout sets error bit 1 and the workgroup writes
 // NaN. Workspace reads and writes go through buffer descriptors sized to their region.
-#define DECB_MAXN 64               // tokens per call at most
-#define DECB_S 16                  // neuron slices of the down projection
-#define DECB_RED_BYTES (32 * 1024)  // LDS of the gate/up K-split reduction (four waves' partials)
-#define DECB_DOWN_LDS (96 * 1024)   // LDS of the down rows of one pass
-#define DECB_FLAG_WORDS (3 * DEC2_WMAX)  // route, act and partial flags, one word per workgroup
+#define DECB_MAXN 64                   // tokens per call at most
+#define DECB_S 16                      // neuron slices of the down projection
+#define DECB_NB 24                     // neurons per gate/up block
+#define DECB_STAGE (2 * DECB_NB * 128)  // one K-block of a neuron block: gate rows | up rows, 128 B each
+#define DECB_RING_WAVE (3 * DECB_STAGE)  // LDS ring of one wave (three stages)
+#define DECB_RED_BYTES (32 * 1024)      // LDS of the K-split reduction (four waves' partials)
+#define DECB_DOWN_LDS (96 * 1024)       // LDS of the down rows of one pass (after the reduction area)
+#define DECB_SMEM (8 * DECB_RING_WAVE)  // dynamic LDS: the rings; later the reduction area and down rows
+static_assert(DECB_RED_BYTES + DECB_DOWN_LDS <= DECB_SMEM, "batch decode LDS plan");
+// In the decode workspace (zeroed once, private to its epoch): everything that carries a
+// tag -- the tagged gates [64][16] u64, then the act and partial flags (a word per
+// workgroup). A tag is only meaningful against the epoch of its own workspace, so tagged
+// words never live in the batch workspace, which needs no initialisation and may be
+// shared by several decode workspaces (layers) or recycled by an allocator.
+#define DECB_SELG_BYTES (DECB_MAXN * 16 * 8)
+#define DECB_STATE_BYTES (DECB_SELG_BYTES + 2 * DEC2_WMAX * 4)
 
 struct DecbLayout {
-  size_t selg, xbf, act, part, total;
+  size_t xf, af, part, total;
 };
-// batch workspace: gates [64][16] fp32 | x [64][H] bf16 | act [64][16 G] bf16 |
-// partial sums [16][H][64] fp32
+// batch workspace: x fragments (H / 64 K-blocks x 4 k-steps x 2 token blocks x 64 lanes x
+// 16 B) | act fragments (16 G / 16 k-steps x 2 x 64 x 16 B) | partial sums [16][H][64] fp32
 __host__ __device__ __forceinline__ DecbLayout decb_layout(int H, int G) {
   DecbLayout L;
   size_t o = 0;
-  L.selg = o;
-  o += (size_t)DECB_MAXN * 16 * 4;
-  L.xbf = o;
+  L.xf = o;
   o += (size_t)DECB_MAXN * H * 2;
-  L.act = o;
+  L.af = o;
   o += (size_t)DECB_MAXN * 16 * G * 2;
   L.part = o;
   o += (size_t)DECB_S * H * DECB_MAXN * 4;
   L.total = o;
   return L;
+}
+// byte offset of the 16-byte MFMA fragment (k-step ks, token block tb, lane L) in the x and
+// act fragment arrays: lane L holds row tb * 32 + L % 32, elements 16 ks + 8 (L / 32) ..
+__device__ __forceinline__ uint32_t decb_frag(int ks, int tb, int L) {
+  return (uint32_t)(((ks * 2 + tb) * 64 + L) * 16);
 }
 
 typedef __amdgpu_buffer_rsrc_t decb_rsrc_t;
@@ -1373,15 +1391,27 @@ __device__ __forceinline__ bool decb_wait(const uint32_t* f, uint32_t tag) {
   return true;
 }
 
+// the loads feeding `v` have completed (the compiler waits for them here), and no memory
+// access below moves above this point
+__device__ __forceinline__ void decb_ready(dec_u32x4& v) { asm volatile("" : "+v"(v) : : "memory"); }
+__device__ __forceinline__ dec_u32x4 decb_ld16v(decb_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, DECB_SC1);
+}
+__device__ __forceinline__ f32x16_t mfma32x(dec_u32x4 a, uint4 b, f32x16_t c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a), as_bf16x8(b), c, 0, 0, 0);
+}
+
 template <typename XT, int CPL, int TB>
 __global__ __launch_bounds__(512) void decodeb_kernel(
     const XT* __restrict__ x, int N, const float* __restrict__ router, const float* __restrict__ bias, int G,
     float tau, const bf16_t* __restrict__ gu, const bf16_t* __restrict__ down_t, bf16_t* __restrict__ out,
     float* __restrict__ logits_out, uint8_t* __restrict__ mask_out, pp_decode_state* __restrict__ st,
-    uint32_t* __restrict__ flags, unsigned char* __restrict__ bw, int rows_pp) {
+    unsigned char* __restrict__ bstate, unsigned char* __restrict__ bw, int rows_pp) {
   constexpr int NW = 8, NT = 512, H = 512 * CPL, HC = H / 8;
-  extern __shared__ __align__(16) unsigned char smem[];  // [reduction | down rows of a pass]
+  constexpr int DP = CPL < 3 ? CPL : 3;  // gate/up stages in flight per wave (CPL K-blocks per wave)
+  extern __shared__ __align__(16) unsigned char smem[];  // rings | later: reduction area, down rows
   float* red_s = (float*)smem;
+  bf16_t* act_s = (bf16_t*)smem;  // [64][32] acts of a neuron block, after the reduction
   unsigned char* dn_s = smem + DECB_RED_BYTES;
   __shared__ __align__(16) float part_s[16 * NW];
   __shared__ __align__(16) float pg_s[32];
@@ -1394,43 +1424,63 @@ __global__ __launch_bounds__(512) void decodeb_kernel(
   const uint32_t tag = ld_rlx(&st->epochb) + 1u;
   bool fail = (ld_rlx(&st->error) & 1u) != 0u;  // an earlier wait timed out: NaN until re-initialised
   const DecbLayout Lb = decb_layout(H, G);
-  const int TS = 16 * G;  // act row stride (elements)
-  const decb_rsrc_t r_selg = decb_rsrc(bw + Lb.selg, Lb.xbf - Lb.selg);
-  const decb_rsrc_t r_xbf = decb_rsrc(bw + Lb.xbf, Lb.act - Lb.xbf);
-  const decb_rsrc_t r_act = decb_rsrc(bw + Lb.act, Lb.part - Lb.act);
+  unsigned long long* selg = (unsigned long long*)bstate;
+  const decb_rsrc_t r_xf = decb_rsrc(bw + Lb.xf, Lb.af - Lb.xf);
+  const decb_rsrc_t r_af = decb_rsrc(bw + Lb.af, Lb.part - Lb.af);
   const decb_rsrc_t r_part = decb_rsrc(bw + Lb.part, Lb.total - Lb.part);
-  const decb_rsrc_t r_gu = decb_rsrc(gu, (size_t)16 * G * 3 * H * 2);
-  uint32_t* rflag = flags;
-  uint32_t* aflag = flags + DEC2_WMAX;
-  uint32_t* pflag = flags + 2 * DEC2_WMAX;
+  uint32_t* aflag = (uint32_t*)(bstate + DECB_SELG_BYTES);
+  uint32_t* pflag = aflag + DEC2_WMAX;
 
   // ---- A: routing of token b
   if (b < N) {
     const XT* xt = x + (size_t)b * H;
     const float xl = dec16_logits<XT, CPL, NW>(xt, router, bias, part_s, lane, wv);
-    for (int c = tid; c < HC; c += NT) decb_st16(r_xbf, (uint32_t)(b * H + 8 * c) * 2, load_x8_bf16<XT>(xt, c));
+    for (int c = tid; c < HC; c += NT) {  // chunk c: K-block c / 8, k-step c % 4, half (c / 4) % 2
+      const int q = c & 7;
+      decb_st16(r_xf, decb_frag((c >> 3) * 4 + (q & 3), b >> 5, (b & 31) + 32 * (q >> 2)), load_x8_bf16<XT>(xt, c));
+    }
+    bool sel = false;
     if (wv == 0) {
-      const float m = row16_max(xl);
       int rank, k;
-      const bool sel = sel16_wave(xl, m, tau, pg_s, srt_s, lane, rank, k);
-      if (lane < 16) {
-        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(sel ? pg_s[16 + lane] : -1.0f), r_selg,
-                                              (b * 16 + lane) * 4, 0, DECB_SC1);
-        if (logits_out != nullptr) logits_out[b * 16 + lane] = xl;
-        if (mask_out != nullptr) mask_out[b * 16 + lane] = sel ? 1 : 0;
-      }
+      sel = sel16_wave(xl, row16_max(xl), tau, pg_s, srt_s, lane, rank, k);
     }
     vm_wait();
-    __syncthreads();
-    if (tid == 0) st_rlx(&rflag[b], tag);
+    __syncthreads();  // x is stored: the gates may go out
+    if (wv == 0 && lane < 16) {
+      const uint32_t gb = __float_as_uint(sel ? pg_s[16 + lane] : -1.0f);
+      __hip_atomic_store(&selg[b * 16 + lane], ((unsigned long long)tag << 32) | gb, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+      if (logits_out != nullptr) logits_out[b * 16 + lane] = xl;
+      if (mask_out != nullptr) mask_out[b * 16 + lane] = sel ? 1 : 0;
+    }
   }
 
-  // ---- B: every token's gates; the union of the selected experts
-  if (tid < N && !decb_wait(&rflag[tid], tag)) fail = true;
+  // ---- B: every token's gates (tagged words, at most two per thread); the union
+  {
+    unsigned long long v[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int i = tid + NT * u;
+      v[u] = i < N * 16 ? __hip_atomic_load(&selg[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                        : ((unsigned long long)tag << 32);
+    }
+    uint32_t n = 0;
+    while (!fail && ((uint32_t)(v[0] >> 32) != tag || (uint32_t)(v[1] >> 32) != tag)) {
+      __builtin_amdgcn_s_sleep(2);
+      if (++n > DEC_SPIN_LIMIT) {
+        fail = true;
+        break;
+      }
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+        if ((uint32_t)(v[u] >> 32) != tag)
+          v[u] = __hip_atomic_load(&selg[tid + NT * u], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+      if (tid + NT * u < N * 16) sg_s[tid + NT * u] = __uint_as_float((uint32_t)v[u]);
+  }
   fail = __syncthreads_or(fail);  // from here on a failed workgroup publishes NaN
-  for (int i = tid; i < N * 16; i += NT)
-    sg_s[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r_selg, i * 4, 0, DECB_SC1));
-  __syncthreads();
   if (wv == 0) {
     bool hit = false;
     if (lane < 16)
@@ -1441,9 +1491,9 @@ __global__ __launch_bounds__(512) void decodeb_kernel(
   }
   __syncthreads();
   const int T = nu_s * G;
-  const int jn = lane & 31, kh = lane >> 5;  // TB: token blocks of 32 (N <= 32 TB)
+  const int jn = lane & 31, kh = lane >> 5;
 
-  // rows and slice of phase D (known now: its down rows are fetched during C)
+  // rows and slice of phase D
   const int R = W / DECB_S, s = b % DECB_S, r = b / DECB_S;
   int rb0, rb1, sb0, sb1;
   pp_split((uint32_t)(H / 8), (uint32_t)R, (uint32_t)r, rb0, rb1);
@@ -1469,55 +1519,68 @@ __global__ __launch_bounds__(512) void decodeb_kernel(
     }
   };
 
-  // ---- C: gate/up of union neurons [q0, q1)
-  int q0, q1;
-  pp_split((uint32_t)T, (uint32_t)W, (uint32_t)b, q0, q1);
-  for (int nb0 = q0; nb0 < q1; nb0 += 32) {
-    const int qn = min(nb0 + jn, q1 - 1);  // this lane's neuron (B column)
-    const int eg = qn / G;
-    const uint32_t grow = (uint32_t)(((ul_s[eg] * G + qn - eg * G) * 3) * H) * 2;  // gate row; up row + 2H
-    uint32_t xrow[TB];
+  // ---- C: gate/up of union neurons [q0, q1), blocks of at most DECB_NB
+  int g0, g1;
+  pp_split((uint32_t)(T / 8), (uint32_t)W, (uint32_t)b, g0, g1);
+  const int q0 = 8 * g0, q1 = 8 * g1;
+  unsigned char* ring = smem + wv * DECB_RING_WAVE;
+  for (int nb0 = q0; nb0 < q1; nb0 += DECB_NB) {
+    const int nq = min(DECB_NB, q1 - nb0);  // a multiple of 8
+    const int nn = min(jn, nq - 1);         // this lane's neuron (B column; lanes beyond nq repeat the last)
+    // K-block kb of the wave -> stage: gate rows 0 .. nq-1, up rows nq .. 2nq-1, chunk c of
+    // row r at position c ^ (r & 7) (nq is a multiple of 8: a neuron's gate and up rows
+    // share the swizzle)
+    auto issue = [&](int j, dec_u32x4 (&xa)[TB][4]) {
+      const int kb = wv + NW * j;
+      unsigned char* slot = ring + (j % DP) * DECB_STAGE;
+      for (int ii = 0; ii < nq / 4; ++ii) {  // 1 KB (8 rows x 128 B) per instruction
+        const int f = 64 * ii + lane, rr = f >> 3;
+        const int which = rr >= nq ? 1 : 0, q = nb0 + rr - which * nq;
+        const int eg = q / G;
+        const bf16_t* src = gu + (size_t)((ul_s[eg] * G + q - eg * G) * 3 + which) * H + kb * 64 +
+                            8 * ((f & 7) ^ (rr & 7));
+        __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(slot + 1024 * ii), 16, 0,
+                                         DECB_NT);
+      }
 #pragma unroll
-    for (int tb = 0; tb < TB; ++tb) xrow[tb] = (uint32_t)(min(tb * 32 + jn, N - 1) * H) * 2;  // A row (token)
+      for (int tb = 0; tb < TB; ++tb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) xa[tb][i] = decb_ld16v(r_xf, decb_frag(kb * 4 + i, tb, lane));
+    };
     f32x16_t ag[TB], au[TB];
 #pragma unroll
     for (int tb = 0; tb < TB; ++tb)
 #pragma unroll
       for (int q = 0; q < 16; ++q) ag[tb][q] = au[tb][q] = 0.0f;
-    // wave wv: K range [64 CPL wv, 64 CPL (wv + 1)); per macro-step of 64 elements, lane
-    // (., kh) holds elements 32 kh .. 32 kh + 31 of its rows, k-step i taking its 8
-    // elements 8i ..; DP macro-steps in flight (registers: DP (32 + 16 TB) + 32 TB)
-    constexpr int DP = TB == 1 ? 3 : 2;
-    uint4 g4[DP][4], u4[DP][4], x4[DP][TB][4];
-    auto issue = [&](int m) {
-      const int sl = m % DP;
-      const uint32_t ko = (uint32_t)(64 * CPL * wv + 64 * m + 32 * kh) * 2;
+    dec_u32x4 xa[DP][TB][4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        g4[sl][i] = decb_ld16<DECB_NT>(r_gu, grow + ko + 16 * i);
-        u4[sl][i] = decb_ld16<DECB_NT>(r_gu, grow + 2 * H + ko + 16 * i);
-      }
+    for (int j = 0; j < DP; ++j) issue(j, xa[j]);
+    const uint32_t rg = (uint32_t)nn * 128, ru = (uint32_t)(nq + nn) * 128;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      dec_u32x4(&xj)[TB][4] = xa[j % DP];
 #pragma unroll
       for (int tb = 0; tb < TB; ++tb)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) x4[sl][tb][i] = decb_ld16<DECB_SC1>(r_xbf, xrow[tb] + ko + 16 * i);
-    };
+        for (int i = 0; i < 4; ++i) decb_ready(xj[tb][i]);  // block j's x and (issued before) its rows
+      const unsigned char* slot = ring + (j % DP) * DECB_STAGE;
 #pragma unroll
-    for (int m = 0; m < DP - 1 && m < CPL; ++m) issue(m);
-#pragma unroll
-    for (int m = 0; m < CPL; ++m) {
-      if (m + DP - 1 < CPL) issue(m + DP - 1);
-      asm volatile("" ::: "memory");  // keeps later stages' loads from being hoisted here
-      const int sl = m % DP;
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t pos = 16u * (uint32_t)((i + 4 * kh) ^ (nn & 7));
+        const uint4 bg = *(const uint4*)(slot + rg + pos);
+        const uint4 bu = *(const uint4*)(slot + ru + pos);
 #pragma unroll
         for (int tb = 0; tb < TB; ++tb) {
-          ag[tb] = mfma32(x4[sl][tb][i], g4[sl][i], ag[tb]);
-          au[tb] = mfma32(x4[sl][tb][i], u4[sl][i], au[tb]);
+          ag[tb] = mfma32x(xj[tb][i], bg, ag[tb]);
+          au[tb] = mfma32x(xj[tb][i], bu, au[tb]);
         }
+      }
+      if (j + DP < CPL) {
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this stage's LDS reads are done
+        issue(j + DP, xa[j % DP]);
+      }
     }
-    if (nb0 == q0 && wv > 0) dma_rows(hr0, min(rows_pp, hr1 - hr0), wv - 1, NW - 1);
+    wg_lds_barrier();  // every wave is done with its ring: the reduction area may be written
     // the eight K partials, added in a fixed tree: w += w + 4, then w += w + 2, then w += w + 1
 #pragma unroll
     for (int tb = 0; tb < TB; ++tb) {
@@ -1542,21 +1605,34 @@ __global__ __launch_bounds__(512) void decodeb_kernel(
         wg_lds_barrier();
       }
     }
-    if (wv == 0) {  // act[t][nb0 + jn] of every token
+    if (nb0 + DECB_NB >= q1 && wv > 0)  // the last block: the rings are free for the down rows
+      dma_rows(hr0, min(rows_pp, hr1 - hr0), wv - 1, NW - 1);
+    if (wv == 0) {
+      // acts of the block as bf16 [t][32] in LDS, then published in fragment order (16 B =
+      // 8 neurons of one token)
       const int qq = nb0 + jn;
-      const int e = qq < q1 ? ul_s[qq / G] : 0;
+      const int e = jn < nq ? ul_s[qq / G] : 0;
 #pragma unroll
-      for (int tb = 0; tb < TB; ++tb) {
+      for (int tb = 0; tb < TB; ++tb)
 #pragma unroll
         for (int q = 0; q < 16; ++q) {
           const int t = tb * 32 + mfma32_row(q, lane);
-          if (t < N && qq < q1) {
+          if (t < N && jn < nq) {
             const float gt = sg_s[t * 16 + e];
-            const float a = fail ? __int_as_float(0x7fc00000) : gt != -1.0f ? pp_silu(ag[tb][q]) * au[tb][q] * gt : 0.0f;
-            __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16(a), r_act, (uint32_t)(t * TS + qq) * 2, 0, DECB_SC1);
+            const float a = fail ? __int_as_float(0x7fc00000)
+                                 : gt != -1.0f ? pp_silu(ag[tb][q]) * au[tb][q] * gt : 0.0f;
+            act_s[t * 32 + jn] = f32_to_bf16(a);
           }
         }
+      wave_lds_sync();
+      const int ng = nq / 8;
+      for (int it = lane; it < N * ng; it += 64) {
+        const int t = it / ng, gi = it - t * ng;
+        const int k = nb0 + 8 * gi;  // union neuron of the group (a multiple of 8)
+        decb_st16(r_af, decb_frag(k >> 4, t >> 5, (t & 31) + 32 * ((k >> 3) & 1)),
+                  *(const uint4*)(act_s + t * 32 + 8 * gi));
       }
+      wave_lds_sync();
     }
   }
   if (q0 >= q1 && wv > 0) dma_rows(hr0, min(rows_pp, hr1 - hr0), wv - 1, NW - 1);
@@ -1570,11 +1646,12 @@ __global__ __launch_bounds__(512) void decodeb_kernel(
     // the acts of [a0, a0 + nk) come from the workgroups whose [q0, q1) meet it
     for (int p = tid; p < W; p += NT) {
       int lo, hi;
-      pp_split((uint32_t)T, (uint32_t)W, (uint32_t)p, lo, hi);
-      if (lo < hi && lo < a0 + nk && hi > a0 && !decb_wait(&aflag[p], tag)) fail = true;
+      pp_split((uint32_t)(T / 8), (uint32_t)W, (uint32_t)p, lo, hi);
+      if (lo < hi && 8 * lo < a0 + nk && 8 * hi > a0 && !decb_wait(&aflag[p], tag)) fail = true;
     }
     vm_wait();  // the first pass's down rows
     fail = __syncthreads_or(fail);
+    const int nks = nk / 16;
     for (int p0 = hr0; p0 < hr1; p0 += rows_pp) {
       const int nr = min(rows_pp, hr1 - p0);
       if (p0 != hr0) {  // later passes (row groups beyond rows_pp rows)
@@ -1587,16 +1664,12 @@ __global__ __launch_bounds__(512) void decodeb_kernel(
       for (int tile = wv; tile < nrb * TB; tile += NW) {
         const int rbk = tile / TB, tb = tile - rbk * TB;
         const int rho = min(rbk * 32 + jn, nr - 1);  // A row: down row of the pass
-        const int tk = min(tb * 32 + jn, N - 1);     // B column: token
         const unsigned char* arow = dn_s + rho * RSB + 16 * kh;
-        const uint32_t boff = (uint32_t)(tk * TS + a0 + 8 * kh) * 2;
-        // every act fragment of the tile requested at once (nk <= G <= DEC2_GMAX), then the
-        // MFMAs: one memory round trip per tile
-        const int nks = nk / 16;
+        // every act fragment of the tile requested at once (nk <= G <= DEC2_GMAX)
         uint4 bv[DEC2_GMAX / 16];
 #pragma unroll
         for (int ks = 0; ks < DEC2_GMAX / 16; ++ks)
-          if (ks < nks) bv[ks] = decb_ld16<DECB_SC1>(r_act, boff + 32 * ks);
+          if (ks < nks) bv[ks] = decb_ld16<DECB_SC1>(r_af, decb_frag(a0 / 16 + ks, tb, lane));
         f32x16_t acc;
 #pragma unroll
         for (int q = 0; q < 16; ++q) acc[q] = 0.0f;
@@ -1660,9 +1733,9 @@ __global__ void decode_ws_clear_kernel(uint32_t* p, size_t n_words) {
 
 // Workspace: state | decode_kernel: 2 x DEC_NCOPY x hs fixed-point accumulators,
 // DEC_SLOT_REPS x PP_MAX_EXPERTS 64-bit logit slots, completion-ticket counters | the
-// two-phase kernels: two act banks of DEC2_BANK_WORDS words | the batch kernel: its flags. The two families keep separate
-// epochs (router_ticket, epoch16), so calls of either kind may follow each other on one
-// workspace.
+// two-phase kernels: two act banks of DEC2_BANK_WORDS words | the batch kernel: its tagged
+// gates and flags. The kernel families keep separate epochs (router_ticket, epoch16,
+// epochb), so calls of any kind may follow each other on one workspace.
 static constexpr size_t dec_general_bytes(int hs) {
   return (size_t)2 * DEC_NCOPY * hs * sizeof(dec_acc_t) + (size_t)DEC_SLOT_REPS * PP_MAX_EXPERTS * sizeof(unsigned long long) +
          (size_t)DEC_TICKET_WORDS * sizeof(uint32_t);
@@ -1670,12 +1743,12 @@ static constexpr size_t dec_general_bytes(int hs) {
 static constexpr size_t dec_banks_offset(int hs) { return (dec_acc_offset() + dec_general_bytes(hs) + 255) / 256 * 256; }
 static constexpr size_t dec_banks_bytes() { return (size_t)2 * DEC2_BANK_WORDS * sizeof(uint32_t); }
 
-// the batch kernel's flags follow the banks (the allocation-free scratch stops before them)
+// the batch kernel's tagged state follows the banks (the allocation-free scratch stops before it)
 static constexpr size_t dec_bflags_offset(int hs) { return dec_banks_offset(hs) + dec_banks_bytes(); }
 
 extern "C" size_t pp_decode_workspace_bytes(int H, int E) {
   (void)E;
-  return dec_bflags_offset(H) + (size_t)DECB_FLAG_WORDS * sizeof(uint32_t);
+  return dec_bflags_offset(H) + (size_t)DECB_STATE_BYTES;
 }
 
 extern "C" int pp_decode_workspace_init(void* workspace, int H, int E, void* stream) {
@@ -1916,7 +1989,7 @@ extern "C" int pp_moe_decode_batch(const void* x, int x_dtype, int64_t n_tokens,
   const int N = (int)n_tokens;
   hipStream_t s = (hipStream_t)stream;
   pp_decode_state* st = (pp_decode_state*)workspace;
-  uint32_t* flags = (uint32_t*)((char*)workspace + dec_bflags_offset(H));
+  unsigned char* bstate = (unsigned char*)workspace + dec_bflags_offset(H);
   const bf16_t* gu = (const bf16_t*)packed;
   const bf16_t* down_t = gu + (size_t)16 * G * 3 * H;
   // W: a multiple of DECB_S, at least N, at most what the device holds at once (every
@@ -1926,7 +1999,7 @@ extern "C" int pp_moe_decode_batch(const void* x, int x_dtype, int64_t n_tokens,
   int rp = 8 * ((H / 8 + R0 - 1) / R0);
   auto lds_rows = [&](int rows) { return (size_t)((rows * (G / 8 + 1) + 63) / 64 * 64) * 16; };
   while (rp > 1 && lds_rows(rp) > DECB_DOWN_LDS) --rp;
-  const size_t smem = DECB_RED_BYTES + lds_rows(rp);
+  const size_t smem = DECB_SMEM;
   auto launch = [&](auto kern, auto xp) {
     const int cap = dec_capacity((const void*)kern, 512, smem);
     W = min(W, cap) / DECB_S * DECB_S;
@@ -1937,7 +2010,7 @@ extern "C" int pp_moe_decode_batch(const void* x, int x_dtype, int64_t n_tokens,
       return;
     }
     kern<<<W, 512, smem, s>>>(xp, N, router_packed, bias, G, tau, gu, down_t, (bf16_t*)out_bf16, logits_out, mask_out,
-                              st, flags, (unsigned char*)batch_workspace, rp);
+                              st, bstate, (unsigned char*)batch_workspace, rp);
   };
 #define PP_DECB_CASE(C)                                                                      \
   case C:                                                                                    \

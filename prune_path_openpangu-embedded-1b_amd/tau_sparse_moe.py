@@ -23,7 +23,7 @@ Differences by design (each a documented build choice, not an omission):
   calls ``total_tiles.item()``, :581).
 * Every neuron of every selected expert is computed (the reference decode grid
   covers only 64 neurons per expert, :398-399, 515).
-* Small batches (2 <= N <= ``batch_max`` tokens, 32 by default and at most 64, at E = 16
+* Small batches (2 <= N <= ``batch_max`` tokens, 64 by default and at most 64, at E = 16
   with H % 512 == 0 and G <= 512) run the one-launch batch kernel (``ops.moe_decode_batch``) instead of the prefill pipeline the
   reference uses for every N > 1: same routing and output within the north-star
   tolerance, one kernel instead of five. Its batch workspace is allocated on first use.
@@ -75,7 +75,7 @@ class TauSparseMoE(nn.Module):
         self._packed_key = None
         self.checked = False
         # token counts up to which forward() takes the one-launch batch kernel
-        self.batch_max = 32
+        self.batch_max = 64
 
     # ------------------------------------------------------------------ packing
     def _weights_key(self):
