@@ -1330,10 +1330,10 @@ __global__ __launch_bounds__(512) void decode2p_kernel(
 #define DECB_NB 24                     // neurons per gate/up block
 #define DECB_STAGE (2 * DECB_NB * 128)  // one K-block of a neuron block: gate rows | up rows, 128 B each
 #define DECB_RING_WAVE (3 * DECB_STAGE)  // LDS ring of one wave (three stages)
-#define DECB_RED_BYTES (32 * 1024)      // LDS of the K-split reduction (four waves' partials)
-#define DECB_DOWN_LDS (96 * 1024)       // LDS of the down rows of one pass (after the reduction area)
-#define DECB_SMEM (8 * DECB_RING_WAVE)  // dynamic LDS: the rings; later the reduction area and down rows
-static_assert(DECB_RED_BYTES + DECB_DOWN_LDS <= DECB_SMEM, "batch decode LDS plan");
+#define DECB_RED_BYTES (2 * 8 * 2048 * 4)  // LDS of the K partials: two token blocks x eight waves x g|u x 16 x 64
+#define DECB_SMEM (8 * DECB_RING_WAVE)  // dynamic LDS: the rings; then the partials and acts; then down rows
+#define DECB_DOWN_LDS DECB_SMEM         // LDS of the down rows of one pass
+static_assert(DECB_RED_BYTES + 64 * 32 * 2 <= DECB_SMEM, "batch decode LDS plan");
 // In the decode workspace (zeroed once, private to its epoch): everything that carries a
 // tag -- the tagged gates [64][16] u64, then the act and partial flags (a word per
 // workgroup). A tag is only meaningful against the epoch of its own workspace, so tagged
@@ -1410,9 +1410,9 @@ __global__ __launch_bounds__(512) void decodeb_kernel(
   constexpr int NW = 8, NT = 512, H = 512 * CPL, HC = H / 8;
   constexpr int DP = CPL < 3 ? CPL : 3;  // gate/up stages in flight per wave (CPL K-blocks per wave)
   extern __shared__ __align__(16) unsigned char smem[];  // rings | later: reduction area, down rows
-  float* red_s = (float*)smem;
-  bf16_t* act_s = (bf16_t*)smem;  // [64][32] acts of a neuron block, after the reduction
-  unsigned char* dn_s = smem + DECB_RED_BYTES;
+  float* red_s = (float*)smem;                         // [TB][8 waves][g|u][16][64] K partials
+  bf16_t* act_s = (bf16_t*)(smem + DECB_RED_BYTES);    // [64][32] acts of a neuron block
+  unsigned char* dn_s = smem;                          // down rows (once the acts are published)
   __shared__ __align__(16) float part_s[16 * NW];
   __shared__ __align__(16) float pg_s[32];
   __shared__ __align__(16) float srt_s[16];
@@ -1430,6 +1430,48 @@ __global__ __launch_bounds__(512) void decodeb_kernel(
   const decb_rsrc_t r_part = decb_rsrc(bw + Lb.part, Lb.total - Lb.part);
   uint32_t* aflag = (uint32_t*)(bstate + DECB_SELG_BYTES);
   uint32_t* pflag = aflag + DEC2_WMAX;
+
+  const int jn = lane & 31, kh = lane >> 5;
+  // gate/up rows of K-block wv + 8 j of the neuron block [nb0, nb0 + nq) -> ring stage j % DP:
+  // gate rows 0 .. nq-1, up rows nq .. 2nq-1, chunk c of row r at position c ^ (r & 7) (nq is a
+  // multiple of 8: a neuron's gate and up rows share the swizzle); whole 128-byte lines, 1 KB
+  // per instruction. expert(u): expert of union position u.
+  unsigned char* ring = smem + wv * DECB_RING_WAVE;
+  auto issue_w = [&](int nb0, int nq, int j, auto expert) {
+    const int kb = wv + NW * j;
+    unsigned char* slot = ring + (j % DP) * DECB_STAGE;
+    for (int ii = 0; ii < nq / 4; ++ii) {
+      const int f = 64 * ii + lane, rr = f >> 3;
+      const int which = rr >= nq ? 1 : 0, q = nb0 + rr - which * nq;
+      const int eg = q / G;
+      const bf16_t* src = gu + (size_t)((expert(eg) * G + q - eg * G) * 3 + which) * H + kb * 64 +
+                          8 * ((f & 7) ^ (rr & 7));
+      __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(slot + 1024 * ii), 16, 0,
+                                       DECB_NT);
+    }
+  };
+  // x fragments of K-block wv + 8 j (1 KB contiguous per instruction)
+  auto issue_x = [&](int j, dec_u32x4 (&xa)[TB][4]) {
+    const int kb = wv + NW * j;
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) xa[tb][i] = decb_ld16v(r_xf, decb_frag(kb * 4 + i, tb, lane));
+  };
+  // Speculation: with every expert selected by some token (the usual case for batches of 16
+  // and more) the union is 0 .. 15 and this workgroup's first neuron block is known before
+  // the routing, so its first DP stages are requested early -- at the start, or, in a
+  // routing workgroup, once its gates are out (its x stores must complete first, and loads
+  // in flight would hold that wait); a wrong guess only costs the bytes.
+  int sp0, sp1;
+  pp_split((uint32_t)(16 * G / 8), (uint32_t)W, (uint32_t)b, sp0, sp1);
+  const bool spec = sp1 > sp0;
+  auto issue_spec = [&]() {
+    if (spec)
+#pragma unroll
+      for (int j = 0; j < DP; ++j) issue_w(8 * sp0, min(DECB_NB, 8 * (sp1 - sp0)), j, [](int e) { return e; });
+  };
+  if (b >= N) issue_spec();
 
   // ---- A: routing of token b
   if (b < N) {
@@ -1453,6 +1495,7 @@ __global__ __launch_bounds__(512) void decodeb_kernel(
       if (logits_out != nullptr) logits_out[b * 16 + lane] = xl;
       if (mask_out != nullptr) mask_out[b * 16 + lane] = sel ? 1 : 0;
     }
+    issue_spec();
   }
 
   // ---- B: every token's gates (tagged words, at most two per thread); the union
@@ -1491,7 +1534,6 @@ __global__ __launch_bounds__(512) void decodeb_kernel(
   }
   __syncthreads();
   const int T = nu_s * G;
-  const int jn = lane & 31, kh = lane >> 5;
 
   // rows and slice of phase D
   const int R = W / DECB_S, s = b % DECB_S, r = b / DECB_S;
@@ -1523,38 +1565,22 @@ __global__ __launch_bounds__(512) void decodeb_kernel(
   int g0, g1;
   pp_split((uint32_t)(T / 8), (uint32_t)W, (uint32_t)b, g0, g1);
   const int q0 = 8 * g0, q1 = 8 * g1;
-  unsigned char* ring = smem + wv * DECB_RING_WAVE;
+  const bool spec_hit = spec && nu_s == 16;  // the rows requested at the start are this block's
+  if (spec && !spec_hit) vm_wait();          // wrong guess: they land before the rings are reused
   for (int nb0 = q0; nb0 < q1; nb0 += DECB_NB) {
     const int nq = min(DECB_NB, q1 - nb0);  // a multiple of 8
     const int nn = min(jn, nq - 1);         // this lane's neuron (B column; lanes beyond nq repeat the last)
-    // K-block kb of the wave -> stage: gate rows 0 .. nq-1, up rows nq .. 2nq-1, chunk c of
-    // row r at position c ^ (r & 7) (nq is a multiple of 8: a neuron's gate and up rows
-    // share the swizzle)
-    auto issue = [&](int j, dec_u32x4 (&xa)[TB][4]) {
-      const int kb = wv + NW * j;
-      unsigned char* slot = ring + (j % DP) * DECB_STAGE;
-      for (int ii = 0; ii < nq / 4; ++ii) {  // 1 KB (8 rows x 128 B) per instruction
-        const int f = 64 * ii + lane, rr = f >> 3;
-        const int which = rr >= nq ? 1 : 0, q = nb0 + rr - which * nq;
-        const int eg = q / G;
-        const bf16_t* src = gu + (size_t)((ul_s[eg] * G + q - eg * G) * 3 + which) * H + kb * 64 +
-                            8 * ((f & 7) ^ (rr & 7));
-        __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(slot + 1024 * ii), 16, 0,
-                                         DECB_NT);
-      }
+    dec_u32x4 xa[DP][TB][4];
+    if (!(spec_hit && nb0 == q0))
 #pragma unroll
-      for (int tb = 0; tb < TB; ++tb)
+      for (int j = 0; j < DP; ++j) issue_w(nb0, nq, j, [&](int e) { return ul_s[e]; });
 #pragma unroll
-        for (int i = 0; i < 4; ++i) xa[tb][i] = decb_ld16v(r_xf, decb_frag(kb * 4 + i, tb, lane));
-    };
+    for (int j = 0; j < DP; ++j) issue_x(j, xa[j]);
     f32x16_t ag[TB], au[TB];
 #pragma unroll
     for (int tb = 0; tb < TB; ++tb)
 #pragma unroll
       for (int q = 0; q < 16; ++q) ag[tb][q] = au[tb][q] = 0.0f;
-    dec_u32x4 xa[DP][TB][4];
-#pragma unroll
-    for (int j = 0; j < DP; ++j) issue(j, xa[j]);
     const uint32_t rg = (uint32_t)nn * 128, ru = (uint32_t)(nq + nn) * 128;
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
@@ -1577,69 +1603,51 @@ __global__ __launch_bounds__(512) void decodeb_kernel(
       }
       if (j + DP < CPL) {
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this stage's LDS reads are done
-        issue(j + DP, xa[j % DP]);
+        issue_w(nb0, nq, j + DP, [&](int e) { return ul_s[e]; });
+        issue_x(j + DP, xa[j % DP]);
       }
     }
-    wg_lds_barrier();  // every wave is done with its ring: the reduction area may be written
-    // the eight K partials, added in a fixed tree: w += w + 4, then w += w + 2, then w += w + 1
+    wg_lds_barrier();  // every wave is done with its ring: the partials may be written
 #pragma unroll
-    for (int tb = 0; tb < TB; ++tb) {
-      for (int half = 4; half >= 1; half >>= 1) {
-        if (wv >= half && wv < 2 * half) {
-          float* d = red_s + (wv - half) * 2048;
+    for (int tb = 0; tb < TB; ++tb)
 #pragma unroll
-          for (int q = 0; q < 16; ++q) {
-            d[q * 64 + lane] = ag[tb][q];
-            d[1024 + q * 64 + lane] = au[tb][q];
-          }
-        }
-        wg_lds_barrier();
-        if (wv < half) {
-          const float* d = red_s + wv * 2048;
+      for (int q = 0; q < 16; ++q) {
+        red_s[((tb * NW + wv) * 2) * 1024 + q * 64 + lane] = ag[tb][q];
+        red_s[((tb * NW + wv) * 2 + 1) * 1024 + q * 64 + lane] = au[tb][q];
+      }
+    wg_lds_barrier();
+    // entry v = (tb, q, l): token tb * 32 + mfma32_row(q, l), neuron nb0 + l % 32; the
+    // eight K partials added in wave order, then act = silu(g) * u * gate as bf16
+    for (int v = tid; v < TB * 1024; v += NT) {
+      const int tb = v >> 10, q = (v >> 6) & 15, l = v & 63;
+      const int t = tb * 32 + mfma32_row(q, l), n = l & 31;
+      float g = 0.0f, u = 0.0f;
 #pragma unroll
-          for (int q = 0; q < 16; ++q) {
-            ag[tb][q] += d[q * 64 + lane];
-            au[tb][q] += d[1024 + q * 64 + lane];
-          }
-        }
-        wg_lds_barrier();
+      for (int w = 0; w < NW; ++w) {
+        g += red_s[((tb * NW + w) * 2) * 1024 + q * 64 + l];
+        u += red_s[((tb * NW + w) * 2 + 1) * 1024 + q * 64 + l];
+      }
+      if (t < N && n < nq) {
+        const float gt = sg_s[t * 16 + ul_s[(nb0 + n) / G]];
+        const float a = fail ? __int_as_float(0x7fc00000) : gt != -1.0f ? pp_silu(g) * u * gt : 0.0f;
+        act_s[t * 32 + n] = f32_to_bf16(a);
       }
     }
-    if (nb0 + DECB_NB >= q1 && wv > 0)  // the last block: the rings are free for the down rows
-      dma_rows(hr0, min(rows_pp, hr1 - hr0), wv - 1, NW - 1);
-    if (wv == 0) {
-      // acts of the block as bf16 [t][32] in LDS, then published in fragment order (16 B =
-      // 8 neurons of one token)
-      const int qq = nb0 + jn;
-      const int e = jn < nq ? ul_s[qq / G] : 0;
-#pragma unroll
-      for (int tb = 0; tb < TB; ++tb)
-#pragma unroll
-        for (int q = 0; q < 16; ++q) {
-          const int t = tb * 32 + mfma32_row(q, lane);
-          if (t < N && jn < nq) {
-            const float gt = sg_s[t * 16 + e];
-            const float a = fail ? __int_as_float(0x7fc00000)
-                                 : gt != -1.0f ? pp_silu(ag[tb][q]) * au[tb][q] * gt : 0.0f;
-            act_s[t * 32 + jn] = f32_to_bf16(a);
-          }
-        }
-      wave_lds_sync();
-      const int ng = nq / 8;
-      for (int it = lane; it < N * ng; it += 64) {
-        const int t = it / ng, gi = it - t * ng;
-        const int k = nb0 + 8 * gi;  // union neuron of the group (a multiple of 8)
-        decb_st16(r_af, decb_frag(k >> 4, t >> 5, (t & 31) + 32 * ((k >> 3) & 1)),
-                  *(const uint4*)(act_s + t * 32 + 8 * gi));
-      }
-      wave_lds_sync();
+    wg_lds_barrier();
+    // published in fragment order: 16 B = 8 neurons of one token
+    const int ng = nq / 8;
+    for (int it = tid; it < N * ng; it += NT) {
+      const int t = it / ng, gi = it - t * ng;
+      const int k = nb0 + 8 * gi;  // union neuron of the group (a multiple of 8)
+      decb_st16(r_af, decb_frag(k >> 4, t >> 5, (t & 31) + 32 * ((k >> 3) & 1)),
+                *(const uint4*)(act_s + t * 32 + 8 * gi));
     }
+    wg_lds_barrier();  // the acts are read out: the rings may be refilled
   }
-  if (q0 >= q1 && wv > 0) dma_rows(hr0, min(rows_pp, hr1 - hr0), wv - 1, NW - 1);
-  if (wv == 0) {  // this workgroup's acts are stored (only wave 0 stores them)
-    vm_wait();
-    if (lane == 0) st_rlx(&aflag[b], tag);
-  }
+  vm_wait();  // this thread's act stores
+  __syncthreads();
+  if (tid == 0) st_rlx(&aflag[b], tag);
+  dma_rows(hr0, min(rows_pp, hr1 - hr0), wv, NW);  // the first pass's down rows (LDS is free)
 
   // ---- D: partial sums of rows [hr0, hr1) over slice s
   {
