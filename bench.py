@@ -62,6 +62,8 @@ def parse():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the small-batch (config 3) and E=192/G=32 side measurements")
+    ap.add_argument("--small-batch-only", action="store_true",
+                    help="run only the config-3 small-batch section (both paths) and print its numbers")
     ap.add_argument("--grid", type=int, default=0, help="decode workgroups (0 = library default)")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="run 5 plain elementwise passes (torch.neg, fp32) over this many MiB first "
@@ -179,6 +181,68 @@ def cpu_baseline(args):
             "torch_threads": n_all, "configs": out}
 
 
+def small_batch(ops, gi, torch, np, layers, dev, g, reps=1):
+    """Config 3 (bs 16 and 64, tau 0.95, Zipf(1.2) router bias): both paths, graph-replayed
+    (32 calls per graph over the rotating weight sets), `reps` timed replays (median)."""
+    extra = {}
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    Epad = (E + 15) // 16 * 16
+    # config 3: small-batch decode, bs 16 and 64, tau 0.95, Zipf(1.2) router bias;
+    # bytes = union of the selected experts' records + router + x
+    # two paths: the one-launch batch kernel (pp_moe_decode_batch, what TauSparseMoE
+    # runs for 2 <= N <= 64) and the five-kernel prefill pipeline on the same tokens
+    bias = torch.from_numpy(gi.zipf_bias(E)).to(dev)
+    bwsq = torch.empty(ops.decode_batch_workspace_bytes(H, E, G), dtype=torch.uint8, device=dev)
+    for nb in (16, 64):
+        R = 32
+        xq = torch.randn(R, nb, H, device=dev, generator=g)
+        wsq = torch.empty(ops.prefill_workspace_bytes(nb, H, E, G), dtype=torch.uint8, device=dev)
+        outq = torch.empty(nb, H, dtype=torch.bfloat16, device=dev)
+        union = []
+        for r in range(R):
+            packed, rp, _ = layers[r % len(layers)]
+            m = ops.route(xq[r], rp, E, 0.95, bias=bias, want_logits=False)["mask"]
+            union.append(int((m.sum(0) > 0).sum()))
+        u = float(np.mean(union))
+        byt = u * 3 * H * G * 2 + Epad * H * 4 + nb * H * 4 + nb * H * 2
+
+        def call_batch(r):
+            packed, rp, wsd = layers[r % len(layers)]
+            ops.moe_decode_batch(xq[r], rp, bias, E, G, 0.95, packed, wsd, bwsq, out=outq)
+
+        def call_prefill(r):
+            packed, rp, _ = layers[r % len(layers)]
+            ops.moe_prefill(xq[r], rp, bias, E, G, 0.95, packed, workspace=wsq, out=outq)
+
+        for key, call in ((f"bs{nb}", call_batch), (f"bs{nb}_prefill", call_prefill)):
+            for r in range(R):
+                call(r)
+            torch.cuda.synchronize()
+            gq = torch.cuda.CUDAGraph()
+            sq = torch.cuda.Stream()
+            sq.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(sq):
+                with torch.cuda.graph(gq, stream=sq):
+                    for r in range(R):
+                        call(r)
+            torch.cuda.current_stream().wait_stream(sq)
+            gq.replay()
+            torch.cuda.synchronize()
+            e0.record()
+            gq.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) * 1000.0 / R
+            extra[key] = {"us_per_layer": us, "tokens_per_s": nb / (us * 1e-6), "experts_hit_mean": u,
+                          "hbm_gbs": byt / (us * 1e-6) / 1e9, "frac": byt / (us * 1e-6) / (PEAK_HBM_GBS * 1e9),
+                          "tau": 0.95, "router_bias": "zipf(1.2)",
+                          "path": "pp_moe_decode_batch (one launch)" if call is call_batch else
+                                  "pp_moe_prefill (route, bucket, gate/up, down, combine)"}
+        for lid in range(len(layers)):  # the batch calls left the decode workspaces healthy
+            assert ops.decode_state(layers[lid][2], E)["error"] == 0
+    return extra
+
+
 def main():
     args = parse()
     if args.pmc_summary:
@@ -227,6 +291,10 @@ def main():
         layers.append((packed, rp, ws))
         del wg, wu, wd
     torch.cuda.synchronize()
+
+    if args.small_batch_only:
+        print(json.dumps({"small_batch": small_batch(ops, gi, torch, np, layers, dev, g, reps=5)}))
+        return
 
     # ---------------- decode: inputs resident, per-step k from an untimed pass
     K, W = args.steps, args.warmup
@@ -370,59 +438,7 @@ def main():
     extra = None
     if not args.no_extra:
         extra = {}
-        # config 3: small-batch decode, bs 16 and 64, tau 0.95, Zipf(1.2) router bias;
-        # bytes = union of the selected experts' records + router + x
-        # two paths: the one-launch batch kernel (pp_moe_decode_batch, what TauSparseMoE
-        # runs for 2 <= N <= 64) and the five-kernel prefill pipeline on the same tokens
-        bias = torch.from_numpy(gi.zipf_bias(E)).to(dev)
-        bwsq = torch.empty(ops.decode_batch_workspace_bytes(H, E, G), dtype=torch.uint8, device=dev)
-        for nb in (16, 64):
-            R = 32
-            xq = torch.randn(R, nb, H, device=dev, generator=g)
-            wsq = torch.empty(ops.prefill_workspace_bytes(nb, H, E, G), dtype=torch.uint8, device=dev)
-            outq = torch.empty(nb, H, dtype=torch.bfloat16, device=dev)
-            union = []
-            for r in range(R):
-                packed, rp, _ = layers[r % len(layers)]
-                m = ops.route(xq[r], rp, E, 0.95, bias=bias, want_logits=False)["mask"]
-                union.append(int((m.sum(0) > 0).sum()))
-            u = float(np.mean(union))
-            byt = u * 3 * H * G * 2 + Epad * H * 4 + nb * H * 4 + nb * H * 2
-
-            def call_batch(r):
-                packed, rp, wsd = layers[r % len(layers)]
-                ops.moe_decode_batch(xq[r], rp, bias, E, G, 0.95, packed, wsd, bwsq, out=outq)
-
-            def call_prefill(r):
-                packed, rp, _ = layers[r % len(layers)]
-                ops.moe_prefill(xq[r], rp, bias, E, G, 0.95, packed, workspace=wsq, out=outq)
-
-            for key, call in ((f"bs{nb}", call_batch), (f"bs{nb}_prefill", call_prefill)):
-                for r in range(R):
-                    call(r)
-                torch.cuda.synchronize()
-                gq = torch.cuda.CUDAGraph()
-                sq = torch.cuda.Stream()
-                sq.wait_stream(torch.cuda.current_stream())
-                with torch.cuda.stream(sq):
-                    with torch.cuda.graph(gq, stream=sq):
-                        for r in range(R):
-                            call(r)
-                torch.cuda.current_stream().wait_stream(sq)
-                gq.replay()
-                torch.cuda.synchronize()
-                e0.record()
-                gq.replay()
-                e1.record()
-                torch.cuda.synchronize()
-                us = e0.elapsed_time(e1) * 1000.0 / R
-                extra[key] = {"us_per_layer": us, "tokens_per_s": nb / (us * 1e-6), "experts_hit_mean": u,
-                              "hbm_gbs": byt / (us * 1e-6) / 1e9, "frac": byt / (us * 1e-6) / (PEAK_HBM_GBS * 1e9),
-                              "tau": 0.95, "router_bias": "zipf(1.2)",
-                              "path": "pp_moe_decode_batch (one launch)" if call is call_batch else
-                                      "pp_moe_prefill (route, bucket, gate/up, down, combine)"}
-            for lid in range(len(layers)):  # the batch calls left the decode workspaces healthy
-                assert ops.decode_state(layers[lid][2], E)["error"] == 0
+        extra.update(small_batch(ops, gi, torch, np, layers, dev, g))
         # real-checkpoint shape: E=192 experts of G=32, one layer, decode bs=1 and prefill 2048
         E2, G2 = 192, 32
         l192 = []

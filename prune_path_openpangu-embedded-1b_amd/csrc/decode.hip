@@ -1308,12 +1308,14 @@ __global__ __launch_bounds__(512) void decode2p_kernel(
 //    up rows of each of its K-blocks into its own LDS ring of three stages (whole 128-byte
 //    lines per request, chunks XOR-swizzled by row) and loads the x fragments into
 //    registers (1 KB contiguous per request); 32x32x16 MFMA, tokens x neurons. The eight
-//    partials are added in a fixed tree; act[t][q] = silu(g) * u * gate(t, e) (0 where
-//    token t did not select e) is published as bf16 in MFMA-fragment order;
+//    partials go through LDS and every thread adds them in wave order; act[t][q] =
+//    silu(g) * u * gate(t, e) (0 where token t did not select e) is published as bf16 in
+//    MFMA-fragment order. Speculation: the first stages are requested before the routing,
+//    assuming every expert is hit (16 of 16 in config 3), and drained if not;
 // D. down: workgroup b = 16 r + s takes the rows of row group r (8-row blocks of H split
 //    over W / 16 groups) and the union neurons of slice s (16-neuron blocks of T split
 //    over 16 slices; with all 16 experts hit, slice s is expert s): its down rows are
-//    DMA'd to LDS once its gate/up work is done, and MFMA (rows x tokens) over the slice
+//    DMA'd to LDS once its acts are published, and MFMA (rows x tokens) over the slice
 //    writes a partial [row][token] sum in fp32;
 // E. fold: the 8-row block u of H is summed over the 16 slices in slice order by
 //    workgroup u % W, so the bf16 output is the same bits on every call.
@@ -1688,7 +1690,7 @@ __global__ __launch_bounds__(512) void decodeb_kernel(
 #pragma unroll
         for (int q = 0; q < 16; ++q) {
           const int rr = rbk * 32 + mfma32_row(q, lane);
-          if (rr < nr)
+          if (rr < nr && tb * 32 + jn < N)  // the padding tokens' sums are never read
             __builtin_amdgcn_raw_buffer_store_b32(fail ? 0x7fc00000u : __float_as_uint(acc[q]), r_part,
                                                   (uint32_t)(((s * H + p0 + rr) * DECB_MAXN + tb * 32 + jn) * 4), 0,
                                                   DECB_SC1);
