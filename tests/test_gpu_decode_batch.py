@@ -108,6 +108,48 @@ def test_decode_batch_interleaved_with_decode(pkg):
     assert pkg.ops.decode_state(m.decode_workspace, E)["error"] == 0
 
 
+def test_decode_batch_graph_replays(pkg):
+    """A call captured in a hipGraph (as the bench runs it): every replay, with eager calls on
+    the same workspaces and host synchronisations between replays, gives the eager result
+    bit for bit; the epoch and the tags advance per call whichever way the call is launched."""
+    H, E, G, N = 1536, 16, 384, 16
+    w = gi.layer_weights(61, H=H, I=E * G, E=E)
+    m = make_module(pkg, w, 0.95, bias=gi.zipf_bias(E))
+    dev = torch.device("cuda:0")
+    xs = [to_gpu(gi.tokens(62 + i, N, H=H), torch.float32) for i in range(3)]
+    bws = torch.empty(pkg.ops.decode_batch_workspace_bytes(H, E, G), dtype=torch.uint8, device=dev)
+
+    def call(x, out=None):
+        return pkg.ops.moe_decode_batch(x, m.router_packed, m.router_bias, E, G, 0.95, m.packed_experts,
+                                        m.decode_workspace, bws, out=out)
+
+    refs = [call(x) for x in xs]
+    torch.cuda.synchronize()
+    xin = xs[0].clone()
+    out = torch.empty(N, H, dtype=torch.bfloat16, device=dev)
+    call(xin, out)  # warm-up on the capture buffers
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(graph, stream=s):
+            call(xin, out)
+    torch.cuda.current_stream().wait_stream(s)
+    e0 = pkg.ops.decode_state(m.decode_workspace, E)["epochb"]
+    for rep in range(6):
+        i = rep % 3
+        xin.copy_(xs[i])
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, refs[i]), f"replay {rep}"
+        o = call(xs[(i + 1) % 3])  # eager work between the replays
+        torch.cuda.synchronize()
+        assert torch.equal(o, refs[(i + 1) % 3]), f"eager call after replay {rep}"
+    st = pkg.ops.decode_state(m.decode_workspace, E)
+    assert st["error"] == 0 and st["epochb"] == e0 + 12
+
+
 def test_decode_batch_module_dispatch(pkg):
     """TauSparseMoE.forward takes the batch kernel for 2 <= N <= batch_max at the
     supported shapes and prefill beyond; both agree with the float64 restatement."""
