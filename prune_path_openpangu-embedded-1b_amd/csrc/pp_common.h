@@ -123,6 +123,41 @@ __device__ __forceinline__ float row16_max(float v) {
   v = fmaxf(v, dpp_mov<PP_DPP_XOR2>(v));
   return fmaxf(v, dpp_mov<PP_DPP_XOR1>(v));
 }
+// Whole-wave maximum (rows by DPP, then the four row maxima read as scalars); fmaxf is
+// order-free, so the value equals wave_max's. Wave-uniform.
+__device__ __forceinline__ float wave_max_dpp(float v) {
+  v = row16_max(v);
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+// quad_perm [3,2,1,0] (lane 3 - i of the quad) followed by row_half_mirror (lane 7 - i
+// of the half row) reads lane i ^ 4: both are fixed involutions, with no rotation
+// direction to get wrong.
+#define PP_DPP_QREV 0x1B
+// Inclusive prefix sum of doubles over the 64 lanes in lane order: row_shr:1, 2, 4, 8
+// (lane i reads lane i - n of its row; lanes with no source read the identity 0), then
+// row_bcast:15 into rows 1 and 3 and row_bcast:31 into rows 2 and 3 -- the gfx9 wave
+// scan of LLVM's AMDGPU atomic optimizer. The order of the additions differs from a
+// sequential sum, so callers use it where every partial sum is exact.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ double dpp_f64(double v) {
+  const unsigned long long u = (unsigned long long)__double_as_longlong(v);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)u, CTRL, ROW_MASK, 0xf, false);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(u >> 32), CTRL, ROW_MASK, 0xf, false);
+  return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+}
+__device__ __forceinline__ double wave_incl_scan_f64(double v) {
+  v += dpp_f64<0x111, 0xf>(v);
+  v += dpp_f64<0x112, 0xf>(v);
+  v += dpp_f64<0x114, 0xf>(v);
+  v += dpp_f64<0x118, 0xf>(v);
+  v += dpp_f64<0x142, 0xa>(v);
+  v += dpp_f64<0x143, 0xc>(v);
+  return v;
+}
 // Minimum over each 16-lane row (every lane of the row ends with it).
 __device__ __forceinline__ int row16_min_i(int v) {
   v = min(v, __float_as_int(dpp_mov<PP_DPP_ROR8>(__int_as_float(v))));
@@ -600,10 +635,11 @@ __device__ __forceinline__ unsigned long long sel_key(float p, int j) {
   return ((unsigned long long)(~b) << 32) | (uint32_t)j;
 }
 
-// Value of lane (lane ^ j) for a 64-bit key: DPP for j = 1, 2 (quad permutes) and 8 (the
-// half-row rotation, i ^ 8 whichever way it turns), the LDS permute otherwise. j is a
-// constant after unrolling. (A rotation-based xor 4 depends on the rotation's direction:
-// taken the wrong way round it pairs the wrong lanes and the sort loses keys.)
+// Value of lane (lane ^ j) for a 64-bit key: DPP for j = 1, 2 (quad permutes), 4 (quad
+// reverse then half-row mirror, two involutions) and 8 (the half-row rotation, i ^ 8
+// whichever way it turns), the LDS permute for 16 and 32. j is a constant after
+// unrolling. (A rotation-based xor 4 depends on the rotation's direction: taken the
+// wrong way round it pairs the wrong lanes and the sort loses keys.)
 template <int CTRL>
 __device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
   return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xf, 0xf, false);
@@ -617,6 +653,9 @@ __device__ __forceinline__ unsigned long long key_xor(unsigned long long v, int 
   } else if (j == 2) {
     a = dpp_u32<PP_DPP_XOR2>(lo);
     b = dpp_u32<PP_DPP_XOR2>(hi);
+  } else if (j == 4) {
+    a = dpp_u32<PP_DPP_HALF_MIRROR>(dpp_u32<PP_DPP_QREV>(lo));
+    b = dpp_u32<PP_DPP_HALF_MIRROR>(dpp_u32<PP_DPP_QREV>(hi));
   } else if (j == 8) {
     a = dpp_u32<PP_DPP_ROR8>(lo);
     b = dpp_u32<PP_DPP_ROR8>(hi);
@@ -632,7 +671,7 @@ static __device__ void select_one_token_wg(LG lg, int E, float tau, SelScratch* 
   const int lane = tid & 63, wv = tid >> 6, nw = nthreads >> 6;
   const int E16 = (E + 15) & ~15;
   const float x = tid < E ? lg(tid) : -__builtin_huge_valf();
-  float m = wave_max(x);
+  float m = wave_max_dpp(x);
   if (lane == 0) red[wv] = m;
   wg_lds_barrier();
   m = red[0];
@@ -648,8 +687,7 @@ static __device__ void select_one_token_wg(LG lg, int E, float tau, SelScratch* 
 #pragma unroll
     for (int c = 1; c < PP_MAX_EXPERTS / 16; ++c)
       if (16 * c < E16) acc = __fadd_rn(acc, col[c]);
-#pragma unroll
-    for (int o = 8; o >= 1; o >>= 1) acc = __fadd_rn(acc, __shfl_xor(acc, o, 16));
+    acc = row16_sum(acc);  // the xor 8, 4, 2, 1 butterfly, by DPP
     if (tid == 0) red[0] = __fdiv_rn(1.0f, acc);
   }
   wg_lds_barrier();
@@ -658,8 +696,10 @@ static __device__ void select_one_token_wg(LG lg, int E, float tau, SelScratch* 
   // shuffles; padding ~0 sorts last), stores the sorted run, and each key's rank is its
   // place in its run plus the number of smaller keys in the other runs (binary search).
   // The same ranks as counting all smaller keys (E LDS reads per key, 2.4 us at E = 192);
-  // the whole E = 192 decode layer 24.7 -> 24.35 us with LDS-permute shuffles; 14 of the
-  // sort's 21 exchanges go through DPP.
+  // the whole E = 192 decode layer 24.7 -> 24.35 us with LDS-permute shuffles; 18 of the
+  // sort's 21 exchanges go through DPP. The binary searches over the other runs are
+  // interleaved (one LDS round trip per step for all runs, not one per run): runs past
+  // nwk and the wave's own run are searched too, in bounds of keys, and not counted.
   const int nwk = (E + 63) >> 6;  // waves holding keys
   unsigned long long key = tid < E ? sel_key(pt, tid) : ~0ull;
   if (tid < E) ss->e[tid] = pt;
@@ -680,15 +720,17 @@ static __device__ void select_one_token_wg(LG lg, int E, float tau, SelScratch* 
   int rank = lane;
   const int idx = (int)(uint32_t)key;
   if (holder) {
-    for (int w2 = 0; w2 < nwk; ++w2) {
-      if (w2 == wv) continue;
-      const unsigned long long* run = keys + 64 * w2;
-      int lo = 0;  // keys of run w2 below key
+    constexpr int NRUN = PP_MAX_EXPERTS / 64;
+    int lo[NRUN];  // keys of run r below key
 #pragma unroll
-      for (int step = 32; step >= 1; step >>= 1) lo += run[lo + step - 1] < key ? step : 0;
-      lo += (lo == 63 && run[63] < key) ? 1 : 0;
-      rank += lo;
-    }
+    for (int r = 0; r < NRUN; ++r) lo[r] = 0;
+#pragma unroll
+    for (int step = 32; step >= 1; step >>= 1)
+#pragma unroll
+      for (int r = 0; r < NRUN; ++r) lo[r] += keys[64 * r + lo[r] + step - 1] < key ? step : 0;
+#pragma unroll
+    for (int r = 0; r < NRUN; ++r)
+      if (r < nwk && r != wv) rank += lo[r] + ((lo[r] == 63 && keys[64 * r + 63] < key) ? 1 : 0);
     if (rank < E && idx < E) {  // always, for a correct sort (else ss->bad below)
       ss->srt[rank] = ss->e[idx];
       ss->order[rank] = idx;
@@ -718,19 +760,13 @@ static __device__ void select_one_token_wg(LG lg, int E, float tau, SelScratch* 
         run += (double)v[i];
         sv[i] = run;
       }
-      double incl = run;
-#pragma unroll
-      for (int o = 1; o < PP_WAVE; o <<= 1) {
-        const double t = __shfl_up(incl, o, PP_WAVE);
-        if (lane >= o) incl += t;
-      }
+      const double incl = wave_incl_scan_f64(run);
       const double excl = incl - run;
       const float tau32 = tau;
-      int c = 0;
+      int c = 0;  // ranks whose running sum stays below tau, counted by ballots
 #pragma unroll
-      for (int i = 0; i < QPL; ++i) c += (lane * QPL + i < E && (float)(excl + sv[i]) < tau32) ? 1 : 0;
-#pragma unroll
-      for (int o = 32; o >= 1; o >>= 1) c += __shfl_xor(c, o, PP_WAVE);
+      for (int i = 0; i < QPL; ++i)
+        c += __popcll(__ballot(lane * QPL + i < E && (float)(excl + sv[i]) < tau32));
       k = c > 0 ? c : 1;
     } else {
       k = tau_cut([&](int q) { return ss->srt[q]; }, E, tau);

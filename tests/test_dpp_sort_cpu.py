@@ -1,20 +1,22 @@
 """CPU restatement of the workgroup rank computation of the E > 16 decode selection
 (select_one_token_wg in csrc/pp_common.h): per 64-lane wave a bitonic sort of 64-bit
-keys whose partner exchanges use DPP lane moves for xor 1, 2 and 8 and the LDS permute
-otherwise, then each key's rank = its place in its run + the number of smaller keys in
+keys whose partner exchanges use DPP lane moves for xor 1, 2, 4 and 8 and the LDS permute
+for 16 and 32, then each key's rank = its place in its run + the number of smaller keys in
 every other run (binary search). No GPU.
 
 The DPP lane maps are written from the ISA definitions of the two controls the kernel
 uses (lane i of the result reads source lane src[i]):
 * quad_perm [p0, p1, p2, p3]: src[i] = 4 * (i // 4) + p[i % 4];
+* row_half_mirror: src[i] = 8 * (i // 8) + 7 - i % 8;
 * row_ror:n: inside each 16-lane row, the row rotated by n lanes. The direction is the
   thing that once went wrong (a two-rotation xor 4 that assumed the opposite direction
   lost keys), so every check below runs under BOTH directions, and the kernel only uses
-  row_ror:8, which is direction-free.
+  row_ror:8, which is direction-free. xor 4 is now quad_perm [3,2,1,0] followed by
+  row_half_mirror: two fixed involutions, no direction involved.
 
 Checks: each DPP exchange the kernel uses is the permutation lane i <-> lane i ^ j
 (an involution pairing i with i ^ j) under either rotation direction; row_ror:4 is not
-i ^ 4 under either direction (why the kernel keeps xor 4 on the LDS permute); the whole
+i ^ 4 under either direction (why the kernel builds xor 4 from the two mirrors); the whole
 rank computation equals a plain sort of the keys on random, tie-heavy, all-equal and NaN
 rows for E = 17 .. 256 (a permutation of 0 .. E-1 with no lost or duplicated key).
 """
@@ -35,6 +37,17 @@ def row_ror(n, direction):
 
 XOR1 = [1, 0, 3, 2]  # PP_DPP_XOR1 = 0xB1: quad_perm fields 1,0,3,2 (2 bits each, lane 0 first)
 XOR2 = [2, 3, 0, 1]  # PP_DPP_XOR2 = 0x4E
+QREV = [3, 2, 1, 0]  # PP_DPP_QREV = 0x1B
+
+
+def half_mirror():
+    return np.array([8 * (i // 8) + 7 - i % 8 for i in range(WAVE)])
+
+
+def then(first, second):
+    """Source lanes of DPP move `second` applied to the result of `first`: lane i of
+    the result reads lane second[i] of the intermediate, which holds lane first[second[i]]."""
+    return first[second]
 
 
 def _decode_quad_perm(ctrl):
@@ -43,9 +56,10 @@ def _decode_quad_perm(ctrl):
 
 def lane_maps(direction):
     """Source lane of every lane for the partner exchange of distance j, as the kernel
-    does it (key_xor): DPP for j = 1, 2, 8, the LDS permute (exact xor) otherwise."""
-    m = {1: quad_perm(XOR1), 2: quad_perm(XOR2), 8: row_ror(8, direction)}
-    for j in (4, 16, 32):
+    does it (key_xor): DPP for j = 1, 2, 4, 8, the LDS permute (exact xor) otherwise."""
+    m = {1: quad_perm(XOR1), 2: quad_perm(XOR2), 4: then(quad_perm(QREV), half_mirror()),
+         8: row_ror(8, direction)}
+    for j in (16, 32):
         m[j] = np.arange(WAVE) ^ j
     return m
 
@@ -53,6 +67,7 @@ def lane_maps(direction):
 def test_dpp_controls_encode_the_quad_perms():
     assert _decode_quad_perm(0xB1) == XOR1
     assert _decode_quad_perm(0x4E) == XOR2
+    assert _decode_quad_perm(0x1B) == QREV
 
 
 @pytest.mark.parametrize("direction", [+1, -1])
@@ -158,3 +173,40 @@ def test_a_wrong_exchange_is_caught_by_the_permutation_check():
     keys = sel_key(rng.standard_normal(E).astype(np.float32), np.arange(E))
     order, collided = wg_ranks(keys, maps)
     assert collided and (order == -1).any()
+
+
+def _dpp_scan_step(v, ctrl, row_mask):
+    """One `v += update_dpp(0, v, ctrl, row_mask, 0xf, false)` of wave_incl_scan_f64
+    (csrc/pp_common.h): row_shr:n (0x110 + n) reads lane i - n of the row, row_bcast:15
+    (0x142) lane 15 of the previous row, row_bcast:31 (0x143) lane 31; a lane with no
+    source, or in a row the row mask leaves out, reads the identity 0."""
+    out = np.zeros_like(v)
+    for i in range(WAVE):
+        row, r = divmod(i, 16)
+        if not (row_mask >> row) & 1:
+            continue
+        if 0x111 <= ctrl <= 0x11F:
+            n = ctrl - 0x110
+            if r >= n:
+                out[i] = v[i - n]
+        elif ctrl == 0x142:
+            if row > 0:
+                out[i] = v[16 * row - 1]
+        elif ctrl == 0x143:
+            out[i] = v[31]
+        else:
+            raise AssertionError(hex(ctrl))
+    return v + out
+
+
+def test_dpp_wave_scan_is_an_inclusive_prefix_sum():
+    """The six DPP steps of wave_incl_scan_f64 give every lane the sum of lanes 0..i (on
+    integers, where the addition order cannot matter -- as for the exact fp64 partial
+    sums the selection cut feeds it)."""
+    rng = np.random.default_rng(7)
+    for _ in range(20):
+        v = rng.integers(0, 1 << 20, WAVE).astype(np.int64)
+        s = v.copy()
+        for ctrl, mask in ((0x111, 0xF), (0x112, 0xF), (0x114, 0xF), (0x118, 0xF), (0x142, 0xA), (0x143, 0xC)):
+            s = _dpp_scan_step(s, ctrl, mask)
+        np.testing.assert_array_equal(s, np.cumsum(v))
