@@ -642,7 +642,8 @@ __device__ __forceinline__ unsigned long long sel_key(float p, int j) {
 // wrong way round it pairs the wrong lanes and the sort loses keys.)
 template <int CTRL>
 __device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
-  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xf, 0xf, false);
+  // every lane has a source lane for these controls, so no old value is needed
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, CTRL, 0xf, 0xf, false);
 }
 __device__ __forceinline__ unsigned long long key_xor(unsigned long long v, int j) {
   const uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
@@ -711,7 +712,9 @@ static __device__ void select_one_token_wg(LG lg, int E, float tau, SelScratch* 
       for (int j = k2 >> 1; j > 0; j >>= 1) {
         const unsigned long long o = key_xor(key, j);
         const bool keep_min = ((lane & j) == 0) == ((lane & k2) == 0);
-        key = keep_min ? (o < key ? o : key) : (o > key ? o : key);
+        // one compare: real keys are unique, and two padding keys are equal, so
+        // "o < key" decides both the minimum and the maximum
+        key = ((o < key) == keep_min) ? o : key;
       }
     keys[tid] = key;
   }
