@@ -1060,7 +1060,7 @@ __global__ __launch_bounds__(512) void decode2p_kernel(
 #pragma unroll
       for (int i = 0; i < KPT; ++i)
         if (tid + i * NT < H) sacc = __builtin_fmaf(xv[i], wr[i], sacc);
-      sacc = wave_sum(sacc);
+      sacc = wave_sum_dpp(sacc);  // fixed order: rows by DPP, then the four row totals
       if (lane == 0) red_s[wv] = sacc;
       __syncthreads();
       if (tid < DEC2_LREPS) {
