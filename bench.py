@@ -181,6 +181,64 @@ def cpu_baseline(args):
             "torch_threads": n_all, "configs": out}
 
 
+def eager_decode(pkg, ops, torch, layer, x, E, G, tau, dev, g, reps=2000):
+    """Host cost of one eager (not graph-captured) bs = 1 decode call through each layer a
+    caller can use: the C ABI over ctypes, the torch.library op
+    (torch.ops.prunepath.moe_decode_into) and the TauSparseMoE module. Per path: `reps`
+    calls back to back after 50 warm-up calls; host_us = time to issue them / reps (no
+    synchronisation inside the loop), wall_us = time until the GPU has finished them /
+    reps. The kernel itself takes ~11.5 us, so a host_us above that is the host's bound."""
+    import ctypes
+    packed, rp, ws = layer
+    H = x.numel()
+    out = torch.empty(1, H, dtype=torch.bfloat16, device=dev)
+    lib = pkg._lib.lib()
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    xp, rpp, pp, op, wsp = (ctypes.c_void_p(t.data_ptr()) for t in (x, rp, packed, out, ws))
+    tau_c = ctypes.c_float(tau)
+
+    def abi():
+        rc = lib.pp_moe_decode(xp, 0, H, rpp, None, E, G, tau_c, pp, op, wsp, 0, stream)
+        if rc != 0:
+            raise RuntimeError("pp_moe_decode: %d" % rc)
+
+    x2 = x.reshape(1, H)
+    top = pkg._lib.torch_ops().moe_decode_into
+
+    def torch_op():
+        top(x2, rp, None, E, G, float(tau), packed, ws, out, 0)
+
+    I = E * G
+    mod = pkg.TauSparseMoE(H, I, E, G, tau).to(dev)
+    with torch.no_grad():
+        mod.load_from_masked(torch.randn(I, H, device=dev, generator=g) * 0.02,
+                             torch.randn(I, H, device=dev, generator=g) * 0.02,
+                             torch.randn(H, I, device=dev, generator=g) * 0.02,
+                             torch.randn(E, H, device=dev, generator=g) * 0.02,
+                             torch.arange(I, device=dev) // G)
+    x3 = x.reshape(1, 1, H)
+
+    def module():
+        with torch.no_grad():
+            mod(x3)
+
+    res = {"reps": reps, "note": "eager bs=1 decode calls back to back; host_us = issue time per call, "
+                                 "wall_us = time per call until the GPU finished"}
+    for name, fn in (("c_abi_ctypes", abi), ("torch_op", torch_op), ("module", module)):
+        for _ in range(50):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            fn()
+        t1 = time.perf_counter()
+        torch.cuda.synchronize()
+        t2 = time.perf_counter()
+        res[name] = {"host_us": (t1 - t0) * 1e6 / reps, "wall_us": (t2 - t0) * 1e6 / reps}
+    del mod
+    return res
+
+
 def small_batch(ops, gi, torch, np, layers, dev, g, reps=1):
     """Config 3 (bs 16 and 64, tau 0.95, Zipf(1.2) router bias): both paths, graph-replayed
     (32 calls per graph over the rotating weight sets), `reps` timed replays (median)."""
@@ -438,6 +496,7 @@ def main():
     extra = None
     if not args.no_extra:
         extra = {}
+        extra["eager_decode"] = eager_decode(pkg, ops, torch, layers[0], xs[0], E, G, args.tau, dev, g)
         extra.update(small_batch(ops, gi, torch, np, layers, dev, g))
         # real-checkpoint shape: E=192 experts of G=32, one layer, decode bs=1 and prefill 2048
         E2, G2 = 192, 32

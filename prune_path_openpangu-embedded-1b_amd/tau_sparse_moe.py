@@ -43,7 +43,18 @@ from typing import Optional
 import torch
 import torch.nn as nn
 
-from . import ops
+from . import _lib, ops
+
+
+_DECODE_OP = None
+
+
+def _decode_op():
+    """torch.ops.prunepath.moe_decode.default, resolved once."""
+    global _DECODE_OP
+    if _DECODE_OP is None:
+        _DECODE_OP = _lib.torch_ops().moe_decode.default
+    return _DECODE_OP
 
 
 class TauSparseMoE(nn.Module):
@@ -79,8 +90,11 @@ class TauSparseMoE(nn.Module):
 
     # ------------------------------------------------------------------ packing
     def _weights_key(self):
-        return tuple((t.data_ptr(), t._version, t.device, t.dtype) for t in
-                     (self.W_gate, self.W_up, self.W_down, self.router))
+        # read from _buffers directly (nn.Module.__getattr__ costs ~1 us per lookup) and
+        # with get_device() (an int, where .device builds an object): this runs per call
+        b = self._buffers
+        return tuple((t.data_ptr(), t._version, t.get_device(), t.dtype) for t in
+                     (b["W_gate"], b["W_up"], b["W_down"], b["router"]))
 
     def mark_weights_changed(self) -> None:
         self._packed_key = None
@@ -163,8 +177,11 @@ class TauSparseMoE(nn.Module):
 
     # ------------------------------------------------------------------ forward
     def forward_decode(self, x_flat: torch.Tensor, B: int, L: int, H: int) -> torch.Tensor:
-        out = ops.moe_decode(x_flat, self.router_packed, self.router_bias, self.num_experts, self.group_size,
-                             self.tau, self.packed_experts, self.decode_workspace)
+        # the op overload called directly with the buffers from _buffers: the eager host
+        # cost of a decode call is what bounds an eager caller (the kernel takes ~11 us)
+        b = self._buffers
+        out = _decode_op()(x_flat, b["router_packed"], b["router_bias"], self.num_experts, self.group_size,
+                           float(self.tau), b["packed_experts"], b["decode_workspace"], 0)
         if self.checked:
             self.check_decode()
         return out.view(B, L, H)
