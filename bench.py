@@ -540,6 +540,28 @@ def main():
         byt = k2 * 3 * H * G2 * 2 + 192 * H * 4 + H * 6
         extra["e192_g32_decode"] = {"us_per_layer": us, "k_mean": k2, "hbm_gbs": byt / (us * 1e-6) / 1e9,
                                     "weight_sets": NS}
+        # the same shape's prefill (2048 tokens): G = 32 takes the G % 64 != 0 GEMMs, in
+        # passes of at most 455 tokens (bounded workspace); eager calls between events
+        if not args.no_prefill:
+            Np = args.prefill_tokens
+            xp = torch.randn(Np, H, device=dev, generator=g)
+            packed, rp, _ = l192[0]
+            wsp = torch.empty(ops.prefill_workspace_bytes(Np, H, E2, G2), dtype=torch.uint8, device=dev)
+            opf = torch.empty(Np, H, dtype=torch.bfloat16, device=dev)
+            P2 = int(ops.route(xp, rp, E2, args.tau)["count"].sum())
+            for _ in range(2):
+                ops.moe_prefill(xp, rp, None, E2, G2, args.tau, packed, workspace=wsp, out=opf)
+            torch.cuda.synchronize()
+            e0.record()
+            for _ in range(5):
+                ops.moe_prefill(xp, rp, None, E2, G2, args.tau, packed, workspace=wsp, out=opf)
+            e1.record()
+            torch.cuda.synchronize()
+            ms2 = e0.elapsed_time(e1) / 5
+            extra["e192_g32_prefill"] = {
+                "tokens": Np, "tau": args.tau, "pairs": P2, "ms_per_call": ms2, "tokens_per_s": Np / (ms2 * 1e-3),
+                "layer_mfma_util": 6.0 * P2 * H * G2 / (ms2 * 1e-3) / (PEAK_BF16_TFLOPS * 1e12)}
+            del wsp, opf, xp
         del l192
         # masked training path: the expert gating of MoELayer.forward and its backward on
         # a training batch of 16 x 1024 tokens, bf16 activations [16384, 6144] (200 MB per

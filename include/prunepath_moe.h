@@ -236,6 +236,19 @@ int pp_expert_down(const void* act_bf16, int H, int G, const void* packed, int E
 int pp_combine(const float* y_f32, const int32_t* token_pairs, const int32_t* count,
                int64_t n_tokens, int H, int E, void* out_bf16, void* stream);
 
+/* SwiGLU with the expert gating for the dense prefill form, where the grouped GEMMs
+ * have no MFMA tiling (G % 64 != 0, e.g. the checkpoint's E = 192, G = 32): the
+ * torch.library op prunepath::moe_prefill computes gate and up of every neuron for
+ * every token with library GEMMs (fp32 results), this, then one down GEMM over all
+ * neurons. Replaces the epilogue of the reference's fused expert kernel
+ * (src/tl_kernel_optimized_Ultimate_PanGU.py:316-321: silu(acc_gate) * acc_up * weight,
+ * rounded to bf16), with the weight of an unselected expert 0:
+ *   act[t, n] = bf16(silu(gate[t, n]) * up[t, n] * gates[t, n / G])
+ * gate_f32, up_f32 fp32 [n_tokens, E*G]; gates fp32 [n_tokens, E] (the router's gates,
+ * 0 where not selected); act_bf16 [n_tokens, E*G]. gate, up and act 16-byte aligned. */
+int pp_swiglu_gate(const float* gate_f32, const float* up_f32, const float* gates, int64_t n_tokens,
+                   int E, int G, void* act_bf16, void* stream);
+
 /* ------------------------------------------------------------------------- *
  * Masked training path: the expert gating of MoELayer.forward
  * (src/MoEBlock_origin.py:205-212: self_moe_mask = experts_prob @ experts_masks;

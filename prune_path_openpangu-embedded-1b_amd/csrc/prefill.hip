@@ -16,6 +16,8 @@
 // beyond the last partial tile of each expert), 256 threads = 4 waves, BK = 64:
 // gemm_v3_kernel for G % 64 == 0 (LDS-DMA pipeline, below), gateup_kernel /
 // down_kernel (register-staged, row-padded LDS tiles) otherwise.
+#include <algorithm>
+
 #include "pp_common.h"
 
 #define GM_THREADS 256
@@ -998,6 +1000,60 @@ extern "C" int pp_combine(const float* y_f32, const int32_t* token_pairs, const 
   PP_REQUIRE(n_tokens == 0 || (y_f32 && token_pairs && count && out_bf16), PP_ERR_INVALID,
              "pp_combine: null pointer");
   return combine_launch(y_f32, token_pairs, count, n_tokens, H, E, (bf16_t*)out_bf16, (hipStream_t)stream);
+}
+
+// ------------------------------------------------------------------ dense SwiGLU with expert gating
+// For the dense prefill form (gate and up of every neuron for every token, from two
+// library GEMMs with fp32 results; then one down GEMM over all neurons), used where the
+// grouped GEMMs have no MFMA tiling (G % 64 != 0, the checkpoint's E = 192, G = 32):
+//   act[t, n] = bf16(silu(g[t, n]) * u[t, n] * gates[t, n / G])
+// with gates 0 for the experts token t does not select, so their neurons add exactly
+// nothing to the down projection. The same expression and rounding as the grouped
+// gate/up epilogue (the reference's fused expert kernel,
+// src/tl_kernel_optimized_Ultimate_PanGU.py:316-321: silu(acc_gate) * acc_up * weight,
+// then bf16). Eight neurons per thread (one expert: G % 8 == 0), 16-byte loads and
+// stores; HBM-bound: 10 bytes per (token, neuron).
+__global__ __launch_bounds__(256) void swiglu_gate_kernel(const float* __restrict__ g, const float* __restrict__ u,
+                                                          const float* __restrict__ gates, int64_t n, int E,
+                                                          int G, bf16_t* __restrict__ act) {
+  const int I = E * G, IC = I >> 3;
+  const int64_t total = n * IC;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+    const int64_t t = i / IC;
+    const int c = (int)(i - t * IC);
+    const float gt = gates[t * E + (c * 8) / G];
+    const float4* gp = (const float4*)(g + t * I + c * 8);
+    const float4* up = (const float4*)(u + t * I + c * 8);
+    const float4 g0 = gp[0], g1 = gp[1], u0 = up[0], u1 = up[1];
+    const float gv[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+    const float uv[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+    uint32_t w[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t lo = f32_to_bf16(pp_silu(gv[2 * q]) * uv[2 * q] * gt);
+      const uint32_t hi = f32_to_bf16(pp_silu(gv[2 * q + 1]) * uv[2 * q + 1] * gt);
+      w[q] = lo | (hi << 16);
+    }
+    *(uint4*)(act + t * I + c * 8) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
+extern "C" int pp_swiglu_gate(const float* gate_f32, const float* up_f32, const float* gates, int64_t n_tokens,
+                              int E, int G, void* act_bf16, void* stream) {
+  PP_REQUIRE(E >= 1 && E <= PP_MAX_EXPERTS, PP_ERR_UNSUPPORTED, "pp_swiglu_gate: E=%d unsupported (1..256)", E);
+  PP_REQUIRE(G >= 32 && G % 32 == 0 && G <= 8192, PP_ERR_UNSUPPORTED,
+             "pp_swiglu_gate: G=%d unsupported (G %% 32 == 0, 32 <= G <= 8192)", G);
+  PP_REQUIRE(n_tokens >= 0 && n_tokens <= ((int64_t)1 << 40) / ((int64_t)E * G), PP_ERR_INVALID,
+             "pp_swiglu_gate: n_tokens %lld out of range", (long long)n_tokens);
+  if (n_tokens == 0) return PP_OK;
+  PP_REQUIRE(gate_f32 && up_f32 && gates && act_bf16, PP_ERR_INVALID, "pp_swiglu_gate: null pointer");
+  PP_REQUIRE((((uintptr_t)gate_f32 | (uintptr_t)up_f32 | (uintptr_t)act_bf16) & 15) == 0, PP_ERR_INVALID,
+             "pp_swiglu_gate: gate, up and act must be 16-byte aligned");
+  const int64_t total = n_tokens * ((int64_t)E * G / 8);
+  const int64_t blocks = std::min<int64_t>((total + 255) / 256, (int64_t)pp_device_cus() * 16);
+  swiglu_gate_kernel<<<(unsigned)blocks, 256, 0, (hipStream_t)stream>>>(gate_f32, up_f32, gates, n_tokens, E, G,
+                                                                        (bf16_t*)act_bf16);
+  return pp_check_launch("pp_swiglu_gate");
 }
 
 // ------------------------------------------------------------------ whole prefill

@@ -18,6 +18,7 @@
 //                         tokens (the reference takes it for every N > 1, :606-615)
 //   moe_prefill(_into)    TauSparseMoE.forward_prefill (:532-604)
 #include <ATen/ATen.h>
+#include <algorithm>
 #include <c10/core/DeviceGuard.h>
 #include <c10/hip/HIPStream.h>
 #include <ATen/core/dispatch/Dispatcher.h>
@@ -343,6 +344,70 @@ void moe_decode_batch_into_meta(const Tensor&, const Tensor&, const optional<Ten
                                 const optional<Tensor>&, int64_t) {}
 
 // ------------------------------------------------------------------ prefill
+// Dense form, for G % 64 != 0 (the checkpoint's E = 192, G = 32), where the grouped
+// GEMMs have no MFMA tiling and each selected pair's down projection would be a K = G
+// GEMM writing a full fp32 row of H: per chunk of tokens, the router (pp_route: bit-exact
+// selection, gates 0 where not selected), gate and up of every neuron as two library
+// GEMMs with fp32 results (bf16 x and weights, the packed records read in place: rows
+// 3H apart), pp_swiglu_gate (the grouped gate/up epilogue's expression and rounding),
+// then the down GEMM over all neurons (fp32 result, rounded to bf16 once). The
+// unselected experts' neurons carry act 0 and add exactly nothing. Every intermediate
+// lives in the caller's workspace (pp_prefill_workspace_bytes, at least ~70 KB per
+// token here), chunked to fit it.
+void prefill_dense(const Tensor& x, const Tensor& router_packed, const optional<Tensor>& bias, int64_t E,
+                   int64_t G, double tau, const Tensor& packed, const Tensor& workspace, const Tensor& out) {
+  const int64_t N = x.size(0), H = x.size(1), I = E * G;
+  TORCH_CHECK(x.is_contiguous() && out.is_contiguous() && packed.is_contiguous(),
+              "prunepath.moe_prefill: x, out and packed must be contiguous");
+  TORCH_CHECK(packed.numel() >= 3 * I * H, "prunepath.moe_prefill: packed expert buffer too small");
+  if (N == 0) return;
+  const auto fopt = x.options().dtype(at::kFloat), bopt = x.options().dtype(at::kBFloat16);
+  const Tensor rec = packed.narrow(0, 0, 3 * I * H).view({I, 3, H});
+  const Tensor wg = rec.select(1, 0), wu = rec.select(1, 1), wd = rec.select(1, 2);  // [I, H], rows 3H apart
+  auto up256 = [](int64_t b) { return (b + 255) & ~(int64_t)255; };
+  // bytes per token: logits, probs, gates, mask, count; gate, up (fp32), act, x (bf16); out fp32
+  const int64_t per_tok = up256(E * 4) * 3 + up256(E) + 256 + I * 4 * 2 + I * 2 + H * 2 + H * 4;
+  const int64_t nc = std::min<int64_t>(N, (workspace.numel() - 16 * 256) / per_tok);
+  TORCH_CHECK(nc >= 1, "prunepath.moe_prefill: workspace too small for the dense form");
+  uint8_t* base = workspace.data_ptr<uint8_t>();
+  const Tensor out2 = out.view({N, H});
+  for (int64_t t0 = 0; t0 < N; t0 += nc) {
+    const int64_t n = std::min(nc, N - t0);
+    int64_t off = 0;
+    auto carve = [&](int64_t bytes) {
+      void* p = base + off;
+      off += up256(bytes);
+      return p;
+    };
+    float* logits = (float*)carve(n * E * 4);
+    float* probs = (float*)carve(n * E * 4);
+    float* gates = (float*)carve(n * E * 4);
+    uint8_t* mask = (uint8_t*)carve(n * E);
+    int32_t* count = (int32_t*)carve(n * 4);
+    const Tensor xc = x.narrow(0, t0, n);
+    check_rc(pp_route(xc.data_ptr(), x_code(x, "moe_prefill"), n, (int)H, router_packed.data_ptr<float>(),
+                      (const float*)ptr(bias), (int)E, (float)tau, logits, probs, gates, mask, count, stream_of(x)),
+             "moe_prefill (route)");
+    Tensor gt = at::from_blob(carve(n * I * 4), {n, I}, fopt);
+    Tensor ut = at::from_blob(carve(n * I * 4), {n, I}, fopt);
+    Tensor act = at::from_blob(carve(n * I * 2), {n, I}, bopt);
+    Tensor xb = xc;
+    if (x.scalar_type() != at::kBFloat16) {
+      xb = at::from_blob(carve(n * H * 2), {n, H}, bopt);
+      xb.copy_(xc);
+    }
+    Tensor o32 = at::from_blob(carve(n * H * 4), {n, H}, fopt);
+    TORCH_CHECK(off <= workspace.numel(), "prunepath.moe_prefill: dense workspace overrun");
+    at::mm_out(gt, xb, wg.t(), at::kFloat);
+    at::mm_out(ut, xb, wu.t(), at::kFloat);
+    check_rc(pp_swiglu_gate(gt.data_ptr<float>(), ut.data_ptr<float>(), gates, n, (int)E, (int)G, act.data_ptr(),
+                            stream_of(x)),
+             "moe_prefill (swiglu)");
+    at::mm_out(o32, act, wd, at::kFloat);
+    out2.narrow(0, t0, n).copy_(o32);
+  }
+}
+
 void prefill_into(const Tensor& x, const Tensor& router_packed, const optional<Tensor>& bias, int64_t E, int64_t G,
                   double tau, const Tensor& packed, const Tensor& workspace, const Tensor& out) {
   TORCH_CHECK(x.dim() == 2, "prunepath.moe_prefill: x must be [N, H]");
@@ -355,6 +420,10 @@ void prefill_into(const Tensor& x, const Tensor& router_packed, const optional<T
   need_gpu("moe_prefill", x,
            {&x, &router_packed, bias.has_value() ? &*bias : nullptr, &packed, &workspace, &out});
   const c10::DeviceGuard g(x.device());
+  if (G % 64 != 0) {
+    prefill_dense(x, router_packed, bias, E, G, tau, packed, workspace, out);
+    return;
+  }
   check_rc(pp_moe_prefill(x.data_ptr(), x_code(x, "moe_prefill"), N, (int)H, router_packed.data_ptr<float>(),
                           (const float*)ptr(bias), (int)E, (int)G, (float)tau, packed.data_ptr(), out.data_ptr(),
                           workspace.data_ptr(), stream_of(x)),

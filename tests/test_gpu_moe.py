@@ -205,22 +205,45 @@ def test_prefill_stages_vs_oracle(pkg):
 
 
 def test_prefill_in_passes_e192(pkg):
-    """A prefill longer than one pass (the worst-case pair buffers of a pass are bounded:
-    455 tokens a pass at E = 192, H = 1536), here 1000 tokens in three passes on a
-    workspace sized for one: every row vs the float64 reference, selection bit-exact, and
-    the output identical to the same tokens run as separate calls."""
-    E, G, N = 192, 32, 1000
-    assert pkg.ops.prefill_workspace_bytes(N, 1536, E, G) == pkg.ops.prefill_workspace_bytes(455, 1536, E, G)
+    """E = 192, G = 32, 1000 tokens, on both prefill forms:
+    * the C ABI's pp_moe_prefill (the grouped pipeline; its worst-case pair buffers are
+      bounded: 455 tokens a pass at H = 1536) in three passes on a workspace sized for one:
+      every row vs the float64 reference, selection bit-exact, and the output identical to
+      the same tokens run as separate calls;
+    * the module (torch op prunepath::moe_prefill, the dense form at G % 64 != 0: library
+      GEMMs around pp_swiglu_gate): every row vs the same reference, and repeated calls
+      identical. (Its rows are not bit-identical across calls of different token counts:
+      the library picks its GEMM kernel by the row count.)"""
+    import ctypes
+    E, G, N, H = 192, 32, 1000, 1536
+    assert pkg.ops.prefill_workspace_bytes(N, H, E, G) == pkg.ops.prefill_workspace_bytes(455, H, E, G)
     w = gi.layer_weights(41, E=E)
     m = make_module(pkg, w, 0.7)
     x = gi.tokens(42, N)
-    out = m(to_gpu(x[None])).float().cpu().numpy()[0]
-    res = pkg.ops.route(to_gpu(x), m.router_packed, E, 0.7)
+    xg = to_gpu(x)
+    res = pkg.ops.route(xg, m.router_packed, E, 0.7)
     sel = oracle.select(res["logits"].cpu().numpy(), 0.7)
     np.testing.assert_array_equal(res["mask"].cpu().numpy(), sel.mask)
-    assert_close(out, sparse_expected_gpu(x, w, sel.gates), what="E=192 prefill in passes")
-    parts = [m(to_gpu(x[None, a:b])).float().cpu().numpy()[0] for a, b in ((0, 455), (455, 910), (910, N))]
+    expected = sparse_expected_gpu(x, w, sel.gates)
+    lib = pkg._lib.lib()
+    vp = lambda t: ctypes.c_void_p(t.data_ptr() if t is not None else 0)  # noqa: E731
+
+    def abi(xs):
+        n = xs.shape[0]
+        y = torch.empty(n, H, dtype=torch.bfloat16, device=xs.device)
+        ws = torch.empty(pkg.ops.prefill_workspace_bytes(n, H, E, G), dtype=torch.uint8, device=xs.device)
+        pkg._lib.check(lib.pp_moe_prefill(vp(xs), 0, n, H, vp(m.router_packed), vp(None), E, G, ctypes.c_float(0.7),
+                                          vp(m.packed_experts), vp(y), vp(ws),
+                                          ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)), "moe_prefill")
+        return y.float().cpu().numpy()
+
+    out = abi(xg)
+    assert_close(out, expected, what="E=192 prefill in passes (C ABI, grouped pipeline)")
+    parts = [abi(xg[a:b].contiguous()) for a, b in ((0, 455), (455, 910), (910, N))]
     np.testing.assert_array_equal(np.concatenate(parts), out)
+    outm = m(xg[None]).float().cpu().numpy()[0]
+    assert_close(outm, expected, what="E=192 prefill (module, dense form)")
+    np.testing.assert_array_equal(m(xg[None]).float().cpu().numpy()[0], outm)
 
 
 def test_real_checkpoint_shape_e192_g32(pkg):
@@ -449,3 +472,30 @@ def test_decode_top_expert_speculation(pkg, tau, want):
         assert sel.ranked[0, :sel.count[0]].tolist() == want
         sp = sparse_expected(x[None], wts, sel.gates)[0]
         assert_close(out.float().cpu().numpy().reshape(-1), sp, what=f"speculation tau={tau}")
+
+
+@pytest.mark.gpu
+def test_swiglu_gate_abi(pkg):
+    """pp_swiglu_gate (the dense prefill form's SwiGLU with the expert gating) through the C
+    ABI against a torch float32 restatement, act = bf16(silu(g) * u * gates[t, n // G]):
+    within one bf16 step (the kernel's silu uses the fast exp, so the value before the
+    rounding differs by a few fp32 ulps), and exactly 0 where the expert is not selected."""
+    import ctypes
+    lib = pkg._lib.lib()
+    n, E, G = 37, 12, 32
+    I = E * G
+    gen = torch.Generator(device="cuda").manual_seed(3)
+    g = torch.randn(n, I, device="cuda", generator=gen) * 3
+    u = torch.randn(n, I, device="cuda", generator=gen)
+    gates = torch.rand(n, E, device="cuda", generator=gen)
+    gates[gates < 0.5] = 0
+    act = torch.empty(n, I, dtype=torch.bfloat16, device="cuda")
+    vp = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    pkg._lib.check(lib.pp_swiglu_gate(vp(g), vp(u), vp(gates), n, E, G, vp(act),
+                                      ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)), "swiglu_gate")
+    gfull = gates.repeat_interleave(G, dim=1)
+    ref = torch.nn.functional.silu(g) * u * gfull
+    a = act.float()
+    assert torch.allclose(a, ref, rtol=2.0 ** -7, atol=1e-30)
+    assert bool((a[gfull == 0] == 0).all())
+    assert bool((a[gfull != 0] == ref[gfull != 0].to(torch.bfloat16).float()).float().mean() > 0.99)
