@@ -36,7 +36,7 @@ __device__ __forceinline__ float4 load_x4<bf16_t>(const bf16_t* x, int64_t off) 
                      __uint_as_float(u.y << 16), __uint_as_float(u.y & 0xffff0000u));
 }
 
-template <typename XT, bool FROM_LOGITS>
+template <typename XT, bool FROM_LOGITS, bool SELECT = true>
 __global__ __launch_bounds__(256) void route_kernel(
     const XT* __restrict__ x, const float* __restrict__ logits_in, int64_t N, int H,
     const float* __restrict__ router, const float* __restrict__ bias, int E, float tau,
@@ -59,7 +59,10 @@ __global__ __launch_bounds__(256) void route_kernel(
     const int64_t t = tok0 + r;
     const bool valid = t < N;
     const int ntile = (E + 15) / 16;
-    for (int tg = 0; tg < ntile; tg += 4) {
+    // logits-only launches give each group of 64 experts its own workgroup (blockIdx.y)
+    const int tg_lo = SELECT ? 0 : 4 * (int)blockIdx.y;
+    const int tg_hi = SELECT ? ntile : min(ntile, tg_lo + 4);
+    for (int tg = tg_lo; tg < tg_hi; tg += 4) {
       f32x4_t acc[4];
 #pragma unroll
       for (int u = 0; u < 4; ++u) acc[u] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
@@ -100,6 +103,14 @@ __global__ __launch_bounds__(256) void route_kernel(
     }
   }
   __syncthreads();
+  if (!SELECT) {  // logits only, of this workgroup's 64 experts (the selection runs elsewhere)
+    for (int i = tid; i < ROUTE_TOK * ROUTE_EGRP; i += 256) {
+      const int rr = i / ROUTE_EGRP, e = 64 * (int)blockIdx.y + i % ROUTE_EGRP;
+      const int64_t t = tok0 + rr;
+      if (t < N && e < E) logits_out[t * E + e] = lg_s[rr][e];
+    }
+    return;
+  }
 
   // selection: wave w takes tokens 4w .. 4w+3
   SelScratch* ss = ssw + w;
@@ -124,6 +135,47 @@ __global__ __launch_bounds__(256) void route_kernel(
     if (lane == 0 && count_out) count_out[t] = k;
     wave_sync_lds();
   }
+}
+
+// Selection for E > 64, one token per workgroup of 256 threads: the workgroup selection
+// of the E > 16 decode (select_one_token_wg: keys sorted per wave, ranks by merging,
+// parallel exact cut; the same result as select_one_token, pinned on the same golden
+// families), about 3 us per token where one wave ranking E = 192 experts alone takes
+// tens of us. Reads the token's logits (bias already added), writes probs, gates, mask
+// and count. A selection whose ranks are not a permutation (never, for a correct sort)
+// writes NaN probs and gates and count 0 rather than a plausible wrong routing.
+__global__ __launch_bounds__(256) void route_select_wg_kernel(const float* __restrict__ logits, int64_t N, int E,
+                                                              float tau, float* __restrict__ logits_copy,
+                                                              float* __restrict__ probs_out,
+                                                              float* __restrict__ gates_out,
+                                                              uint8_t* __restrict__ mask_out,
+                                                              int32_t* __restrict__ count_out) {
+  __shared__ SelScratch ss;
+  __shared__ unsigned long long keys_s[PP_MAX_EXPERTS];
+  __shared__ float lg_s[PP_MAX_EXPERTS];
+  __shared__ float red_s[4];
+  const int tid = threadIdx.x;
+  const int64_t t = blockIdx.x;
+  if (t >= N) return;  // uniform
+  if (tid < E) {
+    lg_s[tid] = logits[t * E + tid];
+    if (logits_copy) logits_copy[t * E + tid] = lg_s[tid];
+  }
+  __syncthreads();
+  select_one_token_wg([&](int j) { return lg_s[j]; }, E, tau, &ss, keys_s, red_s, tid, 256);
+  const bool bad = ss.bad != 0;
+  const int k = bad ? 0 : ss.k;
+  if (tid < E) ss.sel[tid] = 0;
+  __syncthreads();
+  if (tid < k) ss.sel[ss.order[tid]] = 1;
+  __syncthreads();
+  if (tid < E) {
+    const bool s = ss.sel[tid] != 0;
+    if (probs_out) probs_out[t * E + tid] = bad ? __builtin_nanf("") : ss.e[tid];
+    if (gates_out) gates_out[t * E + tid] = bad ? __builtin_nanf("") : (s ? pp_sigmoid(lg_s[tid]) : 0.0f);
+    if (mask_out) mask_out[t * E + tid] = (uint8_t)s;
+  }
+  if (tid == 0 && count_out) count_out[t] = k;
 }
 
 // ------------------------------------------------------------------ E = 16 fast path
@@ -511,6 +563,31 @@ int pp_route_impl(const void* x, int x_dtype, const float* logits_in, int64_t N,
                                                              logits_out, probs_out, gates_out, mask_out,
                                                              count_out, xbf_out, blkcnt_out);
     return pp_check_launch("route16_kernel");
+  }
+  if (E > 64 && (logits_in || logits_out)) {  // logits, then one token per workgroup
+    if (!logits_in) {
+      if (x_dtype == PP_DTYPE_F32)
+        route_kernel<float, false, false><<<dim3(grid, (E + 63) / 64), threads, smem, st>>>((const float*)x, nullptr, N, H, router, bias,
+                                                                      E, tau, logits_out, nullptr, nullptr,
+                                                                      nullptr, nullptr, xbf_out);
+      else
+        route_kernel<bf16_t, false, false><<<dim3(grid, (E + 63) / 64), threads, smem, st>>>((const bf16_t*)x, nullptr, N, H, router,
+                                                                       bias, E, tau, logits_out, nullptr, nullptr,
+                                                                       nullptr, nullptr, xbf_out);
+      int rc = pp_check_launch("route_kernel (logits)");
+      if (rc) return rc;
+    }
+    const float* lg = logits_in ? logits_in : logits_out;
+    float* lcopy = (logits_in && logits_out && logits_out != logits_in) ? logits_out : nullptr;
+    for (int64_t t0 = 0; t0 < N; t0 += 65535) {
+      const int64_t n = N - t0 < 65535 ? N - t0 : 65535;
+      route_select_wg_kernel<<<(unsigned)n, 256, 0, st>>>(lg + t0 * E, n, E, tau, lcopy ? lcopy + t0 * E : nullptr,
+                                                          probs_out ? probs_out + t0 * E : nullptr,
+                                                          gates_out ? gates_out + t0 * E : nullptr,
+                                                          mask_out ? mask_out + t0 * E : nullptr,
+                                                          count_out ? count_out + t0 : nullptr);
+    }
+    return pp_check_launch("route_select_wg_kernel");
   }
   if (logits_in) {
     route_kernel<float, true><<<grid, threads, smem, st>>>(nullptr, logits_in, N, H, router, bias, E, tau,
