@@ -1072,7 +1072,7 @@ int pp_bucket_impl(const uint8_t* mask, const float* gates, int64_t N, int E, in
 
 struct PrefillWs {
   size_t gates, mask, count, offsets, token_ids, pair_gates, token_pairs, tiles, meta, bws, blk16, xbf, act, y,
-      gws, total;
+      gws, logits, total;
 };
 
 static PrefillWs prefill_layout(int64_t N, int H, int E, int G) {
@@ -1100,6 +1100,7 @@ static PrefillWs prefill_layout(int64_t N, int H, int E, int G) {
   L.act = take((size_t)P * G * 2);
   L.y = take((size_t)P * H * 4);
   L.gws = prefill_short_tiles(N, H, G) ? take(gemm_split_bytes()) : 0;
+  L.logits = E > 64 ? take((size_t)P * 4) : 0;  // the E > 64 router's logits (selection by workgroup)
   L.total = o;
   return L;
 }
@@ -1149,7 +1150,8 @@ static int prefill_pass(const void* x, int x_dtype, int64_t n_tokens, int H, con
   // bucketing is one kernel from those counts (no counting or scan pass)
   const int cb = pp_route_count_block(n_tokens, H, E);
   int32_t* blk16 = pp_bucket_counts_fit(n_tokens, E, cb) ? (int32_t*)(ws + L.blk16) : nullptr;
-  if ((rc = pp_route_impl(x, x_dtype, nullptr, n_tokens, H, router_packed, bias, E, tau, nullptr, nullptr, gates,
+  if ((rc = pp_route_impl(x, x_dtype, nullptr, n_tokens, H, router_packed, bias, E, tau,
+                          E > 64 ? (float*)(ws + L.logits) : nullptr, nullptr, gates,
                           mask, count, x_dtype == PP_DTYPE_BF16 ? nullptr : xbf, st, blk16)))
     return rc;
   if (blk16)
