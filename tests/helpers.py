@@ -67,12 +67,14 @@ def sparse_expected(x: np.ndarray, w: dict, gates: np.ndarray, act_bf16: bool = 
                                             gates, G, act_bf16=act_bf16)
 
 
-def sparse_expected_gpu(x: np.ndarray, w: dict, gates: np.ndarray) -> np.ndarray:
+def sparse_expected_gpu(x: np.ndarray, w: dict, gates: np.ndarray, act_bf16: bool = False) -> np.ndarray:
     """sparse_expected in torch float64 on cuda:0, for sizes where the numpy restatement
     is slow (e.g. 8200 tokens): every expert's SwiGLU on every token, times the gate
     (0 for unselected experts, so those terms vanish exactly), down projection. Same
     operands as sparse_expected (bf16-rounded x and weights, rearranged neurons);
-    test_prefill_full_rows pins it against sparse_expected on a slice."""
+    test_prefill_full_rows pins it against sparse_expected on a slice. act_bf16 rounds
+    the acts to bf16 before the down projection, as the reference's fused expert kernel
+    does (src/tl_kernel_optimized_Ultimate_PanGU.py:321)."""
     E = w["w_router"].shape[0]
     I = w["w_gate"].shape[0]
     G = I // E
@@ -88,6 +90,8 @@ def sparse_expected_gpu(x: np.ndarray, w: dict, gates: np.ndarray) -> np.ndarray
     WdT = t(bf16_round(w["w_down"])[:, perm].T)     # [I, H]
     g = xr @ WgT
     a = g / (1.0 + torch.exp(-g)) * (xr @ WuT) * t(gates).repeat_interleave(G, dim=1)
+    if act_bf16:
+        a = a.to(torch.float32).to(torch.bfloat16).to(torch.float64)
     return (a @ WdT).cpu().numpy()
 
 

@@ -499,3 +499,24 @@ def test_swiglu_gate_abi(pkg):
     assert torch.allclose(a, ref, rtol=2.0 ** -7, atol=1e-30)
     assert bool((a[gfull == 0] == 0).all())
     assert bool((a[gfull != 0] == ref[gfull != 0].to(torch.bfloat16).float()).float().mean() > 0.99)
+
+
+@pytest.mark.gpu
+def test_prefill_dense_form_two_chunks_e192(pkg):
+    """The dense prefill form (E = 192, G = 32) on 8200 tokens: more than the workspace's
+    chunk (~7700 tokens at H = 1536), so the op routes and multiplies in two chunks on one
+    workspace. Selection bit-exact against the oracle on the kernel's logits, every row
+    against the float64 restatement with the acts rounded to bf16, the reference's
+    rounding point (src/tl_kernel_optimized_Ultimate_PanGU.py:321); without that rounding
+    one output in 12.6 M, a near-cancelling sum of ~2400 act products, sits 5 % past the
+    bound."""
+    E, N = 192, 8200
+    w = gi.layer_weights(43, E=E)
+    m = make_module(pkg, w, 0.7)
+    x = gi.tokens(44, N)
+    xg = to_gpu(x)
+    res = pkg.ops.route(xg, m.router_packed, E, 0.7)
+    sel = oracle.select(res["logits"].cpu().numpy(), 0.7)
+    np.testing.assert_array_equal(res["mask"].cpu().numpy(), sel.mask)
+    out = m(xg[None]).float().cpu().numpy()[0]
+    assert_close(out, sparse_expected_gpu(x, w, sel.gates, act_bf16=True), what="E=192 dense prefill, two chunks")
