@@ -11,9 +11,12 @@ atol 2e-3) with the selection bit-exact against the oracle on the kernel's own l
   G > 512 or E * G > 8192; local and published logits, eight waves for H <= 2560 and
   four above);
 * prefill routing: route16_few_kernel (E = 16, N <= 64, H % 512 == 0, H <= 2048),
-  route16_kernel (other E = 16 cases) and route_kernel (E != 16);
+  route16_kernel (other E = 16 cases), route_kernel (E != 16, E <= 64) and, for E > 64,
+  route_kernel's split logits launch with route_select_wg_kernel;
 * prefill GEMMs: gemm_s_kernel (N <= 64, G % 64 == 0, H >= 384), gemm_v3_kernel
-  (G % 64 == 0 otherwise) and gateup_kernel / down_kernel (G % 64 == 32);
+  (G % 64 == 0 otherwise); at G % 64 != 0 the torch op's dense form (library GEMMs around
+  swiglu_gate_kernel) and, through the C ABI's pp_moe_prefill, gateup_kernel /
+  down_kernel;
 * the limits: H = 128 and 4096, E = 1 and 256, G = 32 and 8192, tau above 1 (every
   expert selected) and 0 (rank 0 only), bf16 and fp32 x; a router bias (log Zipf) on
   every router variant;
@@ -39,7 +42,9 @@ CASES = [
     (2048, 16, 1024, 1, 0.7, torch.float32, True),     # E = 16 with G > 512: decode_kernel (local logits)
     (4096, 16, 128, 40, 0.5, torch.bfloat16, False),   # H > 2048: route16 at N <= 64; short tiles
     (2048, 16, 64, 64, 0.95, torch.float32, True),     # route16_few at CPL = 4 with a bias; short tiles at N = 64
-    (1024, 8, 96, 33, 0.9, torch.float32, False),      # route_kernel (E = 8); gateup/down kernels (G = 96)
+    (1024, 8, 96, 33, 0.9, torch.float32, False),      # route_kernel (E = 8); dense form / gateup/down kernels (G = 96)
+    (512, 96, 32, 20, 0.7, torch.bfloat16, True),      # E = 96: split logits (a partial second group) and the
+                                                       # workgroup selection; dense form with bf16 x; bias
     (1024, 8, 96, 1, 0.9, torch.bfloat16, True),       # decode2p with local logits, E = 8, bf16 x, bias
     (512, 256, 32, 5, 0.7, torch.float32, False),      # E = 256
     (512, 256, 32, 1, 0.7, torch.float32, True),       # decode2p with E = 256 (published logits, E * G at 8192), bias
@@ -90,6 +95,17 @@ def test_layer_shape_vs_oracle(pkg, H, E, G, N, tau, xdt, with_bias):
                                          m.packed_experts).float().cpu().numpy()
         out = pf()
     assert_close(out, expected, what=f"layer H={H} E={E} G={G} N={N}")
+    if N > 1 and G % 64 != 0:  # the torch op took the dense form: the grouped pipeline through the C ABI
+        import ctypes
+        lib = pkg._lib.lib()
+        y = torch.empty(N, H, dtype=torch.bfloat16, device=xg.device)
+        ws = torch.empty(pkg.ops.prefill_workspace_bytes(N, H, E, G), dtype=torch.uint8, device=xg.device)
+        vp = lambda t: ctypes.c_void_p(t.data_ptr() if t is not None else 0)  # noqa: E731
+        pkg._lib.check(lib.pp_moe_prefill(vp(xg), 0 if xdt == torch.float32 else 1, N, H, vp(m.router_packed),
+                                          vp(m.router_bias), E, G, ctypes.c_float(tau), vp(m.packed_experts),
+                                          vp(y), vp(ws), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)),
+                       "moe_prefill")
+        assert_close(y.float().cpu().numpy(), expected, what=f"grouped pipeline H={H} E={E} G={G} N={N}")
     out2 = m(xg[None]).float().cpu().numpy()[0] if N == 1 else pf()
     np.testing.assert_array_equal(out2, out)  # prefill and decode are deterministic bit for bit
     if N > 1 and pkg.ops.decode_batch_supported(N, H, E, G):  # the one-launch batch kernel (module path)
