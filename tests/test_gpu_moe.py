@@ -257,8 +257,9 @@ def test_real_checkpoint_shape_e192_g32(pkg):
     res = pkg.ops.route(to_gpu(x), m.router_packed, 192, 0.7)
     sel = oracle.select(res["logits"].cpu().numpy(), 0.7)
     np.testing.assert_array_equal(res["mask"].cpu().numpy(), sel.mask)
+    assert_close(out, sparse_expected_gpu(x, w, sel.gates), what="E=192 prefill, every row")
     rows = np.arange(0, 96, 6)
-    assert_close(out[rows], sparse_expected(x[rows], w, sel.gates[rows]), what="E=192 prefill")
+    assert_close(out[rows], sparse_expected(x[rows], w, sel.gates[rows]), what="E=192 prefill (numpy fp64 rows)")
     od = m(to_gpu(x[None, :1])).float().cpu().numpy()[0, 0]
     st = pkg.ops.decode_state(m.decode_workspace, 192)
     assert st["error"] == 0
