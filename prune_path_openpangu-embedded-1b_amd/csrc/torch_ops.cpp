@@ -365,8 +365,9 @@ void prefill_dense(const Tensor& x, const Tensor& router_packed, const optional<
   const Tensor rec = packed.narrow(0, 0, 3 * I * H).view({I, 3, H});
   const Tensor wg = rec.select(1, 0), wu = rec.select(1, 1), wd = rec.select(1, 2);  // [I, H], rows 3H apart
   auto up256 = [](int64_t b) { return (b + 255) & ~(int64_t)255; };
-  // bytes per token: logits, probs, gates, mask, count; gate, up (fp32), act, x (bf16); out fp32
-  const int64_t per_tok = up256(E * 4) * 3 + up256(E) + 256 + I * 4 * 2 + I * 2 + H * 2 + H * 4;
+  // bytes per token: logits, probs, gates, mask, count; x (fp32, for the router GEMM);
+  // gate, up (fp32), act, x (bf16); out fp32
+  const int64_t per_tok = up256(E * 4) * 3 + up256(E) + 256 + H * 4 + I * 4 * 2 + I * 2 + H * 2 + H * 4;
   const int64_t nc = std::min<int64_t>(N, (workspace.numel() - 16 * 256) / per_tok);
   TORCH_CHECK(nc >= 1, "prunepath.moe_prefill: workspace too small for the dense form");
   uint8_t* base = workspace.data_ptr<uint8_t>();
@@ -385,9 +386,19 @@ void prefill_dense(const Tensor& x, const Tensor& router_packed, const optional<
     uint8_t* mask = (uint8_t*)carve(n * E);
     int32_t* count = (int32_t*)carve(n * 4);
     const Tensor xc = x.narrow(0, t0, n);
-    check_rc(pp_route(xc.data_ptr(), x_code(x, "moe_prefill"), n, (int)H, router_packed.data_ptr<float>(),
-                      (const float*)ptr(bias), (int)E, (float)tau, logits, probs, gates, mask, count, stream_of(x)),
-             "moe_prefill (route)");
+    // router logits as one fp32 library GEMM (x fp32 [n, H] times the router's E rows),
+    // then the bias added to each sum, as the router kernel does; the selection from those
+    // logits is pp_route_logits (bit-exact against the reference's selection ops)
+    Tensor lg = at::from_blob(logits, {n, E}, fopt);
+    Tensor xf = xc;
+    if (x.scalar_type() != at::kFloat) {
+      xf = at::from_blob(carve(n * H * 4), {n, H}, fopt);
+      xf.copy_(xc);
+    }
+    at::mm_out(lg, xf, router_packed.narrow(0, 0, E).t());
+    if (bias.has_value()) lg.add_(*bias);
+    check_rc(pp_route_logits(logits, n, (int)E, (float)tau, probs, gates, mask, count, stream_of(x)),
+             "moe_prefill (route_logits)");
     Tensor gt = at::from_blob(carve(n * I * 4), {n, I}, fopt);
     Tensor ut = at::from_blob(carve(n * I * 4), {n, I}, fopt);
     Tensor act = at::from_blob(carve(n * I * 2), {n, I}, bopt);
