@@ -40,7 +40,7 @@ extern "C" {
 
 /* Message of the last error on this thread ("" if none). */
 const char* pp_last_error(void);
-/* ABI version (incremented on any signature change). */
+/* ABI version (incremented on any signature change): 2. */
 int pp_abi_version(void);
 
 /* ------------------------------------------------------------------------- *
@@ -208,20 +208,38 @@ int pp_moe_decode_batch(const void* x, int x_dtype, int64_t n_tokens, int H, con
                         int grid, void* stream);
 
 /* ------------------------------------------------------------------------- *
- * Prefill / N > 1: route -> bucket -> grouped gate/up GEMM with fused SwiGLU
- * epilogue (bf16 MFMA) -> grouped down GEMM -> per-token combine in fp32 -> bf16.
- * Replaces TauSparseMoE.forward_prefill (src/tl_kernel_optimized_Ultimate_PanGU.py:532-604)
- * and moe_fused_expert_kernel (:271-328). No host synchronisation.
- * workspace: pp_prefill_workspace_bytes(N, H, E, G) bytes of device scratch. The pair
- * buffers are sized for every token selecting every expert, so the call runs in
- * consecutive passes of at most max(64, 512 MiB / (E * H * 4)) tokens (2048 tokens in one
- * pass at E = 16, H = 1536; 455 a pass at E = 192) and the workspace stays bounded for
- * any N; the output is the same as one pass over all N.
+ * Prefill / N > 1. Replaces TauSparseMoE.forward_prefill
+ * (src/tl_kernel_optimized_Ultimate_PanGU.py:532-604) and moe_fused_expert_kernel (:271-328).
+ * No host synchronisation; hand-written kernels only. Two forms, by the expert width G:
+ *   G % 64 == 0: route -> bucket -> grouped gate/up GEMM with fused SwiGLU epilogue
+ *     (bf16 MFMA) -> grouped down GEMM -> per-token combine in fp32 -> bf16. The pair
+ *     buffers are sized for every token selecting every expert, so the call runs in
+ *     consecutive passes of at most max(64, 512 MiB / (E * H * 4)) tokens (2048 tokens in
+ *     one pass at E = 16, H = 1536).
+ *   G % 64 != 0 (e.g. the checkpoint's E = 192 experts of G = 32 neurons, narrower than an
+ *     MFMA column tile): router logits (fp32 MFMA, one fixed summation order per
+ *     (token, expert): a token routes the same way in any batch) -> selection -> dense
+ *     gate/up GEMM over every (token, neuron) with act = bf16(silu(g) * u * gate), 0 for the
+ *     experts a token does not select -> dense down GEMM over all neurons, fp32
+ *     accumulation, one rounding to bf16. Passes of up to ~256 MiB of per-token buffers
+ *     (about 15000 tokens at H = 1536, E = 192, G = 32).
+ * Either way the output is the same as one pass over all N, and the same bits on every
+ * call with the same N.
+ * workspace: pp_prefill_workspace_bytes(N, H, E, G) bytes of device scratch.
  * ------------------------------------------------------------------------- */
 size_t pp_prefill_workspace_bytes(int64_t n_tokens, int H, int E, int G);
 int pp_moe_prefill(const void* x, int x_dtype, int64_t n_tokens, int H,
                    const float* router_packed, const float* bias, int E, int G, float tau,
                    const void* packed, void* out_bf16, void* workspace, void* stream);
+/* pp_moe_prefill that also returns the routing it used: logits_out fp32 [N,E] (the
+ * router's logits, bias included) and mask_out uint8 [N,E] (4-byte aligned), each NULL =
+ * not written. The selection in mask_out is bit-exact with softmax_thresholding
+ * (src/MoEBlock_origin.py:50-97) applied to logits_out. Same reference interface as
+ * pp_moe_prefill (the reference's forward_prefill keeps its routing in locals, :550-564). */
+int pp_moe_prefill_routed(const void* x, int x_dtype, int64_t n_tokens, int H,
+                          const float* router_packed, const float* bias, int E, int G, float tau,
+                          const void* packed, void* out_bf16, void* workspace,
+                          float* logits_out, uint8_t* mask_out, void* stream);
 
 /* Stages of pp_moe_prefill, exposed for testing and for callers that route
  * elsewhere. x is bf16 [N,H]. act is bf16 [N*E][G] capacity (row = pair), y is
@@ -235,19 +253,6 @@ int pp_expert_down(const void* act_bf16, int H, int G, const void* packed, int E
                    float* y_f32, void* stream);
 int pp_combine(const float* y_f32, const int32_t* token_pairs, const int32_t* count,
                int64_t n_tokens, int H, int E, void* out_bf16, void* stream);
-
-/* SwiGLU with the expert gating for the dense prefill form, where the grouped GEMMs
- * have no MFMA tiling (G % 64 != 0, e.g. the checkpoint's E = 192, G = 32): the
- * torch.library op prunepath::moe_prefill computes gate and up of every neuron for
- * every token with library GEMMs (fp32 results), this, then one down GEMM over all
- * neurons. Replaces the epilogue of the reference's fused expert kernel
- * (src/tl_kernel_optimized_Ultimate_PanGU.py:316-321: silu(acc_gate) * acc_up * weight,
- * rounded to bf16), with the weight of an unselected expert 0:
- *   act[t, n] = bf16(silu(gate[t, n]) * up[t, n] * gates[t, n / G])
- * gate_f32, up_f32 fp32 [n_tokens, E*G]; gates fp32 [n_tokens, E] (the router's gates,
- * 0 where not selected); act_bf16 [n_tokens, E*G]. gate, up and act 16-byte aligned. */
-int pp_swiglu_gate(const float* gate_f32, const float* up_f32, const float* gates, int64_t n_tokens,
-                   int E, int G, void* act_bf16, void* stream);
 
 /* ------------------------------------------------------------------------- *
  * Masked training path: the expert gating of MoELayer.forward

@@ -58,12 +58,13 @@ SIGNATURES = {
     "pp_prefill_workspace_bytes": (c_size_t, [c_int64, c_int, c_int, c_int]),
     "pp_moe_prefill": (c_int, [c_void_p, c_int, c_int64, c_int, c_void_p, c_void_p, c_int, c_int, c_float,
                                c_void_p, c_void_p, c_void_p, c_void_p]),
+    "pp_moe_prefill_routed": (c_int, [c_void_p, c_int, c_int64, c_int, c_void_p, c_void_p, c_int, c_int, c_float,
+                                      c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "pp_expert_gateup": (c_int, [c_void_p, c_int, c_int, c_void_p, c_int, c_void_p, c_void_p, c_void_p,
                                  c_void_p, c_int64, c_void_p, c_void_p]),
     "pp_expert_down": (c_int, [c_void_p, c_int, c_int, c_void_p, c_int, c_void_p, c_void_p, c_int64,
                                c_void_p, c_void_p]),
     "pp_combine": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int, c_int, c_void_p, c_void_p]),
-    "pp_swiglu_gate": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int, c_int, c_void_p, c_void_p]),
     "pp_masked_gate_fwd": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_int64, c_int, c_int, c_void_p,
                                    c_void_p]),
     "pp_masked_gate_bwd": (c_int, [c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_int64,

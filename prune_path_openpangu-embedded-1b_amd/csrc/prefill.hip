@@ -294,46 +294,7 @@ __global__ __launch_bounds__(GM_THREADS, 2) void down_kernel(
 // | 9.5 -- the weights stream from HBM into LDS, so the bytes in flight per CU are capped
 // by LDS, ~5 MB over the chip where HBM needs ~16 MB; register-streamed loads (as in
 // decode) are what such batches need.
-typedef __attribute__((address_space(3))) void lds_void_t;
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ void gl2lds(const void* src, unsigned char* lds_base) {
-  __builtin_amdgcn_global_load_lds(src, (lds_void_t*)lds_base, 16, 0, 0);
-}
-
-template <int IMM>
-__device__ __forceinline__ u32x4 gv_read(uint32_t lds_addr) {
-  u32x4 v;
-  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(lds_addr), "i"(IMM));
-  return v;
-}
-
-// Wait until at most N LDS reads are outstanding; ties the four fragments of the
-// current k-step so that their MFMAs cannot be scheduled above the wait.
-template <int N>
-__device__ __forceinline__ void gv_wait(u32x4& a0, u32x4& a1, u32x4& b0, u32x4& b1) {
-  asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(a0), "+v"(a1), "+v"(b0), "+v"(b1) : "n"(N));
-}
-
-__device__ __forceinline__ f32x16_t mfma32v(u32x4 a, u32x4 b, f32x16_t c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c,
-                                                 0, 0, 0);
-}
-
-// Item order: workgroup b runs on XCD b % 8 (round-robin dispatch); XCD x takes the
-// contiguous item range [x * chunk, (x + 1) * chunk), so the column tiles of one row
-// tile, and the row tiles of one expert, share that XCD's L2. gridDim.x is a multiple
-// of 8.
-struct GvItems {
-  int first, last, step;
-  __device__ GvItems(int n_items) {
-    const int xcd = blockIdx.x & 7, per = gridDim.x >> 3;
-    const int chunk = (n_items + 7) >> 3;
-    first = xcd * chunk + (blockIdx.x >> 3);
-    last = min(n_items, (xcd + 1) * chunk);
-    step = per;
-  }
-};
+#include "gemm_lds.h"
 
 #define GP_BK 64         // K block (bf16 elements)
 #define GP_STAGES 2
@@ -352,78 +313,6 @@ struct GvItems {
 // chunk c of row r is stored at position c ^ gp_swz(r): any 16 consecutive rows of a
 // fragment read land in 16 distinct 16-byte slots of a 256-byte bank window
 __device__ __forceinline__ int gp_swz(int r) { return GP_BK == 64 ? (r >> 1) & 7 : (r >> 2) & 3; }
-
-__device__ __forceinline__ void gl2lds4(const void* src, unsigned char* lds_base) {
-  __builtin_amdgcn_global_load_lds(src, (lds_void_t*)lds_base, 4, 0, 0);
-}
-
-template <int N>
-__device__ __forceinline__ void gp_wait_barrier() {
-  asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(N) : "memory");
-}
-
-// ---- split items: the K blocks of an item shared by several workgroups
-// Schedule of both pipelined GEMMs (GpSched): rank q = XCD-major workgroup index (an
-// XCD's ranks are consecutive); full rounds of whole items first -- item r * grid + q in
-// round r, so the workgroups sharing a row tile or an expert's weights walk K in step --
-// then, with a split workspace, the tail items (n_items % grid) each cut into nparts K
-// ranges, one range per workgroup; the workgroups holding the parts of a tail item join
-// their fp32 partial sums (gp_join). Without a workspace: whole items, grid-strided.
-// Split workspace: sync words [0] (reserved), [1, 1 + grid) tickets (one per tail item),
-// then partial-sum slots of NF floats per thread, one slot per part (at most grid). The
-// tickets are zero at launch and every launch leaves them zero.
-#define GP_MIN_PART_BLOCKS 4  // a part shorter than this does not repay its join (measured)
-__device__ __forceinline__ void gp_st(uint32_t* p, uint32_t v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-struct GpSched {
-  int n_whole;       // whole local items
-  int first, step;   // whole local item li is first + li * step
-  int part_item;     // the tail item of this workgroup's part (-1: none)
-  int kb_lo, kb_hi;  // its K blocks
-  int unit, nparts;  // part index = unit % nparts
-  int tail0;         // first tail item
-  __device__ GpSched(int n_items, int nkb, bool can_split) {
-    const int g = gridDim.x, per = g >> 3;
-    const int rank = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
-    const int rounds = n_items / g, tail = n_items - rounds * g;
-    nparts = (can_split && tail > 0) ? max(1, min(nkb / GP_MIN_PART_BLOCKS, g / tail)) : 1;
-    part_item = -1;
-    kb_lo = kb_hi = 0;
-    unit = rank;
-    tail0 = rounds * g;
-    if (nparts > 1) {
-      n_whole = rounds;
-      first = rank;
-      step = g;
-      if (rank < tail * nparts) {
-        const int ti = rank / nparts, pi = rank - ti * nparts;
-        part_item = tail0 + ti;
-        kb_lo = pi * nkb / nparts;
-        kb_hi = (pi + 1) * nkb / nparts;
-      }
-    } else {
-      const GvItems it(n_items);
-      n_whole = it.first < it.last ? (it.last - it.first + it.step - 1) / it.step : 0;
-      first = it.first;
-      step = it.step;
-    }
-  }
-  __device__ int n_local() const { return n_whole + (part_item >= 0 ? 1 : 0); }
-  __device__ int item(int li) const { return li < n_whole ? first + li * step : part_item; }
-  __device__ int units(int nkb) const { return n_whole * nkb + (kb_hi - kb_lo); }
-  // local unit f -> (local item, K block)
-  __device__ void locate(int f, int nkb, int& li, int& kb) const {
-    if (f < n_whole * nkb) {
-      li = f / nkb;
-      kb = f - li * nkb;
-    } else {
-      li = n_whole;
-      kb = kb_lo + (f - n_whole * nkb);
-    }
-  }
-};
 
 // Join of a tail item's parts; every thread calls it, at the part's last K block. Every
 // part stores its partial sums (agent-scope stores), waits until they are performed,
@@ -1002,60 +891,6 @@ extern "C" int pp_combine(const float* y_f32, const int32_t* token_pairs, const 
   return combine_launch(y_f32, token_pairs, count, n_tokens, H, E, (bf16_t*)out_bf16, (hipStream_t)stream);
 }
 
-// ------------------------------------------------------------------ dense SwiGLU with expert gating
-// For the dense prefill form (gate and up of every neuron for every token, from two
-// library GEMMs with fp32 results; then one down GEMM over all neurons), used where the
-// grouped GEMMs have no MFMA tiling (G % 64 != 0, the checkpoint's E = 192, G = 32):
-//   act[t, n] = bf16(silu(g[t, n]) * u[t, n] * gates[t, n / G])
-// with gates 0 for the experts token t does not select, so their neurons add exactly
-// nothing to the down projection. The same expression and rounding as the grouped
-// gate/up epilogue (the reference's fused expert kernel,
-// src/tl_kernel_optimized_Ultimate_PanGU.py:316-321: silu(acc_gate) * acc_up * weight,
-// then bf16). Eight neurons per thread (one expert: G % 8 == 0), 16-byte loads and
-// stores; HBM-bound: 10 bytes per (token, neuron).
-__global__ __launch_bounds__(256) void swiglu_gate_kernel(const float* __restrict__ g, const float* __restrict__ u,
-                                                          const float* __restrict__ gates, int64_t n, int E,
-                                                          int G, bf16_t* __restrict__ act) {
-  const int I = E * G, IC = I >> 3;
-  const int64_t total = n * IC;
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
-    const int64_t t = i / IC;
-    const int c = (int)(i - t * IC);
-    const float gt = gates[t * E + (c * 8) / G];
-    const float4* gp = (const float4*)(g + t * I + c * 8);
-    const float4* up = (const float4*)(u + t * I + c * 8);
-    const float4 g0 = gp[0], g1 = gp[1], u0 = up[0], u1 = up[1];
-    const float gv[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
-    const float uv[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
-    uint32_t w[4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const uint32_t lo = f32_to_bf16(pp_silu(gv[2 * q]) * uv[2 * q] * gt);
-      const uint32_t hi = f32_to_bf16(pp_silu(gv[2 * q + 1]) * uv[2 * q + 1] * gt);
-      w[q] = lo | (hi << 16);
-    }
-    *(uint4*)(act + t * I + c * 8) = make_uint4(w[0], w[1], w[2], w[3]);
-  }
-}
-
-extern "C" int pp_swiglu_gate(const float* gate_f32, const float* up_f32, const float* gates, int64_t n_tokens,
-                              int E, int G, void* act_bf16, void* stream) {
-  PP_REQUIRE(E >= 1 && E <= PP_MAX_EXPERTS, PP_ERR_UNSUPPORTED, "pp_swiglu_gate: E=%d unsupported (1..256)", E);
-  PP_REQUIRE(G >= 32 && G % 32 == 0 && G <= 8192, PP_ERR_UNSUPPORTED,
-             "pp_swiglu_gate: G=%d unsupported (G %% 32 == 0, 32 <= G <= 8192)", G);
-  PP_REQUIRE(n_tokens >= 0 && n_tokens <= ((int64_t)1 << 40) / ((int64_t)E * G), PP_ERR_INVALID,
-             "pp_swiglu_gate: n_tokens %lld out of range", (long long)n_tokens);
-  if (n_tokens == 0) return PP_OK;
-  PP_REQUIRE(gate_f32 && up_f32 && gates && act_bf16, PP_ERR_INVALID, "pp_swiglu_gate: null pointer");
-  PP_REQUIRE((((uintptr_t)gate_f32 | (uintptr_t)up_f32 | (uintptr_t)act_bf16) & 15) == 0, PP_ERR_INVALID,
-             "pp_swiglu_gate: gate, up and act must be 16-byte aligned");
-  const int64_t total = n_tokens * ((int64_t)E * G / 8);
-  const int64_t blocks = std::min<int64_t>((total + 255) / 256, (int64_t)pp_device_cus() * 16);
-  swiglu_gate_kernel<<<(unsigned)blocks, 256, 0, (hipStream_t)stream>>>(gate_f32, up_f32, gates, n_tokens, E, G,
-                                                                        (bf16_t*)act_bf16);
-  return pp_check_launch("pp_swiglu_gate");
-}
-
 // ------------------------------------------------------------------ whole prefill
 int pp_route_impl(const void* x, int x_dtype, const float* logits_in, int64_t N, int H, const float* router,
                   const float* bias, int E, float tau, float* logits_out, float* probs_out, float* gates_out,
@@ -1100,7 +935,7 @@ static PrefillWs prefill_layout(int64_t N, int H, int E, int G) {
   L.act = take((size_t)P * G * 2);
   L.y = take((size_t)P * H * 4);
   L.gws = prefill_short_tiles(N, H, G) ? take(gemm_split_bytes()) : 0;
-  L.logits = E > 64 ? take((size_t)P * 4) : 0;  // the E > 64 router's logits (selection by workgroup)
+  L.logits = E != 16 ? take((size_t)P * 4) : 0;  // the logits pass of E != 16 (selection from its logits)
   L.total = o;
   return L;
 }
@@ -1114,22 +949,33 @@ static PrefillWs prefill_layout(int64_t N, int H, int E, int G) {
 #define PF_PASS_Y_BYTES ((int64_t)512 << 20)
 static int64_t prefill_pass_tokens(int64_t N, int H, int E) {
   const int64_t per_token = (int64_t)E * H * 4;
-  return min(N, max((int64_t)64, PF_PASS_Y_BYTES / per_token));
+  // a multiple of 4 tokens: every pass's mask rows start 4-byte aligned (the bucketing reads words)
+  return min(N, max((int64_t)64, PF_PASS_Y_BYTES / per_token / 4 * 4));
 }
 
+size_t pp_dense_workspace_bytes(int64_t N, int H, int E, int G);
+int pp_dense_prefill(const void* x, int x_dtype, int64_t N, int H, const float* router, const float* bias, int E,
+                     int G, float tau, const void* packed, void* out, void* workspace, hipStream_t st,
+                     float* logits_out, uint8_t* mask_out);
+
+// The dense form (dense.hip) serves the shapes whose experts are narrower than a 64-neuron
+// MFMA column tile; the grouped pipeline below the rest.
+static bool prefill_dense_form(int G) { return G % 64 != 0; }
+
 extern "C" size_t pp_prefill_workspace_bytes(int64_t n_tokens, int H, int E, int G) {
+  if (prefill_dense_form(G)) return pp_dense_workspace_bytes(n_tokens, H, E, G);
   return prefill_layout(prefill_pass_tokens(n_tokens, H, E), H, E, G).total;
 }
 
 // One pass over n_tokens tokens (at most prefill_pass_tokens) on the workspace.
 static int prefill_pass(const void* x, int x_dtype, int64_t n_tokens, int H, const float* router_packed,
                         const float* bias, int E, int G, float tau, const void* packed, void* out_bf16,
-                        void* workspace, hipStream_t st) {
+                        void* workspace, hipStream_t st, float* logits_out, uint8_t* mask_out) {
   int rc;
   const PrefillWs L = prefill_layout(n_tokens, H, E, G);
   char* ws = (char*)workspace;
   float* gates = (float*)(ws + L.gates);
-  uint8_t* mask = (uint8_t*)(ws + L.mask);
+  uint8_t* mask = mask_out ? mask_out : (uint8_t*)(ws + L.mask);
   int32_t* count = (int32_t*)(ws + L.count);
   int32_t* offsets = (int32_t*)(ws + L.offsets);
   int32_t* token_ids = (int32_t*)(ws + L.token_ids);
@@ -1151,7 +997,7 @@ static int prefill_pass(const void* x, int x_dtype, int64_t n_tokens, int H, con
   const int cb = pp_route_count_block(n_tokens, H, E);
   int32_t* blk16 = pp_bucket_counts_fit(n_tokens, E, cb) ? (int32_t*)(ws + L.blk16) : nullptr;
   if ((rc = pp_route_impl(x, x_dtype, nullptr, n_tokens, H, router_packed, bias, E, tau,
-                          E > 64 ? (float*)(ws + L.logits) : nullptr, nullptr, gates,
+                          logits_out ? logits_out : E != 16 ? (float*)(ws + L.logits) : nullptr, nullptr, gates,
                           mask, count, x_dtype == PP_DTYPE_BF16 ? nullptr : xbf, st, blk16)))
     return rc;
   if (blk16)
@@ -1169,9 +1015,10 @@ static int prefill_pass(const void* x, int x_dtype, int64_t n_tokens, int H, con
   return combine_launch(y, token_pairs, count, n_tokens, H, E, (bf16_t*)out_bf16, st);
 }
 
-extern "C" int pp_moe_prefill(const void* x, int x_dtype, int64_t n_tokens, int H, const float* router_packed,
-                              const float* bias, int E, int G, float tau, const void* packed, void* out_bf16,
-                              void* workspace, void* stream) {
+extern "C" int pp_moe_prefill_routed(const void* x, int x_dtype, int64_t n_tokens, int H,
+                                     const float* router_packed, const float* bias, int E, int G, float tau,
+                                     const void* packed, void* out_bf16, void* workspace, float* logits_out,
+                                     uint8_t* mask_out, void* stream) {
   int rc = pp_check_shape(H, E, G);
   if (rc) return rc;
   PP_REQUIRE(n_tokens >= 0 && n_tokens <= (int64_t)0x7fffffff / PP_MAX_EXPERTS, PP_ERR_UNSUPPORTED,
@@ -1180,13 +1027,25 @@ extern "C" int pp_moe_prefill(const void* x, int x_dtype, int64_t n_tokens, int 
              x_dtype);
   if (n_tokens == 0) return PP_OK;
   PP_REQUIRE(x && router_packed && packed && out_bf16 && workspace, PP_ERR_INVALID, "pp_moe_prefill: null pointer");
+  PP_REQUIRE(((uintptr_t)mask_out & 3) == 0, PP_ERR_INVALID, "pp_moe_prefill: mask_out must be 4-byte aligned");
+  if (prefill_dense_form(G))
+    return pp_dense_prefill(x, x_dtype, n_tokens, H, router_packed, bias, E, G, tau, packed, out_bf16, workspace,
+                            (hipStream_t)stream, logits_out, mask_out);
   const int64_t nc = prefill_pass_tokens(n_tokens, H, E);
   const size_t xs = x_dtype == PP_DTYPE_BF16 ? 2 : 4;
   for (int64_t n0 = 0; n0 < n_tokens; n0 += nc) {
     const int64_t nt = min(nc, n_tokens - n0);
     if ((rc = prefill_pass((const char*)x + (size_t)n0 * H * xs, x_dtype, nt, H, router_packed, bias, E, G, tau,
-                           packed, (bf16_t*)out_bf16 + (size_t)n0 * H, workspace, (hipStream_t)stream)))
+                           packed, (bf16_t*)out_bf16 + (size_t)n0 * H, workspace, (hipStream_t)stream,
+                           logits_out ? logits_out + n0 * E : nullptr, mask_out ? mask_out + n0 * E : nullptr)))
       return rc;
   }
   return PP_OK;
+}
+
+extern "C" int pp_moe_prefill(const void* x, int x_dtype, int64_t n_tokens, int H, const float* router_packed,
+                              const float* bias, int E, int G, float tau, const void* packed, void* out_bf16,
+                              void* workspace, void* stream) {
+  return pp_moe_prefill_routed(x, x_dtype, n_tokens, H, router_packed, bias, E, G, tau, packed, out_bf16, workspace,
+                               nullptr, nullptr, stream);
 }

@@ -535,6 +535,9 @@ static void launch_route_few(const XT* x, int64_t N, int H, const float* router,
 // blkcnt_out (E = 16 path only, else untouched): per block of pp_route_count_block
 // tokens, per expert, the number of selections -- the bucketing's block counts, so it
 // needs no counting pass.
+int pp_route_logits_dense(const void* x, int x_dtype, int64_t N, int H, const float* router, const float* bias,
+                          int E, float* logits_out, bf16_t* xbf_out, uint32_t* zero, int nzero, hipStream_t st);
+
 int pp_route_impl(const void* x, int x_dtype, const float* logits_in, int64_t N, int H,
                   const float* router, const float* bias, int E, float tau, float* logits_out,
                   float* probs_out, float* gates_out, uint8_t* mask_out, int32_t* count_out,
@@ -564,21 +567,17 @@ int pp_route_impl(const void* x, int x_dtype, const float* logits_in, int64_t N,
                                                              count_out, xbf_out, blkcnt_out);
     return pp_check_launch("route16_kernel");
   }
-  if (E > 64 && (logits_in || logits_out)) {  // logits, then one token per workgroup
-    if (!logits_in) {
-      if (x_dtype == PP_DTYPE_F32)
-        route_kernel<float, false, false><<<dim3(grid, (E + 63) / 64), threads, smem, st>>>((const float*)x, nullptr, N, H, router, bias,
-                                                                      E, tau, logits_out, nullptr, nullptr,
-                                                                      nullptr, nullptr, xbf_out);
-      else
-        route_kernel<bf16_t, false, false><<<dim3(grid, (E + 63) / 64), threads, smem, st>>>((const bf16_t*)x, nullptr, N, H, router,
-                                                                       bias, E, tau, logits_out, nullptr, nullptr,
-                                                                       nullptr, nullptr, xbf_out);
-      int rc = pp_check_launch("route_kernel (logits)");
-      if (rc) return rc;
-    }
-    const float* lg = logits_in ? logits_in : logits_out;
-    float* lcopy = (logits_in && logits_out && logits_out != logits_in) ? logits_out : nullptr;
+  if (!logits_in && logits_out) {
+    // E != 16 with a logits buffer: the LDS-staged logits pass (one fixed summation order
+    // per (token, expert), the prefill's own router), then the selection from those logits
+    int rc = pp_route_logits_dense(x, x_dtype, N, H, router, bias, E, logits_out, xbf_out, nullptr, 0, st);
+    if (rc) return rc;
+    logits_in = logits_out;
+    logits_out = nullptr;
+  }
+  if (E > 64 && logits_in) {  // one token per workgroup
+    const float* lg = logits_in;
+    float* lcopy = (logits_out && logits_out != logits_in) ? logits_out : nullptr;
     for (int64_t t0 = 0; t0 < N; t0 += 65535) {
       const int64_t n = N - t0 < 65535 ? N - t0 : 65535;
       route_select_wg_kernel<<<(unsigned)n, 256, 0, st>>>(lg + t0 * E, n, E, tau, lcopy ? lcopy + t0 * E : nullptr,

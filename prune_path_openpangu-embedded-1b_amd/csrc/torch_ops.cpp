@@ -344,100 +344,35 @@ void moe_decode_batch_into_meta(const Tensor&, const Tensor&, const optional<Ten
                                 const optional<Tensor>&, int64_t) {}
 
 // ------------------------------------------------------------------ prefill
-// Dense form, for G % 64 != 0 (the checkpoint's E = 192, G = 32), where the grouped
-// GEMMs have no MFMA tiling and each selected pair's down projection would be a K = G
-// GEMM writing a full fp32 row of H: per chunk of tokens, the router (pp_route: bit-exact
-// selection, gates 0 where not selected), gate and up of every neuron as two library
-// GEMMs with fp32 results (bf16 x and weights, the packed records read in place: rows
-// 3H apart), pp_swiglu_gate (the grouped gate/up epilogue's expression and rounding),
-// then the down GEMM over all neurons (fp32 result, rounded to bf16 once). The
-// unselected experts' neurons carry act 0 and add exactly nothing. Every intermediate
-// lives in the caller's workspace (pp_prefill_workspace_bytes, at least ~70 KB per
-// token here), chunked to fit it.
-void prefill_dense(const Tensor& x, const Tensor& router_packed, const optional<Tensor>& bias, int64_t E,
-                   int64_t G, double tau, const Tensor& packed, const Tensor& workspace, const Tensor& out) {
-  const int64_t N = x.size(0), H = x.size(1), I = E * G;
-  TORCH_CHECK(x.is_contiguous() && out.is_contiguous() && packed.is_contiguous(),
-              "prunepath.moe_prefill: x, out and packed must be contiguous");
-  TORCH_CHECK(packed.numel() >= 3 * I * H, "prunepath.moe_prefill: packed expert buffer too small");
-  if (N == 0) return;
-  const auto fopt = x.options().dtype(at::kFloat), bopt = x.options().dtype(at::kBFloat16);
-  const Tensor rec = packed.narrow(0, 0, 3 * I * H).view({I, 3, H});
-  const Tensor wg = rec.select(1, 0), wu = rec.select(1, 1), wd = rec.select(1, 2);  // [I, H], rows 3H apart
-  auto up256 = [](int64_t b) { return (b + 255) & ~(int64_t)255; };
-  // bytes per token: logits, probs, gates, mask, count; x (fp32, for the router GEMM);
-  // gate, up (fp32), act, x (bf16); out fp32
-  const int64_t per_tok = up256(E * 4) * 3 + up256(E) + 256 + H * 4 + I * 4 * 2 + I * 2 + H * 2 + H * 4;
-  const int64_t nc = std::min<int64_t>(N, (workspace.numel() - 16 * 256) / per_tok);
-  TORCH_CHECK(nc >= 1, "prunepath.moe_prefill: workspace too small for the dense form");
-  uint8_t* base = workspace.data_ptr<uint8_t>();
-  const Tensor out2 = out.view({N, H});
-  for (int64_t t0 = 0; t0 < N; t0 += nc) {
-    const int64_t n = std::min(nc, N - t0);
-    int64_t off = 0;
-    auto carve = [&](int64_t bytes) {
-      void* p = base + off;
-      off += up256(bytes);
-      return p;
-    };
-    float* logits = (float*)carve(n * E * 4);
-    float* probs = (float*)carve(n * E * 4);
-    float* gates = (float*)carve(n * E * 4);
-    uint8_t* mask = (uint8_t*)carve(n * E);
-    int32_t* count = (int32_t*)carve(n * 4);
-    const Tensor xc = x.narrow(0, t0, n);
-    // router logits as one fp32 library GEMM (x fp32 [n, H] times the router's E rows),
-    // then the bias added to each sum, as the router kernel does; the selection from those
-    // logits is pp_route_logits (bit-exact against the reference's selection ops)
-    Tensor lg = at::from_blob(logits, {n, E}, fopt);
-    Tensor xf = xc;
-    if (x.scalar_type() != at::kFloat) {
-      xf = at::from_blob(carve(n * H * 4), {n, H}, fopt);
-      xf.copy_(xc);
-    }
-    at::mm_out(lg, xf, router_packed.narrow(0, 0, E).t());
-    if (bias.has_value()) lg.add_(*bias);
-    check_rc(pp_route_logits(logits, n, (int)E, (float)tau, probs, gates, mask, count, stream_of(x)),
-             "moe_prefill (route_logits)");
-    Tensor gt = at::from_blob(carve(n * I * 4), {n, I}, fopt);
-    Tensor ut = at::from_blob(carve(n * I * 4), {n, I}, fopt);
-    Tensor act = at::from_blob(carve(n * I * 2), {n, I}, bopt);
-    Tensor xb = xc;
-    if (x.scalar_type() != at::kBFloat16) {
-      xb = at::from_blob(carve(n * H * 2), {n, H}, bopt);
-      xb.copy_(xc);
-    }
-    Tensor o32 = at::from_blob(carve(n * H * 4), {n, H}, fopt);
-    TORCH_CHECK(off <= workspace.numel(), "prunepath.moe_prefill: dense workspace overrun");
-    at::mm_out(gt, xb, wg.t(), at::kFloat);
-    at::mm_out(ut, xb, wu.t(), at::kFloat);
-    check_rc(pp_swiglu_gate(gt.data_ptr<float>(), ut.data_ptr<float>(), gates, n, (int)E, (int)G, act.data_ptr(),
-                            stream_of(x)),
-             "moe_prefill (swiglu)");
-    at::mm_out(o32, act, wd, at::kFloat);
-    out2.narrow(0, t0, n).copy_(o32);
-  }
-}
-
+// One implementation behind both boundaries: pp_moe_prefill_routed (the grouped pipeline,
+// or for G % 64 != 0 the dense form of csrc/dense.hip), hand-written kernels only.
 void prefill_into(const Tensor& x, const Tensor& router_packed, const optional<Tensor>& bias, int64_t E, int64_t G,
-                  double tau, const Tensor& packed, const Tensor& workspace, const Tensor& out) {
+                  double tau, const Tensor& packed, const Tensor& workspace, const Tensor& out,
+                  const optional<Tensor>& logits_out, const optional<Tensor>& mask_out) {
   TORCH_CHECK(x.dim() == 2, "prunepath.moe_prefill: x must be [N, H]");
   const int64_t N = x.size(0), H = x.size(1);
   check_bias(bias, E, "moe_prefill");
+  TORCH_CHECK(x.is_contiguous() && packed.is_contiguous(), "prunepath.moe_prefill: x and packed must be contiguous");
   TORCH_CHECK(workspace.scalar_type() == at::kByte &&
                   workspace.numel() >= (int64_t)pp_prefill_workspace_bytes(N, (int)H, (int)E, (int)G),
               "prunepath.moe_prefill: uint8 workspace of pp_prefill_workspace_bytes(N, H, E, G) required");
-  TORCH_CHECK(out.scalar_type() == at::kBFloat16 && out.numel() == N * H, "prunepath.moe_prefill: out must be bf16 [N, H]");
+  TORCH_CHECK(out.scalar_type() == at::kBFloat16 && out.numel() == N * H && out.is_contiguous(),
+              "prunepath.moe_prefill: out must be contiguous bf16 [N, H]");
+  if (logits_out.has_value())
+    TORCH_CHECK(logits_out->scalar_type() == at::kFloat && logits_out->numel() == N * E && logits_out->is_contiguous(),
+                "prunepath.moe_prefill: logits_out must be contiguous fp32 [N, E]");
+  if (mask_out.has_value())
+    TORCH_CHECK(mask_out->scalar_type() == at::kByte && mask_out->numel() == N * E && mask_out->is_contiguous(),
+                "prunepath.moe_prefill: mask_out must be contiguous uint8 [N, E]");
   need_gpu("moe_prefill", x,
-           {&x, &router_packed, bias.has_value() ? &*bias : nullptr, &packed, &workspace, &out});
+           {&x, &router_packed, bias.has_value() ? &*bias : nullptr, &packed, &workspace, &out,
+            logits_out.has_value() ? &*logits_out : nullptr, mask_out.has_value() ? &*mask_out : nullptr});
   const c10::DeviceGuard g(x.device());
-  if (G % 64 != 0) {
-    prefill_dense(x, router_packed, bias, E, G, tau, packed, workspace, out);
-    return;
-  }
-  check_rc(pp_moe_prefill(x.data_ptr(), x_code(x, "moe_prefill"), N, (int)H, router_packed.data_ptr<float>(),
-                          (const float*)ptr(bias), (int)E, (int)G, (float)tau, packed.data_ptr(), out.data_ptr(),
-                          workspace.data_ptr(), stream_of(x)),
+  check_rc(pp_moe_prefill_routed(x.data_ptr(), x_code(x, "moe_prefill"), N, (int)H, router_packed.data_ptr<float>(),
+                                 (const float*)ptr(bias), (int)E, (int)G, (float)tau, packed.data_ptr(),
+                                 out.data_ptr(), workspace.data_ptr(),
+                                 logits_out.has_value() ? logits_out->data_ptr<float>() : nullptr,
+                                 mask_out.has_value() ? mask_out->data_ptr<uint8_t>() : nullptr, stream_of(x)),
            "moe_prefill");
 }
 
@@ -448,7 +383,7 @@ Tensor moe_prefill_gpu(const Tensor& x, const Tensor& router_packed, const optio
   Tensor out = at::empty({N, H}, x.options().dtype(at::kBFloat16));
   Tensor ws = at::empty({(int64_t)pp_prefill_workspace_bytes(N, (int)H, (int)E, (int)G)},
                         x.options().dtype(at::kByte));
-  prefill_into(x, router_packed, bias, E, G, tau, packed, ws, out);
+  prefill_into(x, router_packed, bias, E, G, tau, packed, ws, out, c10::nullopt, c10::nullopt);
   return out;
 }
 
@@ -458,7 +393,8 @@ Tensor moe_prefill_meta(const Tensor& x, const Tensor&, const optional<Tensor>&,
 }
 
 void moe_prefill_into_meta(const Tensor&, const Tensor&, const optional<Tensor>&, int64_t, int64_t, double,
-                           const Tensor&, const Tensor&, const Tensor&) {}
+                           const Tensor&, const Tensor&, const Tensor&, const optional<Tensor>&,
+                           const optional<Tensor>&) {}
 
 // CPU tensors: refused with the op's name (there is no host implementation, on purpose).
 void refuse_cpu(const c10::OperatorHandle& op, torch::jit::Stack*) {
@@ -488,7 +424,7 @@ TORCH_LIBRARY(prunepath, m) {
         "Tensor(e!)? mask_out=None, int grid=0) -> ()");
   m.def("moe_prefill(Tensor x, Tensor router_packed, Tensor? bias, int E, int G, float tau, Tensor packed) -> Tensor");
   m.def("moe_prefill_into(Tensor x, Tensor router_packed, Tensor? bias, int E, int G, float tau, Tensor packed, "
-        "Tensor(a!) workspace, Tensor(b!) out) -> ()");
+        "Tensor(a!) workspace, Tensor(b!) out, Tensor(c!)? logits_out=None, Tensor(d!)? mask_out=None) -> ()");
 }
 
 TORCH_LIBRARY_IMPL(prunepath, CUDA, m) {

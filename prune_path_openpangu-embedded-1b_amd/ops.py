@@ -14,7 +14,7 @@ synchronises with the host, so the calls can be captured in a CUDA (HIP) graph.
 from __future__ import annotations
 
 import ctypes
-from typing import Optional
+from typing import Optional, Tuple
 
 import torch
 
@@ -192,22 +192,36 @@ def prefill_workspace_bytes(N: int, H: int, E: int, G: int) -> int:
 
 def moe_prefill(x: torch.Tensor, router_packed: torch.Tensor, bias: Optional[torch.Tensor], E: int, G: int,
                 tau: float, packed: torch.Tensor, workspace: Optional[torch.Tensor] = None,
-                out: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """Route -> bucket -> grouped gate/up GEMM (SwiGLU) -> grouped down GEMM -> combine.
-    x [N,H]; returns bf16 [N,H]. ``torch.ops.prunepath.moe_prefill`` (workspace from the
-    caching allocator), or ``moe_prefill_into`` when a workspace / output is given."""
+                out: Optional[torch.Tensor] = None, logits_out: Optional[torch.Tensor] = None,
+                mask_out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """The prefill layer: x [N,H] -> bf16 [N,H]. G % 64 == 0: route -> bucket -> grouped
+    gate/up GEMM (SwiGLU) -> grouped down GEMM -> combine; otherwise the dense form (router
+    logits, selection, dense gate/up with the gate 0 for unselected experts, dense down).
+    ``torch.ops.prunepath.moe_prefill`` (workspace from the caching allocator), or
+    ``moe_prefill_into`` when a workspace, output or routing output (logits_out fp32 [N,E],
+    mask_out uint8 [N,E]: the routing the call used) is given."""
     if x.dtype not in (torch.float32, torch.bfloat16):
         x = x.float()
     ops = L.torch_ops()
-    if workspace is None and out is None:
+    if workspace is None and out is None and logits_out is None and mask_out is None:
         return ops.moe_prefill(x, router_packed, bias, E, G, float(tau), packed)
     N, H = x.shape
     if workspace is None or workspace.numel() < prefill_workspace_bytes(N, H, E, G):
         workspace = torch.empty(prefill_workspace_bytes(N, H, E, G), dtype=torch.uint8, device=x.device)
     if out is None:
         out = torch.empty(N, H, dtype=torch.bfloat16, device=x.device)
-    ops.moe_prefill_into(x, router_packed, bias, E, G, float(tau), packed, workspace, out)
+    ops.moe_prefill_into(x, router_packed, bias, E, G, float(tau), packed, workspace, out, logits_out, mask_out)
     return out
+
+
+def moe_prefill_routed(x: torch.Tensor, router_packed: torch.Tensor, bias: Optional[torch.Tensor], E: int, G: int,
+                       tau: float, packed: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """(out bf16 [N,H], logits fp32 [N,E], mask uint8 [N,E]): the prefill and the routing it used."""
+    N = x.shape[0]
+    logits = torch.empty(N, E, dtype=torch.float32, device=x.device)
+    mask = torch.empty(N, E, dtype=torch.uint8, device=x.device)
+    out = moe_prefill(x, router_packed, bias, E, G, tau, packed, logits_out=logits, mask_out=mask)
+    return out, logits, mask
 
 
 def expert_gateup(x_bf16: torch.Tensor, packed: torch.Tensor, E: int, G: int, bk: dict) -> torch.Tensor:

@@ -126,3 +126,24 @@ def assert_close(got: np.ndarray, ref: np.ndarray, rtol=RTOL, atol=ATOL, what=""
         raise AssertionError(f"{what}: {bad.sum()} / {bad.size} outside rtol={rtol} atol={atol}; "
                              f"first at {tuple(i)}: got {got[tuple(i)]} ref {ref[tuple(i)]}; "
                              f"max abs err {err.max():.3e}")
+
+
+def abi_prefill(pkg, m, xs, E, G, tau=0.7, routed=True):
+    """pp_moe_prefill_routed through the C ABI on the module's buffers: (out bf16 [n,H],
+    logits fp32 [n,E], mask uint8 [n,E]) -- the routing the call itself used (routed=False:
+    no routing outputs requested)."""
+    import ctypes
+    n, H = xs.shape
+    y = torch.empty(n, H, dtype=torch.bfloat16, device=xs.device)
+    lg = torch.empty(n, E, dtype=torch.float32, device=xs.device)
+    mk = torch.empty(n, E, dtype=torch.uint8, device=xs.device)
+    ws = torch.empty(pkg.ops.prefill_workspace_bytes(n, H, E, G), dtype=torch.uint8, device=xs.device)
+    vp = lambda t: ctypes.c_void_p(t.data_ptr() if t is not None else 0)  # noqa: E731
+    lib = pkg._lib.lib()
+    xc = 0 if xs.dtype == torch.float32 else 1
+    pkg._lib.check(lib.pp_moe_prefill_routed(vp(xs), xc, n, H, vp(m.router_packed), vp(m.router_bias), E, G,
+                                             ctypes.c_float(tau), vp(m.packed_experts), vp(y), vp(ws),
+                                             vp(lg if routed else None), vp(mk if routed else None),
+                                             ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)),
+                   "moe_prefill_routed")
+    return y, lg, mk

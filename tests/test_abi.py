@@ -52,7 +52,7 @@ def test_sizes():
     assert lib.pp_max_tiles(2048, 16, 128) == 2048 * 16 // 128 + 16
     assert lib.pp_decode_workspace_bytes(H, E) >= 32 + 3 * 4 * 256 + 8 * H * 4
     assert lib.pp_prefill_workspace_bytes(2048, H, E, G) > 2048 * 16 * (G + H) * 2
-    assert lib.pp_abi_version() == 1
+    assert lib.pp_abi_version() == 2
 
 
 @pytest.mark.parametrize("H,E,G", [(100, 16, 384), (1536, 0, 384), (1536, 300, 32), (1536, 16, 40),

@@ -16,8 +16,8 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import (GOLDEN, assert_close, assert_close_fp32, bits, gi, make_module, oracle, sparse_expected,
-                     sparse_expected_gpu, to_gpu)
+from helpers import (GOLDEN, abi_prefill as _abi_prefill, assert_close, assert_close_fp32, bits, gi, make_module,
+                     oracle, sparse_expected, sparse_expected_gpu, to_gpu)
 
 pytestmark = pytest.mark.gpu
 
@@ -204,46 +204,90 @@ def test_prefill_stages_vs_oracle(pkg):
     np.testing.assert_array_equal(out.float().cpu().numpy(), full)
 
 
-def test_prefill_in_passes_e192(pkg):
-    """E = 192, G = 32, 1000 tokens, on both prefill forms:
-    * the C ABI's pp_moe_prefill (the grouped pipeline; its worst-case pair buffers are
-      bounded: 455 tokens a pass at H = 1536) in three passes on a workspace sized for one:
-      every row vs the float64 reference, selection bit-exact, and the output identical to
-      the same tokens run as separate calls;
-    * the module (torch op prunepath::moe_prefill, the dense form at G % 64 != 0: library
-      GEMMs around pp_swiglu_gate): every row vs the same reference, and repeated calls
-      identical. (Its rows are not bit-identical across calls of different token counts:
-      the library picks its GEMM kernel by the row count.)"""
-    import ctypes
+def test_prefill_dense_form_e192(pkg):
+    """E = 192, G = 32 (the checkpoint's shape: the dense form of csrc/dense.hip), 1000 tokens:
+    * the routing the call used (its own logits, read back): the selection bit-exact against
+      the oracle on those logits, and every row against the float64 restatement with that
+      selection, acts rounded to bf16 (the reference's rounding point);
+    * the C ABI and the torch op (module) give the same bits, and repeated calls too;
+    * the logits of a token do not depend on the batch: rows 500..599 routed alone equal
+      the same rows of the 1000-token call, and pp_route gives the same logits;
+    * no global torch state reaches the routing (TF32 allowed or not: the same logits)."""
     E, G, N, H = 192, 32, 1000, 1536
-    assert pkg.ops.prefill_workspace_bytes(N, H, E, G) == pkg.ops.prefill_workspace_bytes(455, H, E, G)
     w = gi.layer_weights(41, E=E)
     m = make_module(pkg, w, 0.7)
     x = gi.tokens(42, N)
     xg = to_gpu(x)
+    y, lg, mk = _abi_prefill(pkg, m, xg, E, G)
+    sel = oracle.select(lg.cpu().numpy(), 0.7)
+    np.testing.assert_array_equal(mk.cpu().numpy(), sel.mask)
+    out = y.float().cpu().numpy()
+    assert_close(out, sparse_expected_gpu(x, w, sel.gates, act_bf16=True), what="E=192 dense prefill (C ABI)")
+    outm = m(xg[None]).float().cpu()
+    assert torch.equal(outm[0], y.float().cpu()), "module (torch op) and C ABI differ"
+    assert torch.equal(m(xg[None]).float().cpu(), outm), "repeated call differs"
+    _, lg2, mk2 = _abi_prefill(pkg, m, xg[500:600].contiguous(), E, G)
+    assert torch.equal(lg2, lg[500:600]) and torch.equal(mk2, mk[500:600])
     res = pkg.ops.route(xg, m.router_packed, E, 0.7)
-    sel = oracle.select(res["logits"].cpu().numpy(), 0.7)
-    np.testing.assert_array_equal(res["mask"].cpu().numpy(), sel.mask)
-    expected = sparse_expected_gpu(x, w, sel.gates)
-    lib = pkg._lib.lib()
-    vp = lambda t: ctypes.c_void_p(t.data_ptr() if t is not None else 0)  # noqa: E731
+    assert torch.equal(res["logits"], lg) and torch.equal(res["mask"], mk)
+    old = torch.backends.cuda.matmul.allow_tf32
+    try:
+        torch.backends.cuda.matmul.allow_tf32 = True
+        torch.set_float32_matmul_precision("high")
+        _, lg3, _ = _abi_prefill(pkg, m, xg, E, G)
+    finally:
+        torch.backends.cuda.matmul.allow_tf32 = old
+        torch.set_float32_matmul_precision("highest")
+    assert torch.equal(lg3, lg)
 
-    def abi(xs):
-        n = xs.shape[0]
-        y = torch.empty(n, H, dtype=torch.bfloat16, device=xs.device)
-        ws = torch.empty(pkg.ops.prefill_workspace_bytes(n, H, E, G), dtype=torch.uint8, device=xs.device)
-        pkg._lib.check(lib.pp_moe_prefill(vp(xs), 0, n, H, vp(m.router_packed), vp(None), E, G, ctypes.c_float(0.7),
-                                          vp(m.packed_experts), vp(y), vp(ws),
-                                          ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)), "moe_prefill")
-        return y.float().cpu().numpy()
 
-    out = abi(xg)
-    assert_close(out, expected, what="E=192 prefill in passes (C ABI, grouped pipeline)")
-    parts = [abi(xg[a:b].contiguous()) for a, b in ((0, 455), (455, 910), (910, N))]
-    np.testing.assert_array_equal(np.concatenate(parts), out)
-    outm = m(xg[None]).float().cpu().numpy()[0]
-    assert_close(outm, expected, what="E=192 prefill (module, dense form)")
-    np.testing.assert_array_equal(m(xg[None]).float().cpu().numpy()[0], outm)
+@pytest.mark.parametrize("H,E,G,N,xdt", [
+    (384, 1, 32, 1, torch.float32),      # the smallest call: one token, one 32-neuron expert
+    (128, 3, 32, 5, torch.bfloat16),     # I = 96: the down GEMM's K padded to 128 with zero acts
+    (4096, 192, 32, 300, torch.float32), # H = 4096, two row tiles (the second ragged)
+    (640, 5, 160, 70, torch.float32),    # G = 160: experts straddle K blocks; a short last hidden tile
+    (1536, 24, 32, 257, torch.bfloat16), # E = 24 (two 16-expert logit tiles), bf16 x, ragged N
+    (1536, 16, 96, 40, torch.float32),   # E = 16 with G % 64 != 0: the E = 16 router feeds the dense form
+])
+def test_prefill_dense_form_shapes(pkg, H, E, G, N, xdt):
+    """The dense form across shapes: selection bit-exact on the call's own logits, every row
+    against the float64 restatement (acts rounded to bf16), a router bias on E > 1."""
+    seed = H + E * 5 + G + N
+    w = gi.layer_weights(seed, H=H, I=E * G, E=E)
+    m = make_module(pkg, w, 0.7, bias=gi.zipf_bias(E) if E > 1 else None)
+    x = gi.tokens(seed + 1, N, H=H)
+    xg = to_gpu(x, xdt)
+    y, lg, mk = _abi_prefill(pkg, m, xg, E, G)
+    sel = oracle.select(lg.cpu().numpy(), 0.7)
+    np.testing.assert_array_equal(mk.cpu().numpy(), sel.mask)
+    xr = xg.float().cpu().numpy()
+    assert_close(y.float().cpu().numpy(), sparse_expected(xr, w, sel.gates, act_bf16=True),
+                 what=f"dense form H={H} E={E} G={G} N={N}")
+    y2, _, _ = _abi_prefill(pkg, m, xg, E, G, routed=False)
+    assert torch.equal(y, y2)
+
+
+def test_prefill_dense_form_unselected_expert_not_evaluated(pkg):
+    """An expert no token selects may hold huge weights: its gate/up products overflow to
+    inf, and inf * 0 would make NaN. The dense form never evaluates an unselected expert's
+    act (gate 0 -> act exactly 0), so the outputs stay finite and equal the restatement."""
+    E, G, N, H = 8, 32, 64, 256
+    w = gi.layer_weights(77, H=H, I=E * G, E=E)
+    w["w_router"][5] = -1.0 * np.abs(w["w_router"][5]).sum() - 50.0  # expert 5: never selected
+    x = np.abs(gi.tokens(78, N, H=H)).astype(np.float32)
+    perm = oracle.pack_permutation(w["expert_ids"])
+    hot = perm[5 * G:6 * G]  # source neurons of rearranged expert 5
+    w2 = {k: v.copy() for k, v in w.items()}
+    w2["w_gate"][hot] = 3e38
+    w2["w_up"][hot] = 3e38
+    m2 = make_module(pkg, w2, 0.7)
+    xg = to_gpu(x)
+    y, lg, mk = _abi_prefill(pkg, m2, xg, E, G)
+    assert not mk.cpu().numpy()[:, 5].any()
+    out = y.float().cpu().numpy()
+    assert np.isfinite(out).all()
+    sel = oracle.select(lg.cpu().numpy(), 0.7)
+    assert_close(out, sparse_expected(x, w, sel.gates, act_bf16=True), what="huge unselected expert")
 
 
 def test_real_checkpoint_shape_e192_g32(pkg):
@@ -254,12 +298,14 @@ def test_real_checkpoint_shape_e192_g32(pkg):
     m = make_module(pkg, w, 0.7)
     x = gi.tokens(32, 96)
     out = m(to_gpu(x[None])).float().cpu().numpy()[0]
-    res = pkg.ops.route(to_gpu(x), m.router_packed, 192, 0.7)
-    sel = oracle.select(res["logits"].cpu().numpy(), 0.7)
-    np.testing.assert_array_equal(res["mask"].cpu().numpy(), sel.mask)
-    assert_close(out, sparse_expected_gpu(x, w, sel.gates), what="E=192 prefill, every row")
+    y, lg, mk = _abi_prefill(pkg, m, to_gpu(x), 192, 32)
+    sel = oracle.select(lg.cpu().numpy(), 0.7)
+    np.testing.assert_array_equal(mk.cpu().numpy(), sel.mask)  # the path's own routing
+    np.testing.assert_array_equal(y.float().cpu().numpy(), out)
+    assert_close(out, sparse_expected_gpu(x, w, sel.gates, act_bf16=True), what="E=192 prefill, every row")
     rows = np.arange(0, 96, 6)
-    assert_close(out[rows], sparse_expected(x[rows], w, sel.gates[rows]), what="E=192 prefill (numpy fp64 rows)")
+    assert_close(out[rows], sparse_expected(x[rows], w, sel.gates[rows], act_bf16=True),
+                 what="E=192 prefill (numpy fp64 rows)")
     od = m(to_gpu(x[None, :1])).float().cpu().numpy()[0, 0]
     st = pkg.ops.decode_state(m.decode_workspace, 192)
     assert st["error"] == 0
@@ -476,48 +522,22 @@ def test_decode_top_expert_speculation(pkg, tau, want):
 
 
 @pytest.mark.gpu
-def test_swiglu_gate_abi(pkg):
-    """pp_swiglu_gate (the dense prefill form's SwiGLU with the expert gating) through the C
-    ABI against a torch float32 restatement, act = bf16(silu(g) * u * gates[t, n // G]):
-    within one bf16 step (the kernel's silu uses the fast exp, so the value before the
-    rounding differs by a few fp32 ulps), and exactly 0 where the expert is not selected."""
-    import ctypes
-    lib = pkg._lib.lib()
-    n, E, G = 37, 12, 32
-    I = E * G
-    gen = torch.Generator(device="cuda").manual_seed(3)
-    g = torch.randn(n, I, device="cuda", generator=gen) * 3
-    u = torch.randn(n, I, device="cuda", generator=gen)
-    gates = torch.rand(n, E, device="cuda", generator=gen)
-    gates[gates < 0.5] = 0
-    act = torch.empty(n, I, dtype=torch.bfloat16, device="cuda")
-    vp = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
-    pkg._lib.check(lib.pp_swiglu_gate(vp(g), vp(u), vp(gates), n, E, G, vp(act),
-                                      ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)), "swiglu_gate")
-    gfull = gates.repeat_interleave(G, dim=1)
-    ref = torch.nn.functional.silu(g) * u * gfull
-    a = act.float()
-    assert torch.allclose(a, ref, rtol=2.0 ** -7, atol=1e-30)
-    assert bool((a[gfull == 0] == 0).all())
-    assert bool((a[gfull != 0] == ref[gfull != 0].to(torch.bfloat16).float()).float().mean() > 0.99)
-
-
-@pytest.mark.gpu
-def test_prefill_dense_form_two_chunks_e192(pkg):
-    """The dense prefill form (E = 192, G = 32) on 8200 tokens: more than the workspace's
-    chunk (~7700 tokens at H = 1536), so the op routes and multiplies in two chunks on one
-    workspace. Selection bit-exact against the oracle on the kernel's logits, every row
-    against the float64 restatement with the acts rounded to bf16, the reference's
-    rounding point (src/tl_kernel_optimized_Ultimate_PanGU.py:321); without that rounding
-    one output in 12.6 M, a near-cancelling sum of ~2400 act products, sits 5 % past the
-    bound."""
-    E, N = 192, 8200
-    w = gi.layer_weights(43, E=E)
+def test_prefill_dense_form_two_passes(pkg):
+    """The dense form over more tokens than one pass holds: E = 64 experts of G = 800
+    neurons at H = 128 (about 100 KB of per-token buffers: 2613 tokens a pass), 2700 tokens
+    in two passes on one workspace; the down GEMM's K of 51200 is split over many parts per
+    tile. Selection bit-exact on the call's own logits, every row against the float64
+    restatement (acts rounded to bf16), repeated calls bit-identical."""
+    E, G, N, H = 64, 800, 2700, 128
+    w = gi.layer_weights(43, H=H, I=E * G, E=E)
     m = make_module(pkg, w, 0.7)
-    x = gi.tokens(44, N)
+    x = gi.tokens(44, N, H=H)
     xg = to_gpu(x)
-    res = pkg.ops.route(xg, m.router_packed, E, 0.7)
-    sel = oracle.select(res["logits"].cpu().numpy(), 0.7)
-    np.testing.assert_array_equal(res["mask"].cpu().numpy(), sel.mask)
-    out = m(xg[None]).float().cpu().numpy()[0]
-    assert_close(out, sparse_expected_gpu(x, w, sel.gates, act_bf16=True), what="E=192 dense prefill, two chunks")
+    assert pkg.ops.prefill_workspace_bytes(N, H, E, G) == pkg.ops.prefill_workspace_bytes(2 * N, H, E, G)
+    y, lg, mk = _abi_prefill(pkg, m, xg, E, G)
+    sel = oracle.select(lg.cpu().numpy(), 0.7)
+    np.testing.assert_array_equal(mk.cpu().numpy(), sel.mask)
+    assert_close(y.float().cpu().numpy(), sparse_expected_gpu(x, w, sel.gates, act_bf16=True),
+                 what="dense form, two passes")
+    y2, _, _ = _abi_prefill(pkg, m, xg, E, G, routed=False)
+    assert torch.equal(y, y2)

@@ -11,12 +11,12 @@ atol 2e-3) with the selection bit-exact against the oracle on the kernel's own l
   G > 512 or E * G > 8192; local and published logits, eight waves for H <= 2560 and
   four above);
 * prefill routing: route16_few_kernel (E = 16, N <= 64, H % 512 == 0, H <= 2048),
-  route16_kernel (other E = 16 cases), route_kernel (E != 16, E <= 64) and, for E > 64,
-  route_kernel's split logits launch with route_select_wg_kernel;
+  route16_kernel (other E = 16 cases), and for E != 16 route_logits_kernel (the LDS-staged
+  logits pass, one to three 16-expert tiles per workgroup) with the selection from its
+  logits: route_kernel for E <= 64, route_select_wg_kernel above;
 * prefill GEMMs: gemm_s_kernel (N <= 64, G % 64 == 0, H >= 384), gemm_v3_kernel
-  (G % 64 == 0 otherwise); at G % 64 != 0 the torch op's dense form (library GEMMs around
-  swiglu_gate_kernel) and, through the C ABI's pp_moe_prefill, gateup_kernel /
-  down_kernel;
+  (G % 64 == 0 otherwise); at G % 64 != 0 the dense form (dense_gemm_kernel, gate/up and
+  down), the same implementation behind the torch op and the C ABI (same bits);
 * the limits: H = 128 and 4096, E = 1 and 256, G = 32 and 8192, tau above 1 (every
   expert selected) and 0 (rank 0 only), bf16 and fp32 x; a router bias (log Zipf) on
   every router variant;
@@ -28,7 +28,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import assert_close, gi, make_module, oracle, sparse_expected, to_gpu
+from helpers import abi_prefill as _abi_prefill, assert_close, gi, make_module, oracle, sparse_expected, to_gpu
 
 pytestmark = pytest.mark.gpu
 
@@ -95,17 +95,11 @@ def test_layer_shape_vs_oracle(pkg, H, E, G, N, tau, xdt, with_bias):
                                          m.packed_experts).float().cpu().numpy()
         out = pf()
     assert_close(out, expected, what=f"layer H={H} E={E} G={G} N={N}")
-    if N > 1 and G % 64 != 0:  # the torch op took the dense form: the grouped pipeline through the C ABI
-        import ctypes
-        lib = pkg._lib.lib()
-        y = torch.empty(N, H, dtype=torch.bfloat16, device=xg.device)
-        ws = torch.empty(pkg.ops.prefill_workspace_bytes(N, H, E, G), dtype=torch.uint8, device=xg.device)
-        vp = lambda t: ctypes.c_void_p(t.data_ptr() if t is not None else 0)  # noqa: E731
-        pkg._lib.check(lib.pp_moe_prefill(vp(xg), 0 if xdt == torch.float32 else 1, N, H, vp(m.router_packed),
-                                          vp(m.router_bias), E, G, ctypes.c_float(tau), vp(m.packed_experts),
-                                          vp(y), vp(ws), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)),
-                       "moe_prefill")
-        assert_close(y.float().cpu().numpy(), expected, what=f"grouped pipeline H={H} E={E} G={G} N={N}")
+    if N > 1:  # the C ABI: the same implementation as the torch op, and the routing it used
+        y, lg, mk = _abi_prefill(pkg, m, xg, E, G, tau)
+        np.testing.assert_array_equal(y.float().cpu().numpy(), out)
+        np.testing.assert_array_equal(mk.cpu().numpy(), oracle.select(lg.cpu().numpy(), tau).mask)
+        np.testing.assert_array_equal(lg.cpu().numpy(), logits)
     out2 = m(xg[None]).float().cpu().numpy()[0] if N == 1 else pf()
     np.testing.assert_array_equal(out2, out)  # prefill and decode are deterministic bit for bit
     if N > 1 and pkg.ops.decode_batch_supported(N, H, E, G):  # the one-launch batch kernel (module path)
