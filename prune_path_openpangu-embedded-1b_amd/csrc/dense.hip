@@ -499,15 +499,16 @@ __global__ __launch_bounds__(NW * 64, 1) void dense_gemm_kernel(DgArgs p) {
 }
 
 // ------------------------------------------------------------------ router logits (E > 16)
-// Logits of 32 tokens x 16 TE experts per workgroup of four waves on the fp32 MFMA
-// (v_mfma_f32_16x16x4_f32). x and the router rows pass through LDS in K chunks of RL_KC
+// Logits of 32 tokens x 16 TE experts per workgroup of eight waves on the fp32 MFMA
+// (v_mfma_f32_16x16x4_f32), two waves per SIMD. x and the router rows pass through LDS in K chunks of RL_KC
 // (RL_STAGES stages, DMA RL_STAGES - 1 chunks ahead; every DMA instruction moves whole
 // rows, two 512-byte fp32 rows or four 256-byte bf16 rows). 16-byte chunk c of LDS row r
 // sits at c ^ (r & 15): the sixteen rows a fragment read touches fall in distinct bank
-// slots. Wave w takes the 32-wide K block w of every chunk; lane (t = l % 16, g = l / 16)
+// slots. Wave w takes the 32-wide K block w % 4 of every chunk for the 16-token tile
+// w / 4; lane (t = l % 16, g = l / 16)
 // holds x[t][k + 8 g + j] and W[expert l % 16][k + 8 g + j], j = 0..7, one MFMA per j per
 // 16 x 16 tile, so each k of the block is used exactly once. Each tile accumulates in
-// chunk order, j order; the four wave partials are added in wave order, then the bias:
+// chunk order, j order; the four K-block partials are added in block order, then the bias:
 // one fixed order per (token, expert) whatever N or the token's position, so a token
 // routes the same way in any batch. Result lane l, element q: token 4 (l / 16) + q,
 // expert l % 16 of the tile.
@@ -520,8 +521,8 @@ struct Rl {
   static constexpr int WROW = RL_KC * 4;                // router row bytes in a stage
   static constexpr int XB = 16 * RL_TT * XROW;
   static constexpr int STAGE = XB + 16 * TE * WROW;
-  static constexpr int XI = XB / 4096;               // DMA instructions per wave per chunk, x
-  static constexpr int WI = 16 * TE * WROW / 4096;   // ... router
+  static constexpr int XI = XB / 8192;               // DMA instructions per wave per chunk, x
+  static constexpr int WI = 16 * TE * WROW / 8192;   // ... router
   static constexpr int DMA = XI + WI;
 };
 
@@ -537,7 +538,7 @@ __device__ __forceinline__ void rl_dma(Src&& src, int row0, unsigned char* lds_r
 }
 
 template <typename XT, int TE>
-__global__ __launch_bounds__(256, 1) void route_logits_kernel(const XT* __restrict__ x, int64_t N, int H,
+__global__ __launch_bounds__(512, 1) void route_logits_kernel(const XT* __restrict__ x, int64_t N, int H,
                                                               const float* __restrict__ router, int Epad,
                                                               const float* __restrict__ bias, int E,
                                                               float* __restrict__ logits_out,
@@ -546,10 +547,11 @@ __global__ __launch_bounds__(256, 1) void route_logits_kernel(const XT* __restri
   using R = Rl<XT, TE>;
   extern __shared__ __align__(16) unsigned char smem[];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int kq = w & 3, ta = w >> 2;  // this wave's K block of a chunk and token tile
   const int64_t tok0 = (int64_t)blockIdx.x * (16 * RL_TT);
   const int e0 = (int)blockIdx.y * (16 * TE);
   if (zero && blockIdx.x == 0 && blockIdx.y == 0)
-    for (int i = tid; i < nzero; i += 256) zero[i] = 0u;
+    for (int i = tid; i < nzero; i += 512) zero[i] = 0u;
   const int nch = H / RL_KC;
   auto issue = [&](int c) {
     const int cc = c < nch ? c : nch - 1;  // past the end: the last chunk again, never read
@@ -557,12 +559,12 @@ __global__ __launch_bounds__(256, 1) void route_logits_kernel(const XT* __restri
     const int k0 = cc * RL_KC;
 #pragma unroll
     for (int i = 0; i < R::XI; ++i) {
-      const int row0 = (4 * i + w) * (1024 / R::XROW);
+      const int row0 = (8 * i + w) * (1024 / R::XROW);
       rl_dma<R::XROW, XT>([&](int r) { return x + min(tok0 + r, N - 1) * H + k0; }, row0, st, lane);
     }
 #pragma unroll
     for (int i = 0; i < R::WI; ++i) {
-      const int row0 = (4 * i + w) * (1024 / R::WROW);
+      const int row0 = (8 * i + w) * (1024 / R::WROW);
       rl_dma<R::WROW, float>([&](int r) { return router + (int64_t)min(e0 + r, Epad - 1) * H + k0; }, row0,
                              st + R::XB, lane);
     }
@@ -571,18 +573,16 @@ __global__ __launch_bounds__(256, 1) void route_logits_kernel(const XT* __restri
   for (int c = 0; c < RL_STAGES - 1; ++c) issue(c);
 
   const int t_l = lane & 15, g = lane >> 4;
-  f32x4_t acc[RL_TT][TE];
+  f32x4_t acc[TE];
 #pragma unroll
-  for (int a = 0; a < RL_TT; ++a)
-#pragma unroll
-    for (int b = 0; b < TE; ++b) acc[a][b] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+  for (int b = 0; b < TE; ++b) acc[b] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
   for (int c = 0; c < nch; ++c) {
     asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(R::DMA * (RL_STAGES - 2)) : "memory");
     issue(c + RL_STAGES - 1);
     const unsigned char* st = smem + (c % RL_STAGES) * R::STAGE;
     // x as bf16 for the GEMMs (fp32 x, first expert group only): thread -> row tid / 8,
     // 16 values at (tid % 8) * 16
-    if (sizeof(XT) == 4 && xbf_out && blockIdx.y == 0) {
+    if (sizeof(XT) == 4 && xbf_out && blockIdx.y == 0 && tid < 256) {
       const int r = tid >> 3, k16 = (tid & 7) * 16;
       const int64_t t = tok0 + r;
       if (t < N) {
@@ -598,30 +598,29 @@ __global__ __launch_bounds__(256, 1) void route_logits_kernel(const XT* __restri
         dst[1] = make_uint4(pk[4], pk[5], pk[6], pk[7]);
       }
     }
-    float xv[RL_TT][8], wv[TE][8];
-#pragma unroll
-    for (int a = 0; a < RL_TT; ++a) {
-      const int r = 16 * a + t_l;
+    float xv[8], wv[TE][8];
+    {
+      const int r = 16 * ta + t_l;
       if (sizeof(XT) == 4) {
-        const int c0 = 8 * w + 2 * g;
+        const int c0 = 8 * kq + 2 * g;
         const float4 v0 = *(const float4*)(st + r * R::XROW + ((c0 ^ (r & 15)) << 4));
         const float4 v1 = *(const float4*)(st + r * R::XROW + (((c0 + 1) ^ (r & 15)) << 4));
-        xv[a][0] = v0.x; xv[a][1] = v0.y; xv[a][2] = v0.z; xv[a][3] = v0.w;
-        xv[a][4] = v1.x; xv[a][5] = v1.y; xv[a][6] = v1.z; xv[a][7] = v1.w;
+        xv[0] = v0.x; xv[1] = v0.y; xv[2] = v0.z; xv[3] = v0.w;
+        xv[4] = v1.x; xv[5] = v1.y; xv[6] = v1.z; xv[7] = v1.w;
       } else {
-        const uint4 u = *(const uint4*)(st + r * R::XROW + (((4 * w + g) ^ (r & 15)) << 4));
+        const uint4 u = *(const uint4*)(st + r * R::XROW + (((4 * kq + g) ^ (r & 15)) << 4));
         const uint32_t uw[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          xv[a][2 * i] = __uint_as_float(uw[i] << 16);
-          xv[a][2 * i + 1] = __uint_as_float(uw[i] & 0xffff0000u);
+          xv[2 * i] = __uint_as_float(uw[i] << 16);
+          xv[2 * i + 1] = __uint_as_float(uw[i] & 0xffff0000u);
         }
       }
     }
 #pragma unroll
     for (int b = 0; b < TE; ++b) {
       const int r = 16 * b + t_l;
-      const int c0 = 8 * w + 2 * g;
+      const int c0 = 8 * kq + 2 * g;
       const unsigned char* ws = st + R::XB + r * R::WROW;
       const float4 v0 = *(const float4*)(ws + ((c0 ^ (r & 15)) << 4));
       const float4 v1 = *(const float4*)(ws + (((c0 + 1) ^ (r & 15)) << 4));
@@ -631,23 +630,18 @@ __global__ __launch_bounds__(256, 1) void route_logits_kernel(const XT* __restri
 #pragma unroll
     for (int j = 0; j < 8; ++j)
 #pragma unroll
-      for (int a = 0; a < RL_TT; ++a)
-#pragma unroll
-        for (int b = 0; b < TE; ++b)
-          acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[a][j], wv[b][j], acc[a][b], 0, 0, 0);
+      for (int b = 0; b < TE; ++b) acc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[j], wv[b][j], acc[b], 0, 0, 0);
   }
   // wave partials through LDS (stage memory is free once every wave has passed here)
   asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-  float* part = (float*)smem;  // [4][32][16 TE]
+  float* part = (float*)smem;  // [4 K blocks][32 tokens][16 TE]
   constexpr int NE = 16 * TE, NT = 16 * RL_TT;
 #pragma unroll
-  for (int a = 0; a < RL_TT; ++a)
+  for (int b = 0; b < TE; ++b)
 #pragma unroll
-    for (int b = 0; b < TE; ++b)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) part[(w * NT + 16 * a + 4 * g + q) * NE + 16 * b + t_l] = acc[a][b][q];
+    for (int q = 0; q < 4; ++q) part[(kq * NT + 16 * ta + 4 * g + q) * NE + 16 * b + t_l] = acc[b][q];
   __syncthreads();
-  for (int i = tid; i < NT * NE; i += 256) {
+  for (int i = tid; i < NT * NE; i += 512) {
     const int r = i / NE, ce = i - r * NE;
     const int64_t t = tok0 + r;
     const int e = e0 + ce;
@@ -670,7 +664,7 @@ int pp_route_logits_dense(const void* x, int x_dtype, int64_t N, int H, const fl
   const int te = E <= 16 ? 1 : E <= 32 ? 2 : 3;
   const dim3 grid((unsigned)((N + 16 * RL_TT - 1) / (16 * RL_TT)), (unsigned)((E + 16 * te - 1) / (16 * te)));
 #define PP_RL(XT, TE)                                                                                           \
-  route_logits_kernel<XT, TE><<<grid, 256, RL_STAGES * Rl<XT, TE>::STAGE, st>>>(                                \
+  route_logits_kernel<XT, TE><<<grid, 512, RL_STAGES * Rl<XT, TE>::STAGE, st>>>(                                \
       (const XT*)x, N, H, router, Epad, bias, E, logits_out, xbf_out, zero, nzero)
   if (x_dtype == PP_DTYPE_F32) {
     if (te == 1) PP_RL(float, 1);

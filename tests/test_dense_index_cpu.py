@@ -233,6 +233,7 @@ def test_route_logits_addresses(xs, N, H, E):
     Epad = (E + 15) // 16 * 16
     XROW, WROW = KC * xs, KC * 4
     XB = 16 * TT * XROW
+    NWV = 8
     lanes = np.arange(64)
     for bx in range((N + 31) // 32):
         for by in range((E + 16 * TE - 1) // (16 * TE)):
@@ -240,44 +241,45 @@ def test_route_logits_addresses(xs, N, H, E):
             for c in range(H // KC):
                 k0 = c * KC
                 lds = {}
-                for w in range(4):
-                    for i in range(XB // 4096):
+                for w in range(NWV):
+                    for i in range(XB // (1024 * NWV)):
                         rpi = 1024 // XROW
                         cpr = XROW // 16
-                        row = (4 * i + w) * rpi + lanes // cpr
+                        row = (NWV * i + w) * rpi + lanes // cpr
                         gc = (lanes % cpr) ^ (row & 15)
                         tok = np.minimum(tok0 + row, N - 1)
                         el = tok * H + k0 + gc * (16 // xs)
                         assert el.min() >= 0 and (el + 16 // xs).max() <= N * H
                         for ln in range(64):
-                            lds[(4 * i + w) * 1024 + ln * 16] = ("x", int(tok[ln]), int(k0 + gc[ln] * (16 // xs)))
-                    for i in range(16 * TE * WROW // 4096):
-                        row = (4 * i + w) * 2 + lanes // 32
+                            lds[(NWV * i + w) * 1024 + ln * 16] = ("x", int(tok[ln]), int(k0 + gc[ln] * (16 // xs)))
+                    for i in range(16 * TE * WROW // (1024 * NWV)):
+                        row = (NWV * i + w) * 2 + lanes // 32
                         gc = (lanes % 32) ^ (row & 15)
                         er = np.minimum(e0 + row, Epad - 1)
                         el = er * H + k0 + gc * 4
                         assert el.min() >= 0 and (el + 4).max() <= Epad * H
                         for ln in range(64):
-                            lds[XB + (4 * i + w) * 1024 + ln * 16] = ("w", int(er[ln]), int(k0 + gc[ln] * 4))
-                for w in range(4):
+                            lds[XB + (NWV * i + w) * 1024 + ln * 16] = ("w", int(er[ln]), int(k0 + gc[ln] * 4))
+                assert len(lds) == (XB + 16 * TE * WROW) // 16  # every 16-byte slot written once
+                for w in range(NWV):
+                    kq, ta = w & 3, w >> 2
                     for lane in range(64):
                         t_l, g = lane & 15, lane >> 4
-                        for a in range(TT):
-                            r = 16 * a + t_l
-                            if xs == 4:
-                                c0 = 8 * w + 2 * g
-                                for h, cc in enumerate((c0, c0 + 1)):
-                                    src = lds[r * XROW + ((cc ^ (r & 15)) << 4)]
-                                    assert src == ("x", min(tok0 + r, N - 1), k0 + 32 * w + 8 * g + 4 * h)
-                            else:
-                                src = lds[r * XROW + (((4 * w + g) ^ (r & 15)) << 4)]
-                                assert src == ("x", min(tok0 + r, N - 1), k0 + 32 * w + 8 * g)
-                        for b in range(TE):
-                            r = 16 * b + t_l
-                            c0 = 8 * w + 2 * g
+                        r = 16 * ta + t_l
+                        if xs == 4:
+                            c0 = 8 * kq + 2 * g
                             for h, cc in enumerate((c0, c0 + 1)):
-                                src = lds[XB + r * WROW + ((cc ^ (r & 15)) << 4)]
-                                assert src == ("w", min(e0 + r, Epad - 1), k0 + 32 * w + 8 * g + 4 * h)
+                                src = lds[r * XROW + ((cc ^ (r & 15)) << 4)]
+                                assert src == ("x", min(tok0 + r, N - 1), k0 + 32 * kq + 8 * g + 4 * h)
+                        else:
+                            src = lds[r * XROW + (((4 * kq + g) ^ (r & 15)) << 4)]
+                            assert src == ("x", min(tok0 + r, N - 1), k0 + 32 * kq + 8 * g)
+                        for b in range(TE):
+                            rb = 16 * b + t_l
+                            c0 = 8 * kq + 2 * g
+                            for h, cc in enumerate((c0, c0 + 1)):
+                                src = lds[XB + rb * WROW + ((cc ^ (rb & 15)) << 4)]
+                                assert src == ("w", min(e0 + rb, Epad - 1), k0 + 32 * kq + 8 * g + 4 * h)
 
 
 @pytest.mark.parametrize("mode", [0, 1])
