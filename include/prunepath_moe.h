@@ -40,7 +40,7 @@ extern "C" {
 
 /* Message of the last error on this thread ("" if none). */
 const char* pp_last_error(void);
-/* ABI version (incremented on any signature change): 2. */
+/* ABI version (incremented on any signature or workspace-layout change): 3. */
 int pp_abi_version(void);
 
 /* ------------------------------------------------------------------------- *
@@ -141,7 +141,11 @@ int pp_bucket(const uint8_t* mask, const float* gates, int64_t n_tokens, int E, 
  * after a bounded spin with error bit 1 and NaN outputs, never a hang.
  * The workspace (pp_decode_workspace_bytes) must be zeroed once with
  * pp_decode_workspace_init before the first call; every call leaves it ready for
- * the next one. Calls that share a workspace must be ordered (same stream);
+ * the next one. The init call also writes a layout tag into the workspace (the
+ * library's workspace layout and the H it was sized for, pp_decode_layout_tag): a call
+ * whose tag differs (a workspace initialised by another build of the library or for
+ * another H, or never initialised) writes nothing into the workspace but error bit 8,
+ * and NaN outputs. Calls that share a workspace must be ordered (same stream);
  * overlapping calls on one workspace race. After a call the workspace holds the
  * call's logits, selected experts and gates (struct pp_decode_state below).
  * grid = number of workgroups (0 = automatic).
@@ -154,10 +158,13 @@ typedef struct pp_decode_state {
                              (every later call on the workspace writes NaN), 2 the selection
                              was not a permutation of the experts, 4 a workgroup partial sum
                              was not finite or reached 2^30 (beyond the fixed-point
-                             reduction); stays set until pp_decode_workspace_init clears it */
+                             reduction), 8 the workspace's layout tag did not match the call
+                             (nothing else written); stays set until pp_decode_workspace_init
+                             clears it */
   int32_t k;              /* experts selected by the last call */
   uint32_t error_call;    /* call epoch + 1 of the last failed call: that call wrote NaN outputs */
-  int32_t pad[2];
+  uint32_t layout;        /* layout tag written by pp_decode_workspace_init (pp_decode_layout_tag) */
+  int32_t pad;
   float logits[PP_MAX_EXPERTS];
   int32_t sel_ids[PP_MAX_EXPERTS];   /* selected experts, descending probability */
   float sel_gates[PP_MAX_EXPERTS];   /* sigmoid(logit) of each selected expert */
@@ -165,6 +172,13 @@ typedef struct pp_decode_state {
 
 size_t pp_decode_workspace_bytes(int H, int E);
 int pp_decode_workspace_init(void* workspace, int H, int E, void* stream);
+/* The layout tag pp_decode_workspace_init writes for hidden size H (0 for an H outside
+ * the shape limits). No counterpart in the reference (its decode keeps no workspace). */
+uint32_t pp_decode_layout_tag(int H);
+/* Checks a host copy of a workspace's state header against this library's layout for H:
+ * PP_OK, or PP_ERR_INVALID (with the tags in pp_last_error) when the kernels would refuse
+ * the workspace. No counterpart in the reference. */
+int pp_decode_state_check(const pp_decode_state* state, int H);
 int pp_moe_decode(const void* x, int x_dtype, int H, const float* router_packed,
                   const float* bias, int E, int G, float tau, const void* packed,
                   void* out_bf16, void* workspace, int grid, void* stream);
@@ -177,10 +191,24 @@ int pp_moe_decode(const void* x, int x_dtype, int H, const float* router_packed,
  * ends). Limits: H <= 4096, E <= 256 (the library's shape limits; PP_ERR_UNSUPPORTED
  * beyond). Every call on a GPU shares that GPU's array: calls that overlap on one GPU
  * (different streams, threads or processes' graphs replayed concurrently) race; calls
- * ordered on one stream of any shapes are safe. The call allocates and frees nothing. */
+ * ordered on one stream of any shapes are safe. The call allocates and frees nothing.
+ * The first call on a GPU initialises the array and must not be captured into a graph
+ * (PP_ERR_INVALID while the stream is capturing, nothing launched): make one eager call,
+ * or call pp_decode_noalloc_reset, before capturing. Error bits 1, 2 and 8 of the
+ * array's state are sticky as in a caller's workspace (every later call writes NaN);
+ * pp_decode_noalloc_reset clears them. */
 int pp_moe_decode_noalloc(const void* x, int x_dtype, int H, const float* router_packed,
                           const float* bias, int E, int G, float tau, const void* packed,
                           void* out_bf16, int grid, void* stream);
+/* Re-initialises the current GPU's pp_moe_decode_noalloc array (a fill kernel on `stream`,
+ * no allocation; initialises it on first use). No counterpart in the reference: for the
+ * callers of pp_moe_decode_noalloc, which cannot reach the array to re-initialise it
+ * after an error. error_out (may be NULL): the error bits the array held, read before
+ * the reset (a synchronous copy: waits for the stream's earlier work). error_in: error
+ * bits the array holds after the reset; 0, except to test a caller's error handling
+ * (bit 1 makes every later call write NaN until the next reset). PP_ERR_INVALID while
+ * `stream` is capturing. Must not overlap decode calls on the same GPU. */
+int pp_decode_noalloc_reset(uint32_t* error_out, uint32_t error_in, void* stream);
 
 /* Small-batch decode: 1 <= N <= 64 tokens in one launch. Replaces, for such batches,
  * TauSparseMoE.forward_prefill (src/tl_kernel_optimized_Ultimate_PanGU.py:532-604: route,

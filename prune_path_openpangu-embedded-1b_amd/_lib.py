@@ -48,10 +48,13 @@ SIGNATURES = {
                           c_void_p, c_void_p, c_void_p, c_void_p]),
     "pp_decode_workspace_bytes": (c_size_t, [c_int, c_int]),
     "pp_decode_workspace_init": (c_int, [c_void_p, c_int, c_int, c_void_p]),
+    "pp_decode_layout_tag": (ctypes.c_uint32, [c_int]),
+    "pp_decode_state_check": (c_int, [c_void_p, c_int]),
     "pp_moe_decode": (c_int, [c_void_p, c_int, c_int, c_void_p, c_void_p, c_int, c_int, c_float, c_void_p,
                               c_void_p, c_void_p, c_int, c_void_p]),
     "pp_moe_decode_noalloc": (c_int, [c_void_p, c_int, c_int, c_void_p, c_void_p, c_int, c_int, c_float,
                                       c_void_p, c_void_p, c_int, c_void_p]),
+    "pp_decode_noalloc_reset": (c_int, [c_void_p, ctypes.c_uint32, c_void_p]),
     "pp_decode_batch_workspace_bytes": (c_size_t, [c_int, c_int, c_int]),
     "pp_moe_decode_batch": (c_int, [c_void_p, c_int, c_int64, c_int, c_void_p, c_void_p, c_int, c_int, c_float,
                                     c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_void_p]),

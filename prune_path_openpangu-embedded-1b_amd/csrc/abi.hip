@@ -36,4 +36,4 @@ int pp_device_cus() {
 }
 
 extern "C" const char* pp_last_error(void) { return g_err; }
-extern "C" int pp_abi_version(void) { return 2; }
+extern "C" int pp_abi_version(void) { return 3; }

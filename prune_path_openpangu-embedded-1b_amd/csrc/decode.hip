@@ -31,6 +31,7 @@
 // completion (s_waitcnt vmcnt(0)) before the dependent atomic. Agent-scope fences are
 // avoided on purpose: on gfx950 each one writes back and invalidates the L2, which
 // hundreds of workgroups cannot afford inside a 10 us kernel.
+#include <cstddef>
 #include <mutex>
 
 #include "pp_common.h"
@@ -49,6 +50,17 @@ struct DecNW {
 
 static constexpr size_t dec_acc_offset() { return (sizeof(pp_decode_state) + 255) / 256 * 256; }
 
+// Layout tag of a workspace (pp_decode_state::layout): the version of the workspace layout
+// (the offsets and sizes below; raised whenever any of them changes) and the accumulator
+// stride hs it was initialised for. Every kernel compares the workspace's tag with the one
+// its launch expects before its first write into the workspace.
+#define DEC_LAYOUT_VERSION 3u
+static constexpr uint32_t dec_layout_tag(int hs) {
+  return 0xD5000000u | ((DEC_LAYOUT_VERSION & 0x7ffu) << 13) | ((uint32_t)hs & 0x1fffu);
+}
+static_assert(offsetof(pp_decode_state, layout) == 24 && offsetof(pp_decode_state, error) == 12,
+              "pp_decode_state: the header words every layout version keeps in place");
+
 
 __device__ __forceinline__ void vm_wait() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 template <typename T>
@@ -61,6 +73,17 @@ __device__ __forceinline__ void st_rlx(T* p, T v) {
 }
 __device__ __forceinline__ uint32_t add_rlx(uint32_t* p, uint32_t v) {
   return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The workspace's layout tag differs from the launch's: the workgroup ends without writing
+// into the workspace; workgroup 0 writes NaN to the n outputs and sets error bit 8 (the
+// state header sits at the start of every layout). DMAs into LDS issued so far are waited
+// for before the workgroup ends. Every workgroup reads the same tag, so all of them end here.
+__device__ __forceinline__ void dec_refuse(bf16_t* out, int n, pp_decode_state* st, int b, int tid, int nt) {
+  vm_wait();
+  if (b != 0) return;
+  for (int i = tid; i < n; i += nt) out[i] = (bf16_t)0x7fc0;
+  if (tid == 0) __hip_atomic_fetch_or(&st->error, 8u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Accumulators hold 64-bit fixed point (value * 2^32, two's complement). Integer
@@ -240,7 +263,7 @@ template <typename XT, int CPL, bool LOCAL>
 __global__ __launch_bounds__(DecNW<CPL>::NT) void decode_kernel(
     const XT* __restrict__ x, int H, const float* __restrict__ router, const float* __restrict__ bias,
     int E, int G, float tau, const bf16_t* __restrict__ rows, bf16_t* __restrict__ out,
-    pp_decode_state* __restrict__ st, dec_acc_t* __restrict__ acc, int hs, int hclear) {
+    pp_decode_state* __restrict__ st, dec_acc_t* __restrict__ acc, int hs, int hclear, uint32_t layout) {
   constexpr int NW = DecNW<CPL>::NW, NT = DecNW<CPL>::NT;
   extern __shared__ __align__(16) float red[];  // [NW][H] wave partials
   __shared__ SelScratch ss;
@@ -257,6 +280,7 @@ __global__ __launch_bounds__(DecNW<CPL>::NT) void decode_kernel(
   const int W = gridDim.x, b = blockIdx.x;
   const int HC = H >> 3;  // 16-byte chunks per row
   const uint32_t epoch = ld_rlx(&st->router_ticket);
+  const uint32_t lay = ld_rlx(&st->layout);  // compared before the first workspace write
 
   // x for the stream goes global -> LDS by DMA now (no registers held through the
   // routing); the stream reads it from LDS. Loaded at the stream's start, x cost ~3 us at
@@ -273,6 +297,10 @@ __global__ __launch_bounds__(DecNW<CPL>::NT) void decode_kernel(
   if (LOCAL) {
     // ---------------- every workgroup routes the token itself
     local_logits<XT, CPL>(x, H, router, bias, E, lg_s, tid);
+    if (lay != layout) {
+      dec_refuse(out, H, st, b, tid, NT);
+      return;
+    }
     if (wv == 0) {
       select_small<16>([&](int j) { return lg_s[j]; }, E, tau, &ss, lane);
       const int k = ss.k;
@@ -319,6 +347,12 @@ __global__ __launch_bounds__(DecNW<CPL>::NT) void decode_kernel(
       sacc = wave_sum(sacc);
       if (lane == 0) red4[wv] = sacc;
       __syncthreads();
+    }
+    if (lay != layout) {
+      dec_refuse(out, H, st, b, tid, NT);
+      return;
+    }
+    if (b < E) {
       if (tid < DEC_SLOT_REPS) {  // one copy of the slot per replica, thread r the r-th
         float l = red4[0];
 #pragma unroll
@@ -759,7 +793,7 @@ template <typename XT, int CPL>
 __global__ __launch_bounds__(512) void decode16_kernel(
     const XT* __restrict__ x, const float* __restrict__ router, const float* __restrict__ bias, int G, float tau,
     const bf16_t* __restrict__ gu, int rec_h, const bf16_t* __restrict__ down_t, bf16_t* __restrict__ out,
-    pp_decode_state* __restrict__ st, uint32_t* __restrict__ banks, int rp, int slot_bytes) {
+    pp_decode_state* __restrict__ st, uint32_t* __restrict__ banks, int rp, int slot_bytes, uint32_t layout) {
   constexpr int NW = 8, NT = 512, H = 512 * CPL, HC = H / 8;
   extern __shared__ __align__(16) unsigned char dn_s[];  // [16][slot_bytes]: down rows of a pass
   __shared__ __align__(16) float part_s[16 * NW];
@@ -772,9 +806,9 @@ __global__ __launch_bounds__(512) void decode16_kernel(
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int W = gridDim.x, b = blockIdx.x;
   const uint32_t epoch = ld_rlx(&st->epoch16);
+  const uint32_t lay = ld_rlx(&st->layout);  // compared before the first workspace write
   uint32_t* bank = banks + (size_t)(epoch & 1u) * DEC2_BANK_WORDS;
   if (tid == 0) {
-    st_rlx(&bank[DEC2_ALIVE + b], 1u);  // alive
     fail_s = (ld_rlx(&st->error) & 1u) != 0u;  // an earlier wait timed out: NaN until re-initialised
     ready_s = 0;
   }
@@ -786,6 +820,11 @@ __global__ __launch_bounds__(512) void decode16_kernel(
   const int j = lane & 15;
   const float xl = dec16_logits<XT, CPL, NW>(x, router, bias, part_s, lane, wv);
   const float m = row16_max(xl);
+  if (lay != layout) {
+    dec_refuse(out, H, st, b, tid, NT);
+    return;
+  }
+  if (tid == 0) st_rlx(&bank[DEC2_ALIVE + b], 1u);  // alive (has read the epoch)
 
   int h0, h1;  // output rows of this workgroup
   pp_split((uint32_t)H, (uint32_t)W, (uint32_t)b, h0, h1);
@@ -1017,7 +1056,7 @@ template <typename XT, int CPL, bool LOCAL>
 __global__ __launch_bounds__(512) void decode2p_kernel(
     const XT* __restrict__ x, int H, const float* __restrict__ router, const float* __restrict__ bias, int E,
     int G, float tau, const bf16_t* __restrict__ gu, const bf16_t* __restrict__ down_t, bf16_t* __restrict__ out,
-    pp_decode_state* __restrict__ st, uint32_t* __restrict__ banks, int rp) {
+    pp_decode_state* __restrict__ st, uint32_t* __restrict__ banks, int rp, uint32_t layout) {
   constexpr int NW = 8, NT = 512, NS = NW - 1;
   extern __shared__ __align__(16) unsigned char dn_s[];  // down rows of a pass: [rank][row][G] bf16 + one pad chunk per rank
   __shared__ __align__(16) float act_s[DEC2_RS + 4 * PP_MAX_EXPERTS];  // [rank][G + 4]: padded rows
@@ -1032,44 +1071,46 @@ __global__ __launch_bounds__(512) void decode2p_kernel(
   const int W = gridDim.x, b = blockIdx.x;
   const int HC = H >> 3;
   const uint32_t epoch = ld_rlx(&st->epoch16);
+  const uint32_t lay = ld_rlx(&st->layout);  // compared before the first workspace write
   uint32_t* bank = banks + (size_t)(epoch & 1u) * DEC2_BANK_WORDS;
-  if (tid == 0) {
-    st_rlx(&bank[DEC2_ALIVE + b], 1u);
-    fail_s = (ld_rlx(&st->error) & 1u) != 0u;  // an earlier wait timed out: NaN until re-initialised
-  }
+  if (tid == 0) fail_s = (ld_rlx(&st->error) & 1u) != 0u;  // an earlier wait timed out: NaN until re-initialised
   const uint4 zero4 = make_uint4(0, 0, 0, 0);
   uint4 xb[CPL];  // x as packed bf16 for the records
 #pragma unroll
   for (int c = 0; c < CPL; ++c) xb[c] = lane + 64 * c < HC ? load_x8_bf16<XT>(x, lane + 64 * c) : zero4;
 
   // ---- logits
-  if (LOCAL) {
-    local_logits<XT, CPL>(x, H, router, bias, E, lg_s, tid);
-  } else {
+  if (LOCAL) local_logits<XT, CPL>(x, H, router, bias, E, lg_s, tid);
+  if (!LOCAL && b < E) {  // logit b: every element loaded before the first FMA, added in k order
+    constexpr int KPT = 4096 / NT;
+    float xv[KPT], wr[KPT];
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+      const int kk = tid + i * NT;
+      xv[i] = kk < H ? load_as_f32<XT>(x, kk) : 0.0f;
+      wr[i] = kk < H ? router[(int64_t)b * H + kk] : 0.0f;
+    }
+    float sacc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < KPT; ++i)
+      if (tid + i * NT < H) sacc = __builtin_fmaf(xv[i], wr[i], sacc);
+    sacc = wave_sum_dpp(sacc);  // fixed order: rows by DPP, then the four row totals
+    if (lane == 0) red_s[wv] = sacc;
+    __syncthreads();
+  }
+  if (lay != layout) {
+    dec_refuse(out, H, st, b, tid, NT);
+    return;
+  }
+  if (tid == 0) st_rlx(&bank[DEC2_ALIVE + b], 1u);  // alive (has read the epoch)
+  if (!LOCAL) {
     uint32_t* lw = bank + DEC2_LOGITS;  // [DEC2_LREPS][PP_MAX_EXPERTS]
-    if (b < E) {  // logit b: every element loaded before the first FMA, added in k order
-      constexpr int KPT = 4096 / NT;
-      float xv[KPT], wr[KPT];
+    if (b < E && tid < DEC2_LREPS) {
+      float l = red_s[0];
 #pragma unroll
-      for (int i = 0; i < KPT; ++i) {
-        const int kk = tid + i * NT;
-        xv[i] = kk < H ? load_as_f32<XT>(x, kk) : 0.0f;
-        wr[i] = kk < H ? router[(int64_t)b * H + kk] : 0.0f;
-      }
-      float sacc = 0.0f;
-#pragma unroll
-      for (int i = 0; i < KPT; ++i)
-        if (tid + i * NT < H) sacc = __builtin_fmaf(xv[i], wr[i], sacc);
-      sacc = wave_sum_dpp(sacc);  // fixed order: rows by DPP, then the four row totals
-      if (lane == 0) red_s[wv] = sacc;
-      __syncthreads();
-      if (tid < DEC2_LREPS) {
-        float l = red_s[0];
-#pragma unroll
-        for (int w = 1; w < NW; ++w) l = __fadd_rn(l, red_s[w]);
-        if (bias) l = __fadd_rn(l, bias[b]);
-        st_rlx(&lw[tid * PP_MAX_EXPERTS + b], dec2_word(l));
-      }
+      for (int w = 1; w < NW; ++w) l = __fadd_rn(l, red_s[w]);
+      if (bias) l = __fadd_rn(l, bias[b]);
+      st_rlx(&lw[tid * PP_MAX_EXPERTS + b], dec2_word(l));
     }
     const uint32_t* rl = lw + (b % DEC2_LREPS) * PP_MAX_EXPERTS;
     if (tid < E) {  // E <= 256 < NT: one word per thread, bounded wait
@@ -1408,7 +1449,7 @@ __global__ __launch_bounds__(512) void decodeb_kernel(
     const XT* __restrict__ x, int N, const float* __restrict__ router, const float* __restrict__ bias, int G,
     float tau, const bf16_t* __restrict__ gu, const bf16_t* __restrict__ down_t, bf16_t* __restrict__ out,
     float* __restrict__ logits_out, uint8_t* __restrict__ mask_out, pp_decode_state* __restrict__ st,
-    unsigned char* __restrict__ bstate, unsigned char* __restrict__ bw, int rows_pp) {
+    unsigned char* __restrict__ bstate, unsigned char* __restrict__ bw, int rows_pp, uint32_t layout) {
   constexpr int NW = 8, NT = 512, H = 512 * CPL, HC = H / 8;
   constexpr int DP = CPL < 3 ? CPL : 3;  // gate/up stages in flight per wave (CPL K-blocks per wave)
   extern __shared__ __align__(16) unsigned char smem[];  // rings | later: reduction area, down rows
@@ -1424,6 +1465,7 @@ __global__ __launch_bounds__(512) void decodeb_kernel(
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int W = gridDim.x, b = blockIdx.x;
   const uint32_t tag = ld_rlx(&st->epochb) + 1u;
+  const uint32_t lay = ld_rlx(&st->layout);  // compared before the first workspace write
   bool fail = (ld_rlx(&st->error) & 1u) != 0u;  // an earlier wait timed out: NaN until re-initialised
   const DecbLayout Lb = decb_layout(H, G);
   unsigned long long* selg = (unsigned long long*)bstate;
@@ -1474,6 +1516,19 @@ __global__ __launch_bounds__(512) void decodeb_kernel(
       for (int j = 0; j < DP; ++j) issue_w(8 * sp0, min(DECB_NB, 8 * (sp1 - sp0)), j, [](int e) { return e; });
   };
   if (b >= N) issue_spec();
+  // a workspace of another layout: NaN outputs (logits NaN, masks 0), nothing written into it
+  auto refuse = [&]() {
+    dec_refuse(out, N * H, st, b, tid, NT);
+    if (b == 0)
+      for (int i = tid; i < N * 16; i += NT) {
+        if (logits_out != nullptr) logits_out[i] = __uint_as_float(0x7fc00000u);
+        if (mask_out != nullptr) mask_out[i] = 0;
+      }
+  };
+  if (b >= N && lay != layout) {
+    refuse();
+    return;
+  }
 
   // ---- A: routing of token b
   if (b < N) {
@@ -1490,6 +1545,10 @@ __global__ __launch_bounds__(512) void decodeb_kernel(
     }
     vm_wait();
     __syncthreads();  // x is stored: the gates may go out
+    if (lay != layout) {
+      refuse();
+      return;
+    }
     if (wv == 0 && lane < 16) {
       const uint32_t gb = __float_as_uint(sel ? pg_s[16 + lane] : -1.0f);
       __hip_atomic_store(&selg[b * 16 + lane], ((unsigned long long)tag << 32) | gb, __ATOMIC_RELAXED,
@@ -1736,9 +1795,11 @@ __global__ __launch_bounds__(512) void decodeb_kernel(
   }
 }
 
-__global__ void decode_ws_clear_kernel(uint32_t* p, size_t n_words) {
+// Zeroes a workspace of n_words words, then its state header holds `layout` and `error`.
+__global__ void decode_ws_clear_kernel(uint32_t* p, size_t n_words, uint32_t layout, uint32_t error) {
+  constexpr size_t kLayout = offsetof(pp_decode_state, layout) / 4, kError = offsetof(pp_decode_state, error) / 4;
   for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n_words; i += (size_t)gridDim.x * blockDim.x)
-    p[i] = 0u;
+    p[i] = i == kLayout ? layout : i == kError ? error : 0u;
 }
 
 // Workspace: state | decode_kernel: 2 x DEC_NCOPY x hs fixed-point accumulators,
@@ -1766,8 +1827,24 @@ extern "C" int pp_decode_workspace_init(void* workspace, int H, int E, void* str
   if (rc) return rc;
   PP_REQUIRE(workspace, PP_ERR_INVALID, "pp_decode_workspace_init: null workspace");
   size_t words = pp_decode_workspace_bytes(H, E) / 4;
-  decode_ws_clear_kernel<<<64, 256, 0, (hipStream_t)stream>>>((uint32_t*)workspace, words);
+  decode_ws_clear_kernel<<<64, 256, 0, (hipStream_t)stream>>>((uint32_t*)workspace, words, dec_layout_tag(H), 0u);
   return pp_check_launch("pp_decode_workspace_init");
+}
+
+extern "C" uint32_t pp_decode_layout_tag(int H) {
+  if (H < 128 || H > 4096 || H % 128 != 0) return 0u;  // the shape limits of every entry point
+  return dec_layout_tag(H);
+}
+
+extern "C" int pp_decode_state_check(const pp_decode_state* state, int H) {
+  PP_REQUIRE(state != nullptr, PP_ERR_INVALID, "pp_decode_state_check: null state");
+  const uint32_t want = pp_decode_layout_tag(H);
+  PP_REQUIRE(want != 0u, PP_ERR_INVALID, "pp_decode_state_check: H=%d outside the shape limits", H);
+  PP_REQUIRE(state->layout == want, PP_ERR_INVALID,
+             "pp_decode_state_check: workspace layout tag 0x%08x, this library expects 0x%08x for H=%d (a "
+             "workspace initialised by another build or for another H, or never initialised)",
+             state->layout, want, H);
+  return PP_OK;
 }
 
 // The published-logit mode needs its E router workgroups resident together (each
@@ -1814,7 +1891,7 @@ static int dec_capacity(const void* kern, int nt, size_t smem) {
 template <typename XT, bool LOCAL>
 static int launch_decode(int cpl, int grid, hipStream_t s, const XT* x, int H, const float* router,
                          const float* bias, int E, int G, float tau, const bf16_t* rows, bf16_t* out,
-                         pp_decode_state* st, dec_acc_t* acc, int hs, int hclear) {
+                         pp_decode_state* st, dec_acc_t* acc, int hs, int hclear, uint32_t layout) {
 #define PP_DEC_CASE(C)                                                                                  \
   case C: {                                                                                             \
     const size_t sm = (size_t)DecNW<C>::NW * H * sizeof(float);                                         \
@@ -1823,7 +1900,7 @@ static int launch_decode(int cpl, int grid, hipStream_t s, const XT* x, int H, c
       if (rc) return rc;                                                                                \
     }                                                                                                   \
     decode_kernel<XT, C, LOCAL><<<grid, DecNW<C>::NT, sm, s>>>(x, H, router, bias, E, G, tau, rows, out, st, acc, \
-                                                               hs, hclear);                              \
+                                                               hs, hclear, layout);                      \
   } break;
   switch (cpl) {
     PP_DEC_CASE(1)
@@ -1857,6 +1934,7 @@ static int decode_dispatch(const void* x, int x_dtype, int H, const float* route
                            int E, int G, float tau, const void* packed, void* out_bf16, pp_decode_state* st,
                            dec_acc_t* acc, int hs, int hclear, uint32_t* banks, int grid, hipStream_t s) {
   const int grid_in = grid;
+  const uint32_t layout = dec_layout_tag(hs);  // the workspace's tag its kernels expect
   if (grid == 0) grid = pp_device_cus();
   if (grid < E) grid = E;  // every expert has its router workgroup
   const int cpl = (H / 8 + 63) / 64;  // 16-byte chunks per lane per row (H <= 4096 -> <= 8)
@@ -1881,10 +1959,10 @@ static int decode_dispatch(const void* x, int x_dtype, int H, const float* route
     W = min(W, cap);                                                                                            \
     if (x_dtype == PP_DTYPE_F32)                                                                                \
       decode16_kernel<float, C><<<W, 512, smem, s>>>((const float*)x, router_packed, bias, G, tau, gu, 3, down_t,  \
-                                                     (bf16_t*)out_bf16, st, banks, rp, slot_bytes);            \
+                                                     (bf16_t*)out_bf16, st, banks, rp, slot_bytes, layout);    \
     else                                                                                                        \
       decode16_kernel<bf16_t, C><<<W, 512, smem, s>>>((const bf16_t*)x, router_packed, bias, G, tau, gu, 3, down_t, \
-                                                      (bf16_t*)out_bf16, st, banks, rp, slot_bytes);           \
+                                                      (bf16_t*)out_bf16, st, banks, rp, slot_bytes, layout);   \
   } break;
     switch (H / 512) {
       PP_DEC16_CASE(1)
@@ -1926,7 +2004,7 @@ static int decode_dispatch(const void* x, int x_dtype, int H, const float* route
         rc = PP_ERR_UNSUPPORTED;
         return;
       }
-      kern<<<W, 512, smem, s>>>(xp, H, router_packed, bias, E, G, tau, gu, down_t, o, st, banks, rp);
+      kern<<<W, 512, smem, s>>>(xp, H, router_packed, bias, E, G, tau, gu, down_t, o, st, banks, rp, layout);
     };
 #define PP_DEC2P_CASE(C)                                                                                           \
   case C:                                                                                                          \
@@ -1956,11 +2034,11 @@ static int decode_dispatch(const void* x, int x_dtype, int H, const float* route
   bf16_t* o = (bf16_t*)out_bf16;
   int rc;
   if (x_dtype == PP_DTYPE_F32) {
-    if (local) rc = launch_decode<float, true>(cpl, grid, s, (const float*)x, H, router_packed, bias, E, G, tau, rows, o, st, acc, hs, hclear);
-    else rc = launch_decode<float, false>(cpl, grid, s, (const float*)x, H, router_packed, bias, E, G, tau, rows, o, st, acc, hs, hclear);
+    if (local) rc = launch_decode<float, true>(cpl, grid, s, (const float*)x, H, router_packed, bias, E, G, tau, rows, o, st, acc, hs, hclear, layout);
+    else rc = launch_decode<float, false>(cpl, grid, s, (const float*)x, H, router_packed, bias, E, G, tau, rows, o, st, acc, hs, hclear, layout);
   } else {
-    if (local) rc = launch_decode<bf16_t, true>(cpl, grid, s, (const bf16_t*)x, H, router_packed, bias, E, G, tau, rows, o, st, acc, hs, hclear);
-    else rc = launch_decode<bf16_t, false>(cpl, grid, s, (const bf16_t*)x, H, router_packed, bias, E, G, tau, rows, o, st, acc, hs, hclear);
+    if (local) rc = launch_decode<bf16_t, true>(cpl, grid, s, (const bf16_t*)x, H, router_packed, bias, E, G, tau, rows, o, st, acc, hs, hclear, layout);
+    else rc = launch_decode<bf16_t, false>(cpl, grid, s, (const bf16_t*)x, H, router_packed, bias, E, G, tau, rows, o, st, acc, hs, hclear, layout);
   }
   if (rc) return rc;
   return pp_check_launch("pp_moe_decode");
@@ -2020,7 +2098,7 @@ extern "C" int pp_moe_decode_batch(const void* x, int x_dtype, int64_t n_tokens,
       return;
     }
     kern<<<W, 512, smem, s>>>(xp, N, router_packed, bias, G, tau, gu, down_t, (bf16_t*)out_bf16, logits_out, mask_out,
-                              st, bstate, (unsigned char*)batch_workspace, rp);
+                              st, bstate, (unsigned char*)batch_workspace, rp, dec_layout_tag(H));
   };
 #define PP_DECB_CASE(C)                                                                      \
   case C:                                                                                    \
@@ -2064,25 +2142,70 @@ static __device__ __align__(256) unsigned char scratch[kDecScratchBytes];
 static std::mutex g_scratch_mu;
 static void* g_scratch_ptr[64];
 
-// Device address of this device's scratch; the first call on a device also zeroes it
-// (a fill kernel on the caller's stream, ordered before the caller's decode).
-static int decode_scratch(hipStream_t s, void** out) {
+// The scratch is zeroed (and tagged) by a fill kernel on the caller's stream, ordered before
+// the caller's later work on it: at the first call on a device and at every reset. Never
+// while `s` is capturing: a captured fill would re-run at every replay of the graph, and a
+// graph replayed between eager calls would clear their error state.
+static int decode_scratch_not_capturing(hipStream_t s, const char* who) {
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  const hipError_t e = hipStreamIsCapturing(s, &cs);
+  PP_REQUIRE(e == hipSuccess, PP_ERR_HIP, "%s: hipStreamIsCapturing: %s", who, hipGetErrorString(e));
+  PP_REQUIRE(cs == hipStreamCaptureStatusNone, PP_ERR_INVALID,
+             "%s: the stream is capturing; the allocation-free decode scratch is initialised and reset by eager "
+             "calls only (make one pp_moe_decode_noalloc or pp_decode_noalloc_reset call before capturing)", who);
+  return PP_OK;
+}
+static int decode_scratch_fill(hipStream_t s, void* ptr, uint32_t error, const char* who) {
+  const int rc = decode_scratch_not_capturing(s, who);
+  if (rc) return rc;
+  decode_ws_clear_kernel<<<64, 256, 0, s>>>((uint32_t*)ptr, kDecScratchBytes / 4,
+                                            dec_layout_tag(PP_DECODE_SCRATCH_HS), error);
+  return pp_check_launch(who);
+}
+
+// Device address of this device's scratch (hipGetSymbolAddress once per device, with
+// that device current); `init` is set when this call initialised it.
+static int decode_scratch(hipStream_t s, void** out, bool* init) {
   int dev = 0;
   PP_REQUIRE(hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64, PP_ERR_HIP,
              "pp_moe_decode_noalloc: no current device");
   std::lock_guard<std::mutex> lk(g_scratch_mu);
+  *init = false;
   if (g_scratch_ptr[dev] == nullptr) {
     void* ptr = nullptr;
     const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
     PP_REQUIRE(e == hipSuccess && ptr != nullptr, PP_ERR_HIP, "pp_moe_decode_noalloc: hipGetSymbolAddress: %s",
                hipGetErrorString(e));
-    decode_ws_clear_kernel<<<64, 256, 0, s>>>((uint32_t*)ptr, kDecScratchBytes / 4);
-    const int rc = pp_check_launch("pp_moe_decode_noalloc (scratch init)");
+    const int rc = decode_scratch_fill(s, ptr, 0u, "pp_moe_decode_noalloc (scratch init)");
     if (rc) return rc;
     g_scratch_ptr[dev] = ptr;
+    *init = true;
   }
   *out = g_scratch_ptr[dev];
   return PP_OK;
+}
+
+extern "C" int pp_decode_noalloc_reset(uint32_t* error_out, uint32_t error_in, void* stream) {
+  hipStream_t s = (hipStream_t)stream;
+  int rc = decode_scratch_not_capturing(s, "pp_decode_noalloc_reset");  // before any copy or launch
+  if (rc) return rc;
+  void* ptr = nullptr;
+  bool init = false;
+  rc = decode_scratch(s, &ptr, &init);
+  if (rc) return rc;
+  if (error_out != nullptr) {  // the state before this reset (zero when this call initialised it)
+    uint32_t v = 0u;
+    if (!init) {
+      hipError_t e = hipMemcpyAsync(&v, (char*)ptr + offsetof(pp_decode_state, error), sizeof(v),
+                                    hipMemcpyDeviceToHost, s);
+      if (e == hipSuccess) e = hipStreamSynchronize(s);
+      PP_REQUIRE(e == hipSuccess, PP_ERR_HIP, "pp_decode_noalloc_reset: reading the error bits: %s",
+                 hipGetErrorString(e));
+    }
+    *error_out = v;
+  }
+  if (init && error_in == 0u) return PP_OK;
+  return decode_scratch_fill(s, ptr, error_in, "pp_decode_noalloc_reset");
 }
 
 extern "C" int pp_moe_decode_noalloc(const void* x, int x_dtype, int H, const float* router_packed,
@@ -2095,7 +2218,8 @@ extern "C" int pp_moe_decode_noalloc(const void* x, int x_dtype, int H, const fl
              PP_DECODE_SCRATCH_HS, PP_MAX_EXPERTS);
   hipStream_t s = (hipStream_t)stream;
   void* ptr = nullptr;
-  rc = decode_scratch(s, &ptr);
+  bool init = false;
+  rc = decode_scratch(s, &ptr, &init);
   if (rc) return rc;
   pp_decode_state* st = (pp_decode_state*)ptr;
   dec_acc_t* acc = (dec_acc_t*)((char*)ptr + dec_acc_offset());

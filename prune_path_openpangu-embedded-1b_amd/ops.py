@@ -133,7 +133,8 @@ def decode_state(ws: torch.Tensor, E: int) -> dict:
     ids = body[1024:2048].view(torch.int32)[:k].clone()
     gts = body[2048:3072].view(torch.float32)[:k].clone()
     return {"error": int(u32[3]), "k": k, "logits": logits, "sel_ids": ids, "sel_gates": gts,
-            "router_ticket": int(u32[0]), "epoch16": int(u32[1]), "epochb": int(u32[2])}
+            "router_ticket": int(u32[0]), "epoch16": int(u32[1]), "epochb": int(u32[2]),
+            "layout": int(u32[6]) & 0xffffffff}
 
 
 def moe_decode(x: torch.Tensor, router_packed: torch.Tensor, bias: Optional[torch.Tensor], E: int, G: int,

@@ -52,7 +52,49 @@ def test_sizes():
     assert lib.pp_max_tiles(2048, 16, 128) == 2048 * 16 // 128 + 16
     assert lib.pp_decode_workspace_bytes(H, E) >= 32 + 3 * 4 * 256 + 8 * H * 4
     assert lib.pp_prefill_workspace_bytes(2048, H, E, G) > 2048 * 16 * (G + H) * 2
-    assert lib.pp_abi_version() == 2
+    assert lib.pp_abi_version() == 3
+
+
+def _state(layout):
+    """A host copy of a decode workspace's state header (pp_decode_state) with `layout`
+    in its tag word (bytes 24..28)."""
+    buf = (ctypes.c_uint8 * (32 + 3 * 4 * 256))()
+    ctypes.c_uint32.from_buffer(buf, 24).value = layout
+    return buf
+
+
+def test_decode_workspace_of_another_layout_is_refused():
+    """The decode workspace's layout tag: pp_decode_workspace_init writes
+    pp_decode_layout_tag(H), and a header whose tag is another H's, another layout
+    version's, or zero (never initialised) is refused with both tags named (the kernels
+    compare the same word with the same tag before their first workspace write)."""
+    pkg = import_pkg()
+    lib = pkg._lib.lib()
+    tags = {H: lib.pp_decode_layout_tag(H) for H in (128, 1536, 2048, 4096)}
+    assert len(set(tags.values())) == 4 and all(t != 0 for t in tags.values())
+    assert lib.pp_decode_layout_tag(100) == 0 and lib.pp_decode_layout_tag(8192) == 0
+    for H, t in tags.items():
+        assert lib.pp_decode_state_check(_state(t), H) == 0
+        assert (t >> 13) & 0x7ff == 3  # the layout version this build writes
+    t = tags[1536]
+    for bad, what in [(tags[2048], "another H"), (t ^ (1 << 13), "another layout version"), (0, "never initialised")]:
+        rc = lib.pp_decode_state_check(_state(bad), 1536)
+        assert rc == 1, what
+        msg = lib.pp_last_error().decode()
+        assert f"0x{bad:08x}" in msg and f"0x{t:08x}" in msg, (what, msg)
+    assert lib.pp_decode_state_check(None, 1536) == 1
+
+
+def test_noalloc_reset_without_a_gpu_fails_cleanly():
+    """pp_decode_noalloc_reset needs a current device: on a host without one it returns an
+    error code, it does not crash."""
+    pkg = import_pkg()
+    lib = pkg._lib.lib()
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present: tests/test_zz_no_alloc.py covers the reset")
+    err = ctypes.c_uint32(77)
+    assert lib.pp_decode_noalloc_reset(ctypes.byref(err), 0, None) != 0
+    assert lib.pp_last_error().decode()
 
 
 @pytest.mark.parametrize("H,E,G", [(100, 16, 384), (1536, 0, 384), (1536, 300, 32), (1536, 16, 40),
