@@ -17,7 +17,12 @@ Differences by design (each a documented build choice, not an omission):
 * The kernels read packed copies of the buffers (``packed_experts``,
   ``router_packed``, non-persistent), rebuilt lazily whenever the reference
   buffers change (``load_state_dict``, ``.data =`` assignment, in-place edits
-  through ``mark_weights_changed``).
+  through ``mark_weights_changed``). Once packed, ``W_gate``, ``W_up`` and ``W_down``
+  are not kept: the packed records hold the same bf16 values, so a layer holds 75.5 MB
+  at H=1536, I=6144 instead of 132 MB. Their objects stay registered (so ``.data =``
+  mounting works) with no storage; reading one (``m.W_gate``) or ``state_dict()``
+  rebuilds it from the packed records, bit for bit, and ``load_state_dict`` gives
+  them storage again before copying.
 * Outputs are fresh tensors (the reference decode output aliases a persistent
   buffer, :530) and no call synchronises with the host (the reference prefill
   calls ``total_tiles.item()``, :581).
@@ -47,6 +52,8 @@ from . import _lib, ops
 
 
 _DECODE_OP = None
+# the reference-layout expert buffers, dropped once packed (rebuilt from the records on demand)
+_EXPERT_BUFFERS = ("W_gate", "W_up", "W_down")
 
 
 def _decode_op():
@@ -84,6 +91,9 @@ class TauSparseMoE(nn.Module):
         self.register_buffer("decode_workspace", None, persistent=False)
         self.register_buffer("batch_workspace", None, persistent=False)
         self._packed_key = None
+        # expert buffers rebuilt from the packed records since the last packing:
+        # name -> (data_ptr, version) when rebuilt (unchanged since means nothing to repack)
+        self._rebuilt = {}
         self.checked = False
         # token counts up to which forward() takes the one-launch batch kernel
         self.batch_max = 64
@@ -99,17 +109,80 @@ class TauSparseMoE(nn.Module):
     def mark_weights_changed(self) -> None:
         self._packed_key = None
 
+    # ------------------------------------------------------------------ expert buffers
+    def _ref_shape(self, name: str):
+        H, I = self.hidden_size, self.intermediate_size
+        return (I, H) if name == "W_down" else (H, I)
+
+    def _released(self, name: str) -> bool:
+        """The buffer has no storage: its values are those of the packed records."""
+        return self._buffers[name].numel() == 0 and self._buffers.get("packed_experts") is not None
+
+    def _from_records(self, name: str) -> torch.Tensor:
+        """The reference-layout buffer rebuilt from the packed records (rows region
+        [I][3][H]: gate row, up row, down column of each rearranged neuron; the same bf16
+        values the buffer held): W_gate/W_up [H,I], W_down [I,H], new storage."""
+        H, I = self.hidden_size, self.intermediate_size
+        rec = self._buffers["packed_experts"][:3 * I * H].view(I, 3, H)
+        if name == "W_down":
+            return rec[:, 2, :].contiguous()
+        return rec[:, 0 if name == "W_gate" else 1, :].t().contiguous()
+
+    def _release(self) -> None:
+        for name in _EXPERT_BUFFERS:
+            t = self._buffers[name]
+            t.data = torch.empty(0, dtype=torch.bfloat16, device=t.device)
+        self._rebuilt.clear()
+
+    def __getattr__(self, name: str):
+        # buffers live in _buffers, so reads of them come here: a released expert buffer is
+        # given storage again, rebuilt from the records, in the same tensor object
+        if name in _EXPERT_BUFFERS:
+            bufs = self.__dict__.get("_buffers")
+            if bufs is not None and name in bufs and self._released(name):
+                t = bufs[name]
+                t.data = self._from_records(name)
+                self._rebuilt[name] = (t.data_ptr(), t._version)
+        return super().__getattr__(name)
+
+    def _save_to_state_dict(self, destination, prefix, keep_vars):
+        super()._save_to_state_dict(destination, prefix, keep_vars)
+        for name in _EXPERT_BUFFERS:
+            if self._released(name):
+                destination[prefix + name] = self._from_records(name)
+
+    def _load_from_state_dict(self, state_dict, prefix, local_metadata, strict, missing_keys, unexpected_keys,
+                              error_msgs):
+        for name in _EXPERT_BUFFERS:  # storage to copy into
+            if prefix + name in state_dict and self._released(name):
+                t = self._buffers[name]
+                t.data = torch.empty(self._ref_shape(name), dtype=torch.bfloat16, device=t.device)
+        super()._load_from_state_dict(state_dict, prefix, local_metadata, strict, missing_keys, unexpected_keys,
+                                      error_msgs)
+
     def repack(self) -> None:
-        """Build the kernel layouts from the reference-layout buffers."""
-        dev = self.W_gate.device
+        """Build the kernel layouts from the reference-layout buffers, then drop the
+        expert buffers' storage. A buffer without storage, or rebuilt from the records
+        and not changed since, contributes the records' own values."""
+        b = self._buffers
+        dev = b["W_gate"].device
         if dev.type != "cuda":
             raise RuntimeError("TauSparseMoE: move the module to the GPU first; there is no CPU implementation")
         H, E, G = self.hidden_size, self.num_experts, self.group_size
-        self.packed_experts = ops.pack_experts(self.W_gate.contiguous(), self.W_up.contiguous(),
-                                               self.W_down.contiguous(), E, G, perm=None, layout="tau")
-        self.router_packed = ops.pack_router(self.router.contiguous(), layout="tau")
+
+        def changed(name):
+            t = b[name]
+            return not self._released(name) and self._rebuilt.get(name) != (t.data_ptr(), t._version)
+
+        if b["packed_experts"] is None or b["packed_experts"].device != dev or \
+                any(changed(n) for n in _EXPERT_BUFFERS):
+            src = [b[n] if not self._released(n) else self._from_records(n) for n in _EXPERT_BUFFERS]
+            self.packed_experts = ops.pack_experts(*(t.contiguous() for t in src), E, G, perm=None, layout="tau")
+            del src
+        self.router_packed = ops.pack_router(b["router"].contiguous(), layout="tau")
         if self.decode_workspace is None or self.decode_workspace.device != dev:
             self.decode_workspace = ops.decode_workspace(H, E, dev)
+        self._release()
         self._packed_key = self._weights_key()
 
     def _ensure_packed(self) -> None:
@@ -127,7 +200,7 @@ class TauSparseMoE(nn.Module):
         experts_masks_or_ids: ``experts_masks`` [E,I] one-hot or neuron->expert ids [I].
         Neurons are grouped by expert with a stable order inside each expert.
         """
-        dev = self.W_gate.device
+        dev = self._buffers["W_gate"].device
         ids = experts_masks_or_ids
         if ids.dim() == 2:
             ids = torch.argmax(ids.to(torch.int32), dim=0)
@@ -139,9 +212,8 @@ class TauSparseMoE(nn.Module):
         gw = gate_weight.to(dev)
         uw = up_weight.to(dev)
         dw = down_weight.to(dev)
-        self.W_gate = gw[perm, :].t().contiguous().to(torch.bfloat16)
-        self.W_up = uw[perm, :].t().contiguous().to(torch.bfloat16)
-        self.W_down = dw[:, perm].t().contiguous().to(torch.bfloat16)
+        # W_gate/W_up/W_down (gw[perm].T, uw[perm].T, dw[:, perm].T in bf16) are not formed:
+        # the packed records below hold exactly those values (rebuilt from them on demand)
         self.router = router_weight.to(device=dev, dtype=torch.float32).t().contiguous()
         if tau is not None:
             self.tau = tau
@@ -152,6 +224,7 @@ class TauSparseMoE(nn.Module):
         self.router_packed = ops.pack_router(router_weight.to(device=dev).contiguous(), layout="linear")
         if self.decode_workspace is None or self.decode_workspace.device != dev:
             self.decode_workspace = ops.decode_workspace(H, E, dev)
+        self._release()
         self._packed_key = self._weights_key()
         return self
 

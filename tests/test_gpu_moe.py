@@ -360,6 +360,41 @@ def test_reference_reorder_data_assignment(pkg):
     assert_close(od, sparse_expected(x[:1], w, sel1.gates)[0], what="decode after .data mount")
 
 
+def test_module_footprint_and_partial_mount(pkg):
+    """Once packed, a layer keeps the packed records + down_t (75.5 MB at H=1536, I=6144)
+    and the fp32 router, not the reference-layout W_gate/W_up/W_down (56.6 MB more).
+    Mounting only W_up by .data (here another layer's) repacks with W_gate and W_down
+    taken from the records: the same bits as a module with all three mounted."""
+    H, I, E, G = 1536, 6144, 16, 384
+    dev = torch.device("cuda:0")
+    w, w2 = _layer(57), _layer(59)
+    m = make_module(pkg, w, 0.7)
+    x = to_gpu(gi.tokens(58, 40)[None])
+    ref = m(x)
+    work = {"decode_workspace", "batch_workspace"}
+    weights = sum(t.numel() * t.element_size() for n, t in m.named_buffers() if n not in work)
+    assert weights <= 76e6, weights
+    assert all(getattr(m, "_buffers")[n].numel() == 0 for n in ("W_gate", "W_up", "W_down"))
+    perm = torch.argsort(torch.from_numpy(w["expert_ids"]).long(), stable=True)
+    tau_gu = lambda a: torch.from_numpy(a)[perm, :].t().contiguous().to(dev, torch.bfloat16)  # noqa: E731
+    up2 = tau_gu(w2["w_up"])
+    m.W_up.data = up2.clone()
+    out1 = m(x)
+    assert all(m._buffers[n].numel() == 0 for n in ("W_gate", "W_up", "W_down"))
+    full = pkg.TauSparseMoE(H, I, E, G, 0.7).to(dev)
+    full.W_gate.data = tau_gu(w["w_gate"])
+    full.W_up.data = up2
+    full.W_down.data = torch.from_numpy(w["w_down"])[:, perm].t().contiguous().to(dev, torch.bfloat16)
+    full.router.data = torch.from_numpy(w["w_router"]).t().contiguous().to(dev)
+    out2 = full(x)
+    assert torch.equal(out1, out2) and not torch.equal(out1, ref)
+    # reading a buffer rebuilds it from the records; the next call packs nothing and drops it
+    pe = m._buffers["packed_experts"]
+    assert torch.equal(m.W_up, up2)
+    assert torch.equal(m(x), out1)
+    assert m._buffers["packed_experts"] is pe and m._buffers["W_up"].numel() == 0
+
+
 def _wrapper(pkg, w, tau, G=384):
     import types
     I, H = w["w_gate"].shape

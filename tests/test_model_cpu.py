@@ -118,3 +118,32 @@ def test_moelayer_reference_constructor_and_statistics(pkg):
     assert m2.sparsity_tracking_enabled and m2.get_sparsity_statistics() == (0, 0.0)
     with pytest.raises(ValueError):
         pkg.MoELayer(types.SimpleNamespace(hidden_size=64, intermediate_size=250), types.SimpleNamespace(), 8)
+
+
+def test_expert_buffers_rebuilt_from_the_records(pkg):
+    """Once packed, W_gate/W_up/W_down keep no storage: reading one, or state_dict(),
+    rebuilds it from the packed records' rows region [I][3][H] (gate row, up row, down
+    column of each rearranged neuron), and load_state_dict gives them storage again.
+    Host logic only: the records are a synthetic buffer of random bf16 values, so a
+    transposed or shifted index shows."""
+    H, I, E, G = 128, 256, 4, 64
+    m = pkg.TauSparseMoE(H, I, E, G, 0.7)
+    rec = torch.randn(3 * I * H, generator=torch.Generator().manual_seed(5))
+    packed = torch.cat([rec, torch.zeros(I * H)]).to(torch.bfloat16)  # + the down_t region
+    m._buffers["packed_experts"] = packed
+    m._release()
+    assert all(m._buffers[n].numel() == 0 for n in ("W_gate", "W_up", "W_down"))
+    r3 = packed[:3 * I * H].view(I, 3, H)
+    sd = m.state_dict()
+    assert sorted(sd) == ["W_down", "W_gate", "W_up", "router"]
+    for name, want in (("W_gate", r3[:, 0, :].t()), ("W_up", r3[:, 1, :].t()), ("W_down", r3[:, 2, :])):
+        assert sd[name].shape == want.shape and torch.equal(sd[name], want), name
+    assert m._buffers["W_up"].numel() == 0  # state_dict() does not keep what it rebuilt
+    w = m.W_up  # a read gives the buffer its storage again, in the same object
+    assert w is m._buffers["W_up"] and torch.equal(w, r3[:, 1, :].t())
+    assert m._rebuilt["W_up"] == (w.data_ptr(), w._version)
+    # a state_dict loads into released buffers
+    m._release()
+    sd2 = {k: v.clone() + (1 if k != "router" else 0) for k, v in sd.items()}
+    m.load_state_dict(sd2)
+    assert torch.equal(m._buffers["W_down"], sd2["W_down"]) and "W_down" not in m._rebuilt
