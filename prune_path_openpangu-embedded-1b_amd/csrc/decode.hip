@@ -622,10 +622,16 @@ __device__ __forceinline__ uint4 load_x8_bf16<bf16_t>(const bf16_t* x, int ch) {
 // [512 CPL wv / NW, 512 CPL (wv + 1) / NW) of x, CPL float4 chunks per lane: lanes form
 // rows of LR = 128 / NW lanes, row rw takes experts rw, rw + NR, ... (NR = 64 / LR rows)
 // and lane cl of the row the chunks cl + LR i. Rows add by DPP; the NW wave partials are
-// added in wave order. part_s: LDS [16 * NW]. Contains a workgroup barrier.
-template <typename XT, int CPL, int NW>
+// added in wave order. part_s: LDS [16 * NW]. Contains a workgroup barrier; `issued` runs
+// once this wave's loads are issued, before the barrier (work that waits on an earlier load
+// goes there, so that its wait does not hold the router loads back).
+struct DecNoHook {
+  __device__ void operator()() const {}
+};
+template <typename XT, int CPL, int NW, typename Hook = DecNoHook>
 __device__ __forceinline__ float dec16_logits(const XT* __restrict__ x, const float* __restrict__ router,
-                                              const float* __restrict__ bias, float* part_s, int lane, int wv) {
+                                              const float* __restrict__ bias, float* part_s, int lane, int wv,
+                                              Hook issued = Hook()) {
   constexpr int H = 512 * CPL;
   static_assert(NW == 8 || NW == 16, "dec16_logits: 8 or 16 waves");
   constexpr int LR = 128 / NW, NR = 64 / LR, EPL = 16 / NR;
@@ -642,6 +648,8 @@ __device__ __forceinline__ float dec16_logits(const XT* __restrict__ x, const fl
 #pragma unroll
       for (int i = 0; i < CPL; ++i)
         wr[jj][i] = *(const float4*)(router + (rw + NR * jj) * H + 4 * (ch0 + LR * i));
+    asm volatile("" ::: "memory");  // the loads above are issued before the hook's work
+    issued();
 #pragma unroll
     for (int jj = 0; jj < EPL; ++jj) {
       float sacc = 0.0f;
@@ -801,16 +809,19 @@ __global__ __launch_bounds__(512) void decode16_kernel(
   __shared__ __align__(16) float srt_s[16];
   __shared__ __align__(16) float act_s[16 * 512];
   __shared__ int k_s, fail_s, ready_s;
+  __shared__ uint32_t epoch_s, lay_s;
   __shared__ int L_s[16];    // selected experts in rank order (the stream order)
   __shared__ float Lg_s[16];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int W = gridDim.x, b = blockIdx.x;
-  const uint32_t epoch = ld_rlx(&st->epoch16);
-  const uint32_t lay = ld_rlx(&st->layout);  // compared before the first workspace write
-  uint32_t* bank = banks + (size_t)(epoch & 1u) * DEC2_BANK_WORDS;
+  // The call's state words are read by thread 0 alone, the load issued first and waited
+  // for only once x and the router are requested (inside dec16_logits, before its
+  // barrier); the other waves take them from LDS after the barrier.
+  uint32_t ep0 = 0u, lay0 = 0u, err0 = 0u;
   if (tid == 0) {
-    fail_s = (ld_rlx(&st->error) & 1u) != 0u;  // an earlier wait timed out: NaN until re-initialised
-    ready_s = 0;
+    ep0 = ld_rlx(&st->epoch16);
+    lay0 = ld_rlx(&st->layout);  // compared before the first workspace write
+    err0 = ld_rlx(&st->error);
   }
 
   uint4 xb[CPL];
@@ -818,13 +829,27 @@ __global__ __launch_bounds__(512) void decode16_kernel(
   for (int c = 0; c < CPL; ++c) xb[c] = load_x8_bf16<XT>(x, lane + 64 * c);
 
   const int j = lane & 15;
-  const float xl = dec16_logits<XT, CPL, NW>(x, router, bias, part_s, lane, wv);
+  const float xl = dec16_logits<XT, CPL, NW>(x, router, bias, part_s, lane, wv, [&]() {
+    if (tid == 0) {
+      epoch_s = ep0;
+      lay_s = lay0;
+      if (lay0 == layout)  // alive (has read the epoch)
+        st_rlx(&banks[(size_t)(ep0 & 1u) * DEC2_BANK_WORDS + DEC2_ALIVE + b], 1u);
+      // an earlier wait timed out: NaN until re-initialised (the AND in asm: computed here,
+      // not next to the load, where it would wait for the load before x is requested)
+      uint32_t sticky;
+      asm volatile("v_and_b32 %0, 1, %1" : "=v"(sticky) : "v"(err0));
+      fail_s = (int)sticky;
+      ready_s = 0;
+    }
+  });
   const float m = row16_max(xl);
-  if (lay != layout) {
+  if (lay_s != layout) {
     dec_refuse(out, H, st, b, tid, NT);
     return;
   }
-  if (tid == 0) st_rlx(&bank[DEC2_ALIVE + b], 1u);  // alive (has read the epoch)
+  const uint32_t epoch = epoch_s;
+  uint32_t* bank = banks + (size_t)(epoch & 1u) * DEC2_BANK_WORDS;
 
   int h0, h1;  // output rows of this workgroup
   pp_split((uint32_t)H, (uint32_t)W, (uint32_t)b, h0, h1);
@@ -1073,7 +1098,10 @@ __global__ __launch_bounds__(512) void decode2p_kernel(
   const uint32_t epoch = ld_rlx(&st->epoch16);
   const uint32_t lay = ld_rlx(&st->layout);  // compared before the first workspace write
   uint32_t* bank = banks + (size_t)(epoch & 1u) * DEC2_BANK_WORDS;
-  if (tid == 0) fail_s = (ld_rlx(&st->error) & 1u) != 0u;  // an earlier wait timed out: NaN until re-initialised
+  if (tid == 0) {
+    if (lay == layout) st_rlx(&bank[DEC2_ALIVE + b], 1u);  // alive (has read the epoch)
+    fail_s = (ld_rlx(&st->error) & 1u) != 0u;  // an earlier wait timed out: NaN until re-initialised
+  }
   const uint4 zero4 = make_uint4(0, 0, 0, 0);
   uint4 xb[CPL];  // x as packed bf16 for the records
 #pragma unroll
@@ -1102,7 +1130,6 @@ __global__ __launch_bounds__(512) void decode2p_kernel(
     dec_refuse(out, H, st, b, tid, NT);
     return;
   }
-  if (tid == 0) st_rlx(&bank[DEC2_ALIVE + b], 1u);  // alive (has read the epoch)
   if (!LOCAL) {
     uint32_t* lw = bank + DEC2_LOGITS;  // [DEC2_LREPS][PP_MAX_EXPERTS]
     if (b < E && tid < DEC2_LREPS) {

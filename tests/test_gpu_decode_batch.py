@@ -108,6 +108,29 @@ def test_decode_batch_interleaved_with_decode(pkg):
     assert pkg.ops.decode_state(m.decode_workspace, E)["error"] == 0
 
 
+@pytest.mark.parametrize("xdt,with_bias", [(torch.float32, False), (torch.bfloat16, True)])
+def test_decode_batch_routing_equals_decode_kernel(pkg, xdt, with_bias):
+    """The batch kernel's logits and selection of each token are the single-token decode
+    kernel's bits (both run dec16_logits and sel16_wave): the bench takes each timed
+    decode step's k from one untimed batch call. 40 tokens at tau 0.7, one decode call
+    per token."""
+    H, E, G = 1536, 16, 384
+    w = gi.layer_weights(81, H=H, I=E * G, E=E)
+    m = make_module(pkg, w, 0.7, bias=gi.zipf_bias(E) if with_bias else None)
+    xb = to_gpu(gi.tokens(82, 40, H=H), xdt)
+    _, logits, mask, _ = _run(pkg, m, xb)
+    lg = logits.cpu().numpy()
+    mk = mask.cpu().numpy()
+    for t in range(xb.shape[0]):
+        pkg.ops.moe_decode(xb[t], m.router_packed, m.router_bias, E, G, 0.7, m.packed_experts, m.decode_workspace)
+        st = pkg.ops.decode_state(m.decode_workspace, E)
+        np.testing.assert_array_equal(st["logits"].numpy().view(np.uint32), lg[t].view(np.uint32), err_msg=f"token {t}")
+        sel = np.zeros(E, np.uint8)
+        sel[st["sel_ids"].numpy()] = 1
+        np.testing.assert_array_equal(sel, mk[t], err_msg=f"token {t}")
+        assert st["k"] == int(mk[t].sum())
+
+
 def test_decode_batch_graph_replays(pkg):
     """A call captured in a hipGraph (as the bench runs it): every replay, with eager calls on
     the same workspaces and host synchronisations between replays, gives the eager result
