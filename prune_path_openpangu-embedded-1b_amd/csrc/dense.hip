@@ -19,8 +19,8 @@
 // reference's rounding points: bf16 act (acc_gate.to(bfloat16), :318-321) and fp32 sums
 // of the per-expert down products.
 //
-// GEMM tiles: 256 x 256 outputs (DG_BM token rows x 256 columns: 128 neurons as gate and
-// up, or 256 hidden columns), K blocks of BK bf16, four waves each owning a BM/2 x 128
+// GEMM tiles: BM token rows x BN columns (BN/2 neurons as gate and up, or BN hidden
+// columns), K blocks of BK bf16, NW waves in WR wave rows, each owning a BM/WR x BN/(NW/WR)
 // wave tile of v_mfma_f32_32x32x16_bf16 blocks (accumulators in AGPRs: one workgroup per
 // CU). Operands go global -> LDS by DMA (global_load_lds_dwordx4, no VGPR staging)
 // through STAGES stages; the stream of K blocks runs across a workgroup's items (GpSched:
@@ -43,23 +43,24 @@ __device__ __forceinline__ float dg_silu(float g) {
   return g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g * -1.4426950408889634f));
 }
 
-template <int BM, int BK, int NW>
+template <int BM, int BN, int BK, int NW, int WR>
 struct Dg {
   static constexpr int NT = NW * 64;           // threads
-  static constexpr int WN = NW / 2;            // wave columns (two wave rows)
-  static constexpr int WC = 256 / WN;          // columns of a wave tile
-  static constexpr int MI = BM / 64;           // 32-row MFMA blocks per wave (wave tile BM/2 rows)
+  static constexpr int WN = NW / WR;           // wave columns (WR wave rows)
+  static constexpr int WM = BM / WR;           // rows of a wave tile
+  static constexpr int WC = BN / WN;           // columns of a wave tile
+  static constexpr int MI = WM / 32;           // 32-row MFMA blocks per wave
   static constexpr int NJ = WC / 32;           // 32-column MFMA blocks per wave
   static constexpr int NF = MI * NJ * 16;      // fp32 accumulators per thread
   static constexpr int ROWB = BK * 2;          // bytes of one tile row in a stage
   static constexpr int CH = BK / 8;            // 16-byte chunks per row
   static constexpr int RPI = 1024 / ROWB;      // rows per DMA instruction (a wave's 1 KB)
   static constexpr int NIA = BM / (NW * RPI);  // DMA instructions per wave per block, A
-  static constexpr int NIB = 256 / (NW * RPI); // ... B (256 columns)
+  static constexpr int NIB = BN / (NW * RPI);  // ... B (BN columns)
   static constexpr int DMA = NIA + NIB;
   static constexpr int KS = BK / 16;           // MFMA k-steps per block
   static constexpr int TA = BM * ROWB;         // A tile bytes per stage
-  static constexpr int STAGE = TA + 256 * ROWB;
+  static constexpr int STAGE = TA + BN * ROWB;
   static constexpr int EPW = STAGE / NW;       // epilogue staging bytes per wave (in a free stage)
   // chunk c of row r sits at c ^ swz(r): the 16 rows any 16 lanes of a fragment read
   // touch fall in 16 distinct 16-byte slots of a 256-byte bank window
@@ -75,35 +76,45 @@ struct DgArgs {
   uint32_t* sync;      // split tickets, zero at launch and left zero
   int64_t N;
   int H, E, G, I, Ipad;
+  int ct_lo, ct_hi;  // column tiles [ct_lo, ct_hi) of the launch's tile width
 };
 
-// Wait until at most N LDS reads are outstanding, tying the fragments of the current
-// k-step so that their MFMAs cannot be scheduled above the wait.
+// Wait until at most N LDS reads are outstanding, then tie the fragments of the current
+// k-step (an empty asm per fragment, after the wait in program order: volatile asm
+// statements keep their order), so that their MFMAs cannot be scheduled above the wait.
+template <int I, int M>
+__device__ __forceinline__ void dg_tie(u32x4 (&v)[M]) {
+  if constexpr (I < M) {
+    asm volatile("" : "+v"(v[I]));
+    dg_tie<I + 1, M>(v);
+  }
+}
 template <int N, int MI, int NJ>
 __device__ __forceinline__ void dg_wait(u32x4 (&a)[MI], u32x4 (&b)[NJ]) {
-  static_assert(MI + NJ <= 8 && NJ >= 2, "fragments");
-  if (MI == 4 && NJ == 4)
-    asm volatile("s_waitcnt lgkmcnt(%8)"
-                 : "+v"(a[0]), "+v"(a[1 % MI]), "+v"(a[2 % MI]), "+v"(a[3 % MI]), "+v"(b[0]), "+v"(b[1]),
-                   "+v"(b[2 % NJ]), "+v"(b[3 % NJ])
-                 : "n"(N));
-  else if (MI == 4)
-    asm volatile("s_waitcnt lgkmcnt(%6)"
-                 : "+v"(a[0]), "+v"(a[1 % MI]), "+v"(a[2 % MI]), "+v"(a[3 % MI]), "+v"(b[0]), "+v"(b[1])
-                 : "n"(N));
-  else if (NJ == 4)
-    asm volatile("s_waitcnt lgkmcnt(%6)"
-                 : "+v"(a[0]), "+v"(a[1 % MI]), "+v"(b[0]), "+v"(b[1]), "+v"(b[2 % NJ]), "+v"(b[3 % NJ])
-                 : "n"(N));
-  else
-    asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(a[0]), "+v"(a[1 % MI]), "+v"(b[0]), "+v"(b[1]) : "n"(N));
+  asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(N));
+  dg_tie<0, MI>(a);
+  dg_tie<0, NJ>(b);
 }
 
-template <int MODE, int BM, int BK, int STAGES, int NW>
+// fragments v[0 .. N) of 32-row blocks RB bytes apart from base (compile-time offsets)
+template <int RB, int N, int I = 0>
+__device__ __forceinline__ void dg_read(u32x4 (&v)[N], uint32_t base) {
+  if constexpr (I < N) {
+    v[I] = gv_read<I * RB>(base);
+    dg_read<RB, N, I + 1>(v, base);
+  }
+}
+
+template <int MODE, int BM, int BN, int BK, int STAGES, int NW, int WR>
 __global__ __launch_bounds__(NW * 64, 1) void dense_gemm_kernel(DgArgs p) {
-  using C = Dg<BM, BK, NW>;
+  using C = Dg<BM, BN, BK, NW, WR>;
+  constexpr int NB2 = BN / 2;  // MODE 0: neurons of a column tile (their gate and up rows)
   static_assert(BM == 128 || BM == 256, "tile rows");
   static_assert(NW == 4 || NW == 8, "waves");
+  static_assert(C::MI >= 1 && C::NJ >= 2 && (MODE == 1 || C::NJ % 2 == 0) && C::MI * 32 * WR == BM &&
+                    C::NJ * 32 * C::WN == BN && C::NIA * NW * C::RPI == BM && C::NIB * NW * C::RPI == BN,
+                "tile shape");
+  static_assert(MODE == 1 || (NB2 + 31) / 32 + 1 <= DG_GX, "experts a column tile can touch");
   static_assert(STAGES >= 2 && STAGES * C::STAGE + (MODE == 0 ? BM * DG_GX * 4 : 0) <= 160 * 1024 - 64, "LDS");
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ int role_s;
@@ -112,7 +123,7 @@ __global__ __launch_bounds__(NW * 64, 1) void dense_gemm_kernel(DgArgs p) {
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform, in an SGPR
   const int wm = w / C::WN, wn = w % C::WN;
   const int n_rt = (int)((p.N + BM - 1) / BM);
-  const int n_ct = MODE == 0 ? (p.Ipad + 127) / 128 : (p.H + 255) / 256;
+  const int n_ct = p.ct_hi - p.ct_lo;  // column tiles of this launch, from p.ct_lo
   const int nkb = (MODE == 0 ? p.H : p.Ipad) / BK;
   const int n_items = n_rt * n_ct;
   const GpSched sc(n_items, nkb, p.sync != nullptr, DG_NPMAX);
@@ -134,7 +145,7 @@ __global__ __launch_bounds__(NW * 64, 1) void dense_gemm_kernel(DgArgs p) {
   uint32_t aoff[C::NIA], boff[C::NIB];
   auto setup_item = [&](int li) {
     const int item = sc.item(li);
-    const int ct = item / n_rt, rt = item - ct * n_rt;
+    const int ctl = item / n_rt, rt = item - ctl * n_rt, ct = p.ct_lo + ctl;
     const int64_t t0 = (int64_t)rt * BM;
     a_item = p.a + t0 * arow;
 #pragma unroll
@@ -145,22 +156,22 @@ __global__ __launch_bounds__(NW * 64, 1) void dense_gemm_kernel(DgArgs p) {
     }
     if (MODE == 0) {
       // B row r: wave column r / WC; 32-row block jb = (r % WC) / 32 is the gate (jb < NJ/2)
-      // or up row of neuron ct * 128 + (r / WC) * WC/2 + (jb % (NJ/2)) * 32 + (r & 31)
-      b_item = p.b + (int64_t)ct * 128 * 3 * p.H;
+      // or up row of neuron ct * NB2 + (r / WC) * WC/2 + (jb % (NJ/2)) * 32 + (r & 31)
+      b_item = p.b + (int64_t)ct * NB2 * 3 * p.H;
 #pragma unroll
       for (int i = 0; i < C::NIB; ++i) {
         const int r = (NW * i + w) * C::RPI + lane / C::CH;
         const int jb = (r % C::WC) >> 5;
-        const int nl = min(ct * 128 + (r / C::WC) * (C::WC / 2) + (jb % (C::NJ / 2)) * 32 + (r & 31), p.I - 1) -
-                       ct * 128;
+        const int nl = min(ct * NB2 + (r / C::WC) * (C::WC / 2) + (jb % (C::NJ / 2)) * 32 + (r & 31), p.I - 1) -
+                       ct * NB2;
         boff[i] = (uint32_t)((nl * 3 + jb / (C::NJ / 2)) * p.H + gc8) * 2u;
       }
     } else {
-      b_item = p.b + (int64_t)ct * 256 * p.G;
+      b_item = p.b + (int64_t)ct * BN * p.G;
 #pragma unroll
       for (int i = 0; i < C::NIB; ++i) {
         const int r = (NW * i + w) * C::RPI + lane / C::CH;
-        boff[i] = (uint32_t)((min(ct * 256 + r, p.H - 1) - ct * 256) * p.G) * 2u + lane_k;
+        boff[i] = (uint32_t)((min(ct * BN + r, p.H - 1) - ct * BN) * p.G) * 2u + lane_k;
       }
     }
   };
@@ -213,7 +224,7 @@ __global__ __launch_bounds__(NW * 64, 1) void dense_gemm_kernel(DgArgs p) {
   for (int ks = 0; ks < C::KS; ++ks) {
     const int r = lane & 31, c = ks * 2 + (lane >> 5);
     const uint32_t o = (uint32_t)(r * C::CH + (c ^ C::swz(r))) * 16;
-    offA[ks] = lds0 + wm * (BM / 2) * C::ROWB + o;
+    offA[ks] = lds0 + wm * C::WM * C::ROWB + o;
     offB[ks] = lds0 + C::TA + wn * C::WC * C::ROWB + o;
   }
 
@@ -248,9 +259,9 @@ __global__ __launch_bounds__(NW * 64, 1) void dense_gemm_kernel(DgArgs p) {
       issue(f + STAGES - 1);
       if (MODE == 0 && kb == kb_first) {
         const int item = sc.item(li);
-        const int ct = item / n_rt, rt = item - ct * n_rt;
-        const int e_lo = ct * 128 / p.G;
-        const int ne = min(p.E, (ct * 128 + 127) / p.G + 1) - e_lo;
+        const int ctl = item / n_rt, rt = item - ctl * n_rt, ct = p.ct_lo + ctl;
+        const int e_lo = ct * NB2 / p.G;
+        const int ne = min(p.E, (ct * NB2 + NB2 - 1) / p.G + 1) - e_lo;
         const int64_t tt0 = (int64_t)rt * BM;
 #pragma unroll
         for (int c = 0; c < NGL; ++c) {
@@ -263,18 +274,8 @@ __global__ __launch_bounds__(NW * 64, 1) void dense_gemm_kernel(DgArgs p) {
       const uint32_t sbase = (f % STAGES) * C::STAGE;
       u32x4 fa[2][C::MI], fb[2][C::NJ];
       auto rd = [&](int ks, u32x4(&a)[C::MI], u32x4(&b)[C::NJ]) {
-        a[0] = gv_read<0>(offA[ks] + sbase);
-        a[1] = gv_read<RB>(offA[ks] + sbase);
-        if (C::MI > 2) {
-          a[2 % C::MI] = gv_read<2 * RB>(offA[ks] + sbase);
-          a[3 % C::MI] = gv_read<3 * RB>(offA[ks] + sbase);
-        }
-        b[0] = gv_read<0>(offB[ks] + sbase);
-        b[1] = gv_read<RB>(offB[ks] + sbase);
-        if (C::NJ > 2) {
-          b[2 % C::NJ] = gv_read<2 * RB>(offB[ks] + sbase);
-          b[3 % C::NJ] = gv_read<3 * RB>(offB[ks] + sbase);
-        }
+        dg_read<RB>(a, offA[ks] + sbase);
+        dg_read<RB>(b, offB[ks] + sbase);
       };
       rd(0, fa[0], fb[0]);
 #pragma unroll
@@ -343,9 +344,9 @@ __global__ __launch_bounds__(NW * 64, 1) void dense_gemm_kernel(DgArgs p) {
       int ln = lane;
       asm volatile("" : "+v"(ln));
       const int item = sc.item(li);
-      const int ct = item / n_rt, rt = item - ct * n_rt;
-      const int64_t t0 = (int64_t)rt * BM + wm * (BM / 2);
-      const int rows_in = (int)min((int64_t)(BM / 2), max((int64_t)0, p.N - t0));
+      const int ctl = item / n_rt, rt = item - ctl * n_rt, ct = p.ct_lo + ctl;
+      const int64_t t0 = (int64_t)rt * BM + wm * C::WM;
+      const int rows_in = (int)min((int64_t)C::WM, max((int64_t)0, p.N - t0));
       constexpr int NG = MODE == 0 ? C::NF / 4 : C::NF / 2;  // words per thread to reduce
       constexpr int HW = MODE == 0 ? 2 : 1;                   // words per reduced unit
       const int upc = (STAGES * C::STAGE) / (np * HW * WS);   // units per LDS chunk
@@ -389,13 +390,13 @@ __global__ __launch_bounds__(NW * 64, 1) void dense_gemm_kernel(DgArgs p) {
               const int rl = i * 32 + mfma32_row(2 * c + h, ln);
               if (rl >= rows_in) continue;
               if (MODE == 0) {
-                const int n = ct * 128 + wn * (C::WC / 2) + col;
+                const int n = ct * NB2 + wn * (C::WC / 2) + col;
                 if (n >= p.Ipad) continue;
-                const float gt = n < p.I ? gate_s[(wm * (BM / 2) + rl) * DG_GX + n / p.G - ct * 128 / p.G] : 0.0f;
+                const float gt = n < p.I ? gate_s[(wm * C::WM + rl) * DG_GX + n / p.G - ct * NB2 / p.G] : 0.0f;
                 const float a = gt == 0.0f ? 0.0f : dg_silu(sv[h]) * tv[h] * gt;
                 p.out[(t0 + rl) * p.Ipad + n] = f32_to_bf16(a);
               } else {
-                const int hc = ct * 256 + wn * C::WC + col;
+                const int hc = ct * BN + wn * C::WC + col;
                 if (hc < p.H) p.out[(t0 + rl) * p.H + hc] = f32_to_bf16(sv[h]);
               }
             }
@@ -406,89 +407,75 @@ __global__ __launch_bounds__(NW * 64, 1) void dense_gemm_kernel(DgArgs p) {
       break;
     }
     // ---- epilogue: the wave's results go through its share of the free stage (bf16, row
-    // major), then out as 16-byte row chunks: coalesced stores, no 2-byte scatter
+    // major), then out as 16-byte row chunks: coalesced stores, no 2-byte scatter. Passes of
+    // RP rows x GB 32-column blocks (as many as the wave's EPW bytes hold).
     {
       int ln = lane;
       asm volatile("" : "+v"(ln));  // keep the epilogue's lane math out of the main loop's registers
       const int item = sc.item(li);
-      const int ct = item / n_rt, rt = item - ct * n_rt;
-      const int64_t t0 = (int64_t)rt * BM + wm * (BM / 2);  // this wave's first output row
-      const int rows_in = (int)min((int64_t)(BM / 2), max((int64_t)0, p.N - t0));
+      const int ctl = item / n_rt, rt = item - ctl * n_rt, ct = p.ct_lo + ctl;
+      const int64_t t0 = (int64_t)rt * BM + wm * C::WM;  // this wave's first output row
+      const int rows_in = (int)min((int64_t)C::WM, max((int64_t)0, p.N - t0));
       unsigned char* ep = smem + (fl % STAGES) * C::STAGE + w * C::EPW;
-      if (MODE == 0) {
-        const int e_lo = ct * 128 / p.G;
+      constexpr int NB = MODE == 0 ? C::NJ / 2 : C::NJ;  // 32-column output blocks of the wave
+      constexpr int GB0 = C::EPW / (32 * 64);            // blocks of 32 rows the staging holds
+      constexpr int GB = GB0 < NB ? GB0 : NB;            // blocks per pass
+      constexpr int RW = GB * 64;                        // bytes of an LDS row
+      constexpr int RP0 = C::EPW / RW / 32 * 32;
+      constexpr int RP = RP0 < C::WM ? RP0 : C::WM;      // rows per pass
+      static_assert(GB >= 1 && RP >= 32 && C::WM % RP == 0, "epilogue passes");
+      const int c0 = MODE == 0 ? ct * NB2 + wn * (C::WC / 2) : ct * BN + wn * C::WC;  // first column
+      const int ncol = MODE == 0 ? p.Ipad : p.H;
+      const int cols_in = min(NB * 32, ncol - c0);
+      int64_t oo = t0 * ncol + c0;
+      asm volatile("" : "+s"(oo));
+      bf16_t* ob = p.out + oo;
+      const int e_lo = MODE == 0 ? ct * NB2 / p.G : 0;
+      if (MODE == 0)
         __syncthreads();  // gates staged; every wave done reading the free stage
-        // act of the wave's WC/2 neurons: LDS rows of WC/2 bf16, in passes of HR rows
-        constexpr int RW = C::WC / 2 * 2;  // bytes of an LDS row
-        constexpr int HR = C::EPW / RW < BM / 2 ? C::EPW / RW : BM / 2;  // rows per pass
-        static_assert(HR % 32 == 0 && (BM / 2) % HR == 0, "epilogue passes");
-        const int n0 = ct * 128 + wn * (C::WC / 2);
-        const int cols_in = min(C::WC / 2, p.Ipad - n0);
-        int64_t oo = t0 * p.Ipad + n0;
-        asm volatile("" : "+s"(oo));
-        bf16_t* ob = p.out + oo;
-#pragma unroll
-        for (int hf = 0; hf < (BM / 2) / HR; ++hf) {
-#pragma unroll
-          for (int jj = 0; jj < C::NJ / 2; ++jj) {
-            const int nl = jj * 32 + (ln & 31);
-            const int ek = (n0 + nl) / p.G - e_lo;
-            const bool real = n0 + nl < p.I;  // neurons of the pad [I, Ipad) get act 0
-#pragma unroll
-            for (int i = hf * (HR / 32); i < (hf + 1) * (HR / 32); ++i) {
-              f32x16_t gv = acc[i][jj], uv = acc[i][jj + C::NJ / 2];
-              asm volatile("" : "+v"(gv), "+v"(uv));  // two 16-float blocks in VGPRs at a time
-#pragma unroll
-              for (int q = 0; q < 16; ++q) {
-                const int rl = i * 32 + mfma32_row(q, ln);
-                const float gt = real ? gate_s[(wm * (BM / 2) + rl) * DG_GX + ek] : 0.0f;
-                const float a = gt == 0.0f ? 0.0f : dg_silu(gv[q]) * uv[q] * gt;
-                *(bf16_t*)(ep + (rl - hf * HR) * RW + nl * 2) = f32_to_bf16(a);
-              }
-            }
-          }
-          // out: row rl, 16-byte chunk c of the row (WC/2 neurons = RW / 16 chunks)
-          constexpr int CPR = RW / 16;
-#pragma unroll
-          for (int k = 0; k < HR * CPR / 64; ++k) {
-            const int idx = ln + 64 * k, rl = idx / CPR, c = idx % CPR;
-            const uint4 v = *(const uint4*)(ep + rl * RW + c * 16);
-            const int rg = hf * HR + rl;
-            if (rg < rows_in && c * 8 < cols_in) *(uint4*)(ob + rg * p.Ipad + c * 8) = v;
-          }
-        }
-      } else {
+      else
         asm volatile("s_barrier" ::: "memory");  // every wave done reading the free stage
-        // out rows of the wave's WC columns, in halves of BM/4 rows (EPW bytes each)
-        constexpr int RW = C::WC * 2;  // bytes of an LDS row
-        constexpr int HR = C::EPW / RW < BM / 2 ? C::EPW / RW : BM / 2;  // rows per pass
-        static_assert(HR % 32 == 0 && (BM / 2) % HR == 0, "epilogue passes");
-        const int h0 = ct * 256 + wn * C::WC;
-        const int cols_in = min(C::WC, p.H - h0);
-        int64_t oo = t0 * p.H + h0;
-        asm volatile("" : "+s"(oo));
-        bf16_t* ob = p.out + oo;
 #pragma unroll
-        for (int hf = 0; hf < (BM / 2) / HR; ++hf) {
+      for (int hf = 0; hf < C::WM / RP; ++hf) {
 #pragma unroll
-          for (int i = hf * (HR / 32); i < (hf + 1) * (HR / 32); ++i)
+        for (int jg = 0; jg < NB; jg += GB) {
 #pragma unroll
-            for (int j = 0; j < C::NJ; ++j) {
-              f32x16_t v = acc[i][j];
-              asm volatile("" : "+v"(v));  // one 16-float block in VGPRs at a time
+          for (int jj = jg; jj < (jg + GB < NB ? jg + GB : NB); ++jj) {
+            const int nl = jj * 32 + (ln & 31);  // column inside the wave's NB * 32
+            const int ek = MODE == 0 ? (c0 + nl) / p.G - e_lo : 0;
+            const bool real = MODE == 0 && c0 + nl < p.I;  // neurons of the pad [I, Ipad) get act 0
 #pragma unroll
-              for (int q = 0; q < 16; ++q) {
-                const int rl = (i - hf * (HR / 32)) * 32 + mfma32_row(q, ln);
-                *(bf16_t*)(ep + rl * RW + (j * 32 + (ln & 31)) * 2) = f32_to_bf16(v[q]);
+            for (int i = hf * (RP / 32); i < (hf + 1) * (RP / 32); ++i) {
+              if (MODE == 0) {
+                f32x16_t gv = acc[i][jj], uv = acc[i][jj + NB];
+                asm volatile("" : "+v"(gv), "+v"(uv));  // two 16-float blocks in VGPRs at a time
+#pragma unroll
+                for (int q = 0; q < 16; ++q) {
+                  const int rl = i * 32 + mfma32_row(q, ln);
+                  const float gt = real ? gate_s[(wm * C::WM + rl) * DG_GX + ek] : 0.0f;
+                  const float a = gt == 0.0f ? 0.0f : dg_silu(gv[q]) * uv[q] * gt;
+                  *(bf16_t*)(ep + (rl - hf * RP) * RW + (nl - jg * 32) * 2) = f32_to_bf16(a);
+                }
+              } else {
+                f32x16_t v = acc[i][jj];
+                asm volatile("" : "+v"(v));  // one 16-float block in VGPRs at a time
+#pragma unroll
+                for (int q = 0; q < 16; ++q) {
+                  const int rl = i * 32 + mfma32_row(q, ln);
+                  *(bf16_t*)(ep + (rl - hf * RP) * RW + (nl - jg * 32) * 2) = f32_to_bf16(v[q]);
+                }
               }
             }
+          }
+          // out: row rl of the pass, 16-byte chunk c of its GB * 64 bytes
           constexpr int CPR = RW / 16;
+          static_assert((RP * CPR) % 64 == 0, "epilogue chunks");
 #pragma unroll
-          for (int k = 0; k < HR * CPR / 64; ++k) {
+          for (int k = 0; k < RP * CPR / 64; ++k) {
             const int idx = ln + 64 * k, rl = idx / CPR, c = idx % CPR;
             const uint4 v = *(const uint4*)(ep + rl * RW + c * 16);
-            const int rg = hf * HR + rl;
-            if (rg < rows_in && c * 8 < cols_in) *(uint4*)(ob + rg * p.H + c * 8) = v;
+            const int rg = hf * RP + rl, cg = jg * 32 + c * 8;
+            if (rg < rows_in && cg < cols_in && cg < (jg + GB) * 32) *(uint4*)(ob + rg * ncol + cg) = v;
           }
         }
       }
@@ -685,23 +672,52 @@ int pp_route_impl(const void* x, int x_dtype, const float* logits_in, int64_t N,
                   uint8_t* mask_out, int32_t* count_out, bf16_t* xbf_out, hipStream_t st, int32_t* blkcnt_out);
 
 // GEMM configurations (tile rows, K block, stages) of the two launches.
+// Tiles (rows BM x columns BN, K block BK, stages, wave rows WR of the DG_NW waves).
+// gate/up: 256 x 256 (128 neurons' gate and up rows), K blocks of 64, two stages, waves
+// 2 x 4, for as many column tiles as fill whole rounds of the grid with no K split; the
+// remaining column tiles as 128 x 256 tiles (three stages; a tail of those is K-split),
+// so that no 256-row tile is cut (at N = 2048, I = 6144: 256 + 256 tiles, one round each).
+// down: 256 x 192, K blocks of 64, two stages, waves 4 x 2 (wave tile 64 x 96), K-split
+// (at N = 2048, H = 1536: 64 tiles in four K ranges).
 #ifndef DG_GU_BM
 #define DG_GU_BM 256
 #endif
+#define DG_GU_BN 256  // both gate/up launches: 128-neuron column tiles
 #ifndef DG_GU_BK
 #define DG_GU_BK 64
 #endif
 #ifndef DG_GU_ST
 #define DG_GU_ST 2
 #endif
+#ifndef DG_GU_WR
+#define DG_GU_WR 2
+#endif
+#ifndef DG_GT_BM
+#define DG_GT_BM 128
+#endif
+#ifndef DG_GT_BK
+#define DG_GT_BK 64
+#endif
+#ifndef DG_GT_ST
+#define DG_GT_ST 3
+#endif
+#ifndef DG_GT_WR
+#define DG_GT_WR 2
+#endif
 #ifndef DG_DN_BM
 #define DG_DN_BM 256
+#endif
+#ifndef DG_DN_BN
+#define DG_DN_BN 192
 #endif
 #ifndef DG_DN_BK
 #define DG_DN_BK 64
 #endif
 #ifndef DG_DN_ST
 #define DG_DN_ST 2
+#endif
+#ifndef DG_DN_WR
+#define DG_DN_WR 4
 #endif
 #ifndef DG_SPLIT
 #define DG_SPLIT 1  // tail items cut into K ranges joined in part order (0: whole items only)
@@ -710,7 +726,10 @@ int pp_route_impl(const void* x, int x_dtype, const float* logits_in, int64_t N,
 #define DG_NW 8  // waves per workgroup (two per SIMD)
 #endif
 #define DG_SYNC_WORDS (4 * DG_MAX_GRID)   // per GEMM launch: 2 counters per tail item
-#define DG_SLOT_BYTES ((size_t)256 * 256 * 4)  // one part's fp32 partial sums (a 256 x 256 tile or less)
+// one part's fp32 partial sums: a tile of either K-split launch (gate/up tail, down)
+#define DG_SLOT_BYTES                                                                                  \
+  ((size_t)std::max(Dg<DG_GT_BM, DG_GU_BN, DG_GT_BK, DG_NW, DG_GT_WR>::NF,                             \
+                    Dg<DG_DN_BM, DG_DN_BN, DG_DN_BK, DG_NW, DG_DN_WR>::NF) * DG_NW * 64 * 4)
 
 int pp_dense_ipad(int E, int G) { return (E * G + 63) / 64 * 64; }
 
@@ -758,9 +777,10 @@ static int dense_grid() {
   return std::max(8, std::min(DG_MAX_GRID, g));
 }
 
-template <int MODE, int BM, int BK, int ST>
+template <int MODE, int BM, int BN, int BK, int ST, int WR>
 static int dense_gemm_launch(const DgArgs& a, hipStream_t st) {
-  dense_gemm_kernel<MODE, BM, BK, ST, DG_NW><<<dense_grid(), DG_NW * 64, ST * Dg<BM, BK, DG_NW>::STAGE, st>>>(a);
+  dense_gemm_kernel<MODE, BM, BN, BK, ST, DG_NW, WR>
+      <<<dense_grid(), DG_NW * 64, ST * Dg<BM, BN, BK, DG_NW, WR>::STAGE, st>>>(a);
   return pp_check_launch(MODE == 0 ? "dense_gemm_kernel (gate/up)" : "dense_gemm_kernel (down)");
 }
 
@@ -808,13 +828,33 @@ static int dense_pass(const void* x, int x_dtype, int64_t n, int H, const float*
   a.G = G;
   a.I = I;
   a.Ipad = Ipad;
-  if ((rc = dense_gemm_launch<0, DG_GU_BM, DG_GU_BK, DG_GU_ST>(a, st))) return rc;
+  // gate/up: column tiles [0, ct_main) in whole rounds of 256-row tiles, no K split; the
+  // rest as 128-row tiles
+  const int grid = dense_grid();
+  const int ntc = (Ipad + DG_GU_BN / 2 - 1) / (DG_GU_BN / 2);
+  const int64_t nrt = (n + DG_GU_BM - 1) / DG_GU_BM;
+  const int ct_main = nrt * ntc >= grid ? (int)((nrt * ntc) / grid * grid / nrt) : 0;
+  if (ct_main > 0) {
+    DgArgs m = a;
+    m.part = nullptr;
+    m.sync = nullptr;
+    m.ct_lo = 0;
+    m.ct_hi = ct_main;
+    if ((rc = dense_gemm_launch<0, DG_GU_BM, DG_GU_BN, DG_GU_BK, DG_GU_ST, DG_GU_WR>(m, st))) return rc;
+  }
+  if (ct_main < ntc) {
+    a.ct_lo = ct_main;
+    a.ct_hi = ntc;
+    if ((rc = dense_gemm_launch<0, DG_GT_BM, DG_GU_BN, DG_GT_BK, DG_GT_ST, DG_GT_WR>(a, st))) return rc;
+  }
   a.a = act;
   a.b = (const bf16_t*)packed + (int64_t)I * 3 * H;  // down_t
   if (a.sync) a.sync += DG_SYNC_WORDS / 2;            // the down GEMM's own split counters
   a.gates = nullptr;
   a.out = out;
-  return dense_gemm_launch<1, DG_DN_BM, DG_DN_BK, DG_DN_ST>(a, st);
+  a.ct_lo = 0;
+  a.ct_hi = (H + DG_DN_BN - 1) / DG_DN_BN;
+  return dense_gemm_launch<1, DG_DN_BM, DG_DN_BN, DG_DN_BK, DG_DN_ST, DG_DN_WR>(a, st);
 }
 
 // The whole dense-form prefill over N tokens in passes (inputs validated by the caller).

@@ -21,20 +21,22 @@ def mfma32_row(q, lane):
     return (q >> 2) * 8 + (lane >> 5) * 4 + (q & 3)
 
 
-def dense_gemm_dma(mode, N, H, E, G, BM=256, BK=64, NW=8):
+def dense_gemm_dma(mode, N, H, E, G, BM=256, BK=64, NW=8, BN=256, WR=2):
     """Per (item ct/rt, kb): dict LDS byte -> (operand, global element index) of the
     8-element chunk a lane's DMA writes there, restating setup_item / issue."""
     I = E * G
     Ipad = (I + 63) // 64 * 64
     ROWB, CH = BK * 2, BK // 8
     RPI = 1024 // ROWB
-    NIA, NIB = BM // (NW * RPI), 256 // (NW * RPI)
-    WC = 256 // (NW // 2)
+    NIA, NIB = BM // (NW * RPI), BN // (NW * RPI)
+    assert NIA * NW * RPI == BM and NIB * NW * RPI == BN
+    WC = BN // (NW // WR)
     NJ = WC // 32
+    NB2 = BN // 2
     TA = BM * ROWB
     arow = H if mode == 0 else Ipad
     n_rt = (N + BM - 1) // BM
-    n_ct = (Ipad + 127) // 128 if mode == 0 else (H + 255) // 256
+    n_ct = (Ipad + NB2 - 1) // NB2 if mode == 0 else (H + BN - 1) // BN
     nkb = (H if mode == 0 else Ipad) // BK
     lanes = np.arange(64)
     for ct in range(n_ct):
@@ -54,17 +56,17 @@ def dense_gemm_dma(mode, N, H, E, G, BM=256, BK=64, NW=8):
                         r = (NW * i + w) * RPI + lanes // CH
                         if mode == 0:
                             jb = (r % WC) >> 5
-                            nl = np.minimum(ct * 128 + (r // WC) * (WC // 2) + (jb % (NJ // 2)) * 32 + (r & 31),
-                                            I - 1) - ct * 128
-                            elem = ct * 128 * 3 * H + kb * BK + (nl * 3 + jb // (NJ // 2)) * H + gc8
+                            nl = np.minimum(ct * NB2 + (r // WC) * (WC // 2) + (jb % (NJ // 2)) * 32 + (r & 31),
+                                            I - 1) - ct * NB2
+                            elem = ct * NB2 * 3 * H + kb * BK + (nl * 3 + jb // (NJ // 2)) * H + gc8
                         else:
-                            hl = np.minimum(ct * 256 + r, H - 1) - ct * 256
+                            hl = np.minimum(ct * BN + r, H - 1) - ct * BN
                             bk_whole = BK % G == 0
                             # lane_k_all: a lane's expert / offset inside a block of whole experts
                             lane_k = (gc8 // G) * H * G + gc8 % G if bk_whole else 0
                             boff = hl * G + lane_k
                             if bk_whole and (kb + 1) * BK <= I:
-                                elem = ct * 256 * G + kb * (BK // G) * H * G + boff
+                                elem = ct * BN * G + kb * (BK // G) * H * G + boff
                             else:
                                 e0 = (kb * BK) // G
                                 g = (kb * BK - e0 * G) + gc8
@@ -76,47 +78,47 @@ def dense_gemm_dma(mode, N, H, E, G, BM=256, BK=64, NW=8):
                                 pad = kb * BK + gc8 >= I
                                 de = np.where(pad, E - 1 - e0, de)
                                 g = np.where(pad, G - 8, g)
-                                elem = ct * 256 * G + e0 * H * G + boff + (de * H * G + g - lane_k)
+                                elem = ct * BN * G + e0 * H * G + boff + (de * H * G + g - lane_k)
                         for ln in range(64):
                             lds[TA + (NW * i + w) * 1024 + ln * 16] = ("B", int(elem[ln]))
                 yield ct, rt, kb, lds
 
 
-def expected_elem(mode, operand, row, k, ct, rt, N, H, E, G, BM=256, NW=8):
+def expected_elem(mode, operand, row, k, ct, rt, N, H, E, G, BM=256, NW=8, BN=256, WR=2):
     """Global element index of operand row `row` (tile row), K index k (first of 8): for
     the gate/up B tile, wave column wn = row // WC holds the gate rows of its WC/2 neurons
-    ct * 128 + wn * WC/2 + ..., then their up rows."""
+    ct * BN/2 + wn * WC/2 + ..., then their up rows."""
     I = E * G
     Ipad = (I + 63) // 64 * 64
     if operand == "A":
         t = min(rt * BM + row, N - 1)
         return t * (H if mode == 0 else Ipad) + k
     if mode == 0:
-        WC = 256 // (NW // 2)
+        WC = BN // (NW // WR)
         wn, within = divmod(row, WC)
         part, nb = divmod(within, WC // 2)
-        n = min(ct * 128 + wn * (WC // 2) + nb, I - 1)
+        n = min(ct * (BN // 2) + wn * (WC // 2) + nb, I - 1)
         return (n * 3 + part) * H + k
-    h = min(ct * 256 + row, H - 1)
+    h = min(ct * BN + row, H - 1)
     if k >= I:
         return None  # the pad: act is zero there, any in-range weight
     e, g = divmod(k, G)
     return (e * H + h) * G + g
 
 
-def check_dense(mode, N, H, E, G, BM=256, BK=64, NW=8, plant=False):
+def check_dense(mode, N, H, E, G, BM=256, BK=64, NW=8, BN=256, WR=2, plant=False):
     I = E * G
     Ipad = (I + 63) // 64 * 64
     ROWB, CH = BK * 2, BK // 8
     TA = BM * ROWB
-    WN = NW // 2
-    WC = 256 // WN
+    WN = NW // WR
+    WM, WC = BM // WR, BN // WN
     a_size = N * (H if mode == 0 else Ipad)
     b_size = I * 3 * H if mode == 0 else E * H * G
-    for ct, rt, kb, lds in dense_gemm_dma(mode, N, H, E, G, BM, BK, NW):
+    for ct, rt, kb, lds in dense_gemm_dma(mode, N, H, E, G, BM, BK, NW, BN, WR):
         for byte, (op, el) in lds.items():
             assert 0 <= el and el + 8 <= (a_size if op == "A" else b_size), (mode, op, ct, rt, kb, byte, el)
-        for wm in range(2):
+        for wm in range(WR):
             for wn in range(WN):
                 for ks in range(BK // 16):
                     for lane in range(64):
@@ -124,15 +126,15 @@ def check_dense(mode, N, H, E, G, BM=256, BK=64, NW=8, plant=False):
                         pos = c if plant else c ^ swz(r, BK)
                         o = (r * CH + pos) * 16
                         k = kb * BK + ks * 16 + 8 * (lane >> 5)
-                        for i in range(BM // 64):
-                            row = wm * (BM // 2) + 32 * i + r
-                            op, el = lds[wm * (BM // 2) * ROWB + o + i * 32 * ROWB]
-                            assert op == "A" and el == expected_elem(mode, "A", row, k, ct, rt, N, H, E, G, BM, NW), \
+                        for i in range(WM // 32):
+                            row = wm * WM + 32 * i + r
+                            op, el = lds[wm * WM * ROWB + o + i * 32 * ROWB]
+                            assert op == "A" and el == expected_elem(mode, "A", row, k, ct, rt, N, H, E, G, BM, NW, BN, WR), \
                                 (mode, "A", ct, rt, kb, wm, ks, lane, i)
                         for j in range(WC // 32):
                             row = wn * WC + 32 * j + r
                             op, el = lds[TA + wn * WC * ROWB + o + j * 32 * ROWB]
-                            exp = expected_elem(mode, "B", row, k, ct, rt, N, H, E, G, BM, NW)
+                            exp = expected_elem(mode, "B", row, k, ct, rt, N, H, E, G, BM, NW, BN, WR)
                             assert op == "B" and (exp is None or el == exp), (mode, "B", ct, rt, kb, wn, ks, lane, j)
 
 
@@ -147,9 +149,13 @@ SHAPES = [
 
 @pytest.mark.parametrize("N,H,E,G", SHAPES)
 @pytest.mark.parametrize("mode", [0, 1])
-@pytest.mark.parametrize("BM,BK,NW", [(256, 64, 8), (256, 32, 8), (256, 64, 4), (128, 64, 8)])
-def test_dense_gemm_addresses(mode, N, H, E, G, BM, BK, NW):
-    check_dense(mode, N, H, E, G, BM, BK, NW)
+@pytest.mark.parametrize("BM,BK,NW,BN,WR", [(256, 64, 8, 256, 2), (256, 32, 8, 256, 2), (256, 64, 4, 256, 2),
+                                          (128, 64, 8, 256, 2), (256, 32, 8, 384, 4), (128, 64, 8, 128, 4),
+                                          (256, 64, 8, 192, 4)])
+def test_dense_gemm_addresses(mode, N, H, E, G, BM, BK, NW, BN, WR):
+    if mode == 0 and (BN // (NW // WR)) // 32 % 2:
+        pytest.skip("gate/up needs an even number of 32-column blocks per wave")
+    check_dense(mode, N, H, E, G, BM, BK, NW, BN, WR)
 
 
 def test_dense_gemm_planted_swizzle_fails():
@@ -157,70 +163,80 @@ def test_dense_gemm_planted_swizzle_fails():
         check_dense(0, 64, 128, 4, 32, plant=True)
 
 
-@pytest.mark.parametrize("BM,BK,NW,ST", [(256, 64, 8, 2), (256, 32, 8, 4)])
-def test_dense_gemm_epilogue_bounds(BM, BK, NW, ST):
-    """The epilogue through LDS: every accumulator lands once in the wave's share of the
-    free stage (in range of it), the 16-byte row chunks read back cover exactly what was
-    written, global stores stay inside [N, Ipad] / [N, H] and the gate reads inside the
-    staged [BM][8] gates."""
+@pytest.mark.parametrize("BM,BN,BK,NW,WR,ST", [(256, 256, 64, 8, 2, 2), (256, 256, 32, 8, 2, 4),
+                                                (256, 384, 32, 8, 4, 3), (128, 256, 64, 8, 2, 3),
+                                                (256, 192, 64, 8, 4, 2), (128, 128, 64, 8, 4, 4)])
+def test_dense_gemm_epilogue_bounds(BM, BN, BK, NW, WR, ST):
+    """The epilogue through LDS: passes of RP rows x GB 32-column blocks; every accumulator
+    lands once in the wave's share of the free stage (in range of it), the 16-byte row
+    chunks read back cover what was written, global stores stay inside [N, Ipad] / [N, H]
+    and the gate reads inside the staged [BM][8] gates."""
     DG_GX = 8
     ROWB = BK * 2
-    STAGE = BM * ROWB + 256 * ROWB
+    STAGE = BM * ROWB + BN * ROWB
     EPW = STAGE // NW
-    WN = NW // 2
-    WC = 256 // WN
-    MI, NJ = BM // 64, WC // 32
+    WN = NW // WR
+    WM, WC = BM // WR, BN // WN
+    MI, NJ = WM // 32, WC // 32
+    NB2 = BN // 2
     for (N, H, E, G) in SHAPES:
         I = E * G
         Ipad = (I + 63) // 64 * 64
         for mode in (0, 1):
-            RW = (WC // 2) * 2 if mode == 0 else WC * 2
-            HR = min(EPW // RW, BM // 2)
-            assert HR % 32 == 0 and (BM // 2) % HR == 0 and HR * RW <= EPW
+            if mode == 0 and NJ % 2:
+                continue  # gate/up needs gate and up blocks in pairs
+            NB = NJ // 2 if mode == 0 else NJ
+            GB = min(EPW // (32 * 64), NB)
+            RW = GB * 64
+            RP = min(EPW // RW // 32 * 32, WM)
+            assert GB >= 1 and RP >= 32 and WM % RP == 0 and RP * RW <= EPW
+            cpr = RW // 16
+            assert (RP * cpr) % 64 == 0
             n_rt = (N + BM - 1) // BM
-            n_ct = (Ipad + 127) // 128 if mode == 0 else (H + 255) // 256
+            n_ct = (Ipad + NB2 - 1) // NB2 if mode == 0 else (H + BN - 1) // BN
+            ncol = Ipad if mode == 0 else H
             for ct in range(n_ct):
-                e_lo = ct * 128 // G
-                ne = min(E, (ct * 128 + 127) // G + 1) - e_lo
+                e_lo = ct * NB2 // G
+                ne = min(E, (ct * NB2 + NB2 - 1) // G + 1) - e_lo
                 assert ne <= DG_GX
                 for rt in range(n_rt):
-                    for wm in range(2):
+                    for wm in range(WR):
                         for wn in range(WN):
-                            t0 = rt * BM + wm * (BM // 2)
-                            rows_in = min(BM // 2, max(0, N - t0))
-                            if mode == 0:
-                                n0 = ct * 128 + wn * (WC // 2)
-                                cols_in = min(WC // 2, Ipad - n0)
-                                ncols = WC // 2
-                            else:
-                                n0 = ct * 256 + wn * WC
-                                cols_in = min(WC, H - n0)
-                                ncols = WC
-                            assert cols_in % 8 == 0
-                            for hf in range((BM // 2) // HR):
-                                written = set()
-                                for lane in range(64):
-                                    for i in range(hf * (HR // 32), (hf + 1) * (HR // 32)):
-                                        for jb in range(NJ // 2 if mode == 0 else NJ):
-                                            col = jb * 32 + (lane & 31)
-                                            if mode == 0 and n0 + col < I:
-                                                assert 0 <= (n0 + col) // G - e_lo < ne
-                                            for q in range(16):
-                                                rl = i * 32 + mfma32_row(q, lane)
-                                                byte = (rl - hf * HR) * RW + col * 2
-                                                assert 0 <= byte < HR * RW and byte not in written
-                                                written.add(byte)
-                                assert len(written) == HR * ncols
-                                cpr = RW // 16
-                                assert (HR * cpr) % 64 == 0
-                                for k in range(HR * cpr // 64):
+                            t0 = rt * BM + wm * WM
+                            rows_in = min(WM, max(0, N - t0))
+                            c0 = ct * NB2 + wn * (WC // 2) if mode == 0 else ct * BN + wn * WC
+                            cols_in = min(NB * 32, ncol - c0)
+                            assert cols_in <= 0 or cols_in % 8 == 0
+                            stored = set()
+                            for hf in range(WM // RP):
+                                for jg in range(0, NB, GB):
+                                    written = set()
+                                    jjs = range(jg, min(jg + GB, NB))
                                     for lane in range(64):
-                                        idx = lane + 64 * k
-                                        rl, c = divmod(idx, cpr)
-                                        rg = hf * HR + rl
-                                        if rg < rows_in and c * 8 < cols_in:
-                                            assert t0 + rg < N
-                                            assert n0 + c * 8 + 8 <= (Ipad if mode == 0 else H)
+                                        for jj in jjs:
+                                            nl = jj * 32 + (lane & 31)
+                                            if mode == 0 and c0 + nl < I:
+                                                assert 0 <= (c0 + nl) // G - e_lo < ne
+                                            for i in range(hf * (RP // 32), (hf + 1) * (RP // 32)):
+                                                for q in range(16):
+                                                    rl = i * 32 + mfma32_row(q, lane)
+                                                    byte = (rl - hf * RP) * RW + (nl - jg * 32) * 2
+                                                    assert 0 <= byte < RP * RW and byte not in written
+                                                    written.add(byte)
+                                    assert len(written) == RP * 32 * len(jjs)
+                                    for k in range(RP * cpr // 64):
+                                        for lane in range(64):
+                                            idx = lane + 64 * k
+                                            rl, c = divmod(idx, cpr)
+                                            rg, cg = hf * RP + rl, jg * 32 + c * 8
+                                            if rg < rows_in and cg < cols_in and cg < (jg + GB) * 32:
+                                                # the chunk was written in this pass, stored once, in range
+                                                assert all((rl * RW + c * 16 + 2 * e) in written for e in range(8))
+                                                assert (rg, cg) not in stored
+                                                stored.add((rg, cg))
+                                                assert t0 + rg < N and c0 + cg + 8 <= ncol
+                            # every in-range output chunk of the wave tile is stored
+                            assert len(stored) == rows_in * max(0, cols_in) // 8
 
 
 @pytest.mark.parametrize("xs", [4, 2])
@@ -283,21 +299,24 @@ def test_route_logits_addresses(xs, N, H, E):
 
 
 @pytest.mark.parametrize("mode", [0, 1])
-@pytest.mark.parametrize("NW,BK,ST", [(8, 64, 2), (8, 32, 4), (4, 64, 2)])
-def test_dense_split_join_lds_chunks(mode, NW, BK, ST):
+@pytest.mark.parametrize("NW,BK,ST,BN,WR", [(8, 64, 2, 256, 2), (8, 32, 4, 256, 2), (4, 64, 2, 256, 2),
+                                          (8, 32, 3, 384, 4), (8, 64, 2, 192, 4)])
+def test_dense_split_join_lds_chunks(mode, NW, BK, ST, BN, WR):
     """The distributed join of a split tile: for every part count, the slabs partition the
     words each thread reduces; every chunk's DMA pieces stay inside the stages and inside
     the part slots (np parts of NF floats x threads); the word a thread reads back from LDS
     is its own word of part q -- the one the part's thread tid stored."""
     BM = 256
     NT = NW * 64
-    WN = NW // 2
-    NJ = (256 // WN) // 32
-    MI = BM // 64
+    WN = NW // WR
+    NJ = (BN // WN) // 32
+    if mode == 0 and NJ % 2:
+        pytest.skip("gate/up needs gate and up blocks in pairs")
+    MI = BM // WR // 32
     NF = MI * NJ * 16
     WS = NT * 8
     SLOT = NF * NT * 4
-    STAGE = BM * BK * 2 + 256 * BK * 2
+    STAGE = BM * BK * 2 + BN * BK * 2
     LDS = ST * STAGE
     NG = NF // 4 if mode == 0 else NF // 2
     HW = 2 if mode == 0 else 1

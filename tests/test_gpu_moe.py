@@ -248,6 +248,7 @@ def test_prefill_dense_form_e192(pkg):
     (640, 5, 160, 70, torch.float32),    # G = 160: experts straddle K blocks; a short last hidden tile
     (1536, 24, 32, 257, torch.bfloat16), # E = 24 (two 16-expert logit tiles), bf16 x, ragged N
     (1536, 16, 96, 40, torch.float32),   # E = 16 with G % 64 != 0: the E = 16 router feeds the dense form
+    (1536, 192, 32, 1800, torch.float32),  # whole rounds of 256-row gate/up tiles, then 128-row tiles; ragged N
 ])
 def test_prefill_dense_form_shapes(pkg, H, E, G, N, xdt):
     """The dense form across shapes: selection bit-exact on the call's own logits, every row
