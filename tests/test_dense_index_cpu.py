@@ -240,12 +240,12 @@ def test_dense_gemm_epilogue_bounds(BM, BN, BK, NW, WR, ST):
 
 
 @pytest.mark.parametrize("xs", [4, 2])
-@pytest.mark.parametrize("N,H,E", [(33, 384, 192), (1, 128, 24), (70, 1536, 40)])
-def test_route_logits_addresses(xs, N, H, E):
+@pytest.mark.parametrize("N,H,E,TE", [(33, 384, 192, 3), (1, 128, 24, 2), (70, 1536, 40, 3), (33, 384, 192, 4),
+                                      (40, 256, 200, 4)])
+def test_route_logits_addresses(xs, N, H, E, TE):
     """route_logits_kernel: DMA sources in range; the LDS rows read back as the fragment
     operands x[t][k + 8g + j] and W[e][k + 8g + j]."""
     KC, TT = 128, 2
-    TE = 1 if E <= 16 else 2 if E <= 32 else 3
     Epad = (E + 15) // 16 * 16
     XROW, WROW = KC * xs, KC * 4
     XB = 16 * TT * XROW
