@@ -17,6 +17,8 @@
 //   moe_decode_batch(_into)  TauSparseMoE.forward_prefill (:532-604) for 1 <= N <= 64
 //                         tokens (the reference takes it for every N > 1, :606-615)
 //   moe_prefill(_into)    TauSparseMoE.forward_prefill (:532-604)
+//   masked_gate(_bwd)     MoELayer.forward's expert gating and its backward
+//                         (src/MoEBlock_origin.py:205-212)
 #include <ATen/ATen.h>
 #include <algorithm>
 #include <c10/core/DeviceGuard.h>
@@ -397,6 +399,68 @@ void moe_prefill_into_meta(const Tensor&, const Tensor&, const optional<Tensor>&
                            const optional<Tensor>&) {}
 
 // CPU tensors: refused with the op's name (there is no host implementation, on purpose).
+// ------------------------------------------------------------------ masked gating (training)
+// masked_gate / masked_gate_bwd: MoELayer.forward's mask matmul and multiply
+// (src/MoEBlock_origin.py:205-212), out = inter * gates[:, expert_ids], and its backward
+// (autograd of masked_gate is registered from Python: ops.py). inter / d_out [..., I]
+// (fp32 or bf16, the rows flattened), gates [..., E] fp32, expert_ids / perm int32 [I],
+// seg int32 [E + 1] (masked_gate_layout in ops.py); perm and seg are the backward's
+// expert segments, carried by the forward for autograd.
+void masked_gate_check(const char* name, const Tensor& inter, const Tensor& gates, const Tensor& eid) {
+  TORCH_CHECK(inter.dim() >= 1 && gates.dim() >= 1, "prunepath.", name, ": inter [..., I] and gates [..., E]");
+  TORCH_CHECK(gates.scalar_type() == at::kFloat, "prunepath.", name, ": gates must be float32");
+  TORCH_CHECK(eid.scalar_type() == at::kInt && eid.numel() == inter.size(-1), "prunepath.", name,
+              ": expert_ids must be int32 [I]");
+  TORCH_CHECK(gates.numel() / std::max<int64_t>(1, gates.size(-1)) == inter.numel() / std::max<int64_t>(1, inter.size(-1)),
+              "prunepath.", name, ": inter and gates have different row counts");
+}
+
+Tensor masked_gate_gpu(const Tensor& inter, const Tensor& gates, const Tensor& eid, const Tensor& perm,
+                       const Tensor& seg) {
+  masked_gate_check("masked_gate", inter, gates, eid);
+  need_gpu("masked_gate", inter, {&inter, &gates, &eid, &perm, &seg});
+  const c10::DeviceGuard g(inter.device());
+  const int64_t I = inter.size(-1), E = gates.size(-1), n = inter.numel() / std::max<int64_t>(1, I);
+  Tensor out = at::empty_like(inter);
+  if (n == 0) return out;
+  check_rc(pp_masked_gate_fwd(inter.data_ptr(), x_code(inter, "masked_gate"), gates.data_ptr<float>(),
+                              eid.data_ptr<int32_t>(), n, (int)I, (int)E, out.data_ptr(), stream_of(inter)),
+           "masked_gate");
+  return out;
+}
+
+Tensor masked_gate_meta(const Tensor& inter, const Tensor&, const Tensor&, const Tensor&, const Tensor&) {
+  return at::empty_like(inter);
+}
+
+std::tuple<Tensor, Tensor> masked_gate_bwd_gpu(const Tensor& d_out, const Tensor& inter, const Tensor& gates,
+                                               const Tensor& eid, const Tensor& perm, const Tensor& seg,
+                                               bool need_d_inter) {
+  masked_gate_check("masked_gate_bwd", inter, gates, eid);
+  TORCH_CHECK(d_out.sizes() == inter.sizes() && d_out.scalar_type() == inter.scalar_type(),
+              "prunepath.masked_gate_bwd: d_out must match inter's shape and dtype");
+  TORCH_CHECK(perm.scalar_type() == at::kInt && perm.numel() == inter.size(-1) && seg.scalar_type() == at::kInt &&
+                  seg.numel() == gates.size(-1) + 1,
+              "prunepath.masked_gate_bwd: perm int32 [I] and seg int32 [E + 1] required");
+  need_gpu("masked_gate_bwd", inter, {&d_out, &inter, &gates, &eid, &perm, &seg});
+  const c10::DeviceGuard g(inter.device());
+  const int64_t I = inter.size(-1), E = gates.size(-1), n = inter.numel() / std::max<int64_t>(1, I);
+  Tensor d_inter = need_d_inter ? at::empty_like(inter) : at::empty({0}, inter.options());
+  Tensor d_gates = at::empty_like(gates);
+  if (n == 0) return {d_inter, d_gates};
+  check_rc(pp_masked_gate_bwd(d_out.data_ptr(), inter.data_ptr(), x_code(inter, "masked_gate_bwd"),
+                              gates.data_ptr<float>(), eid.data_ptr<int32_t>(), perm.data_ptr<int32_t>(),
+                              seg.data_ptr<int32_t>(), n, (int)I, (int)E, need_d_inter ? d_inter.data_ptr() : nullptr,
+                              d_gates.data_ptr<float>(), stream_of(inter)),
+           "masked_gate_bwd");
+  return {d_inter, d_gates};
+}
+
+std::tuple<Tensor, Tensor> masked_gate_bwd_meta(const Tensor&, const Tensor& inter, const Tensor& gates,
+                                                const Tensor&, const Tensor&, const Tensor&, bool need_d_inter) {
+  return {need_d_inter ? at::empty_like(inter) : at::empty({0}, inter.options()), at::empty_like(gates)};
+}
+
 void refuse_cpu(const c10::OperatorHandle& op, torch::jit::Stack*) {
   TORCH_CHECK(false, op.schema().name(), ": tensors must be on the GPU (got cpu); there is no CPU implementation");
 }
@@ -425,6 +489,9 @@ TORCH_LIBRARY(prunepath, m) {
   m.def("moe_prefill(Tensor x, Tensor router_packed, Tensor? bias, int E, int G, float tau, Tensor packed) -> Tensor");
   m.def("moe_prefill_into(Tensor x, Tensor router_packed, Tensor? bias, int E, int G, float tau, Tensor packed, "
         "Tensor(a!) workspace, Tensor(b!) out, Tensor(c!)? logits_out=None, Tensor(d!)? mask_out=None) -> ()");
+  m.def("masked_gate(Tensor inter, Tensor gates, Tensor expert_ids, Tensor perm, Tensor seg) -> Tensor");
+  m.def("masked_gate_bwd(Tensor d_out, Tensor inter, Tensor gates, Tensor expert_ids, Tensor perm, Tensor seg, "
+        "bool need_d_inter=True) -> (Tensor d_inter, Tensor d_gates)");
 }
 
 TORCH_LIBRARY_IMPL(prunepath, CUDA, m) {
@@ -440,6 +507,8 @@ TORCH_LIBRARY_IMPL(prunepath, CUDA, m) {
   m.impl("moe_decode_batch_into", &decode_batch_into);
   m.impl("moe_prefill", &moe_prefill_gpu);
   m.impl("moe_prefill_into", &prefill_into);
+  m.impl("masked_gate", &masked_gate_gpu);
+  m.impl("masked_gate_bwd", &masked_gate_bwd_gpu);
 }
 
 TORCH_LIBRARY_IMPL(prunepath, Meta, m) {
@@ -455,11 +524,13 @@ TORCH_LIBRARY_IMPL(prunepath, Meta, m) {
   m.impl("moe_decode_batch_into", &moe_decode_batch_into_meta);
   m.impl("moe_prefill", &moe_prefill_meta);
   m.impl("moe_prefill_into", &moe_prefill_into_meta);
+  m.impl("masked_gate", &masked_gate_meta);
+  m.impl("masked_gate_bwd", &masked_gate_bwd_meta);
 }
 
 TORCH_LIBRARY_IMPL(prunepath, CPU, m) {
   for (const char* name : {"route", "route_logits", "bucket", "pack_experts", "pack_router", "decode_workspace_init",
                            "moe_decode", "moe_decode_into", "moe_decode_batch", "moe_decode_batch_into",
-                           "moe_prefill", "moe_prefill_into"})
+                           "moe_prefill", "moe_prefill_into", "masked_gate", "masked_gate_bwd"})
     m.impl(name, torch::CppFunction::makeFromBoxedFunction<&refuse_cpu>());
 }

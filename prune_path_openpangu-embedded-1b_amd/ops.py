@@ -279,51 +279,57 @@ def _mg_dtype(t: torch.Tensor) -> int:
     raise RuntimeError(f"prunepath.masked_gate: activations must be float32 or bfloat16 (got {t.dtype})")
 
 
-def masked_gate_fwd(inter: torch.Tensor, gates: torch.Tensor, eid: torch.Tensor) -> torch.Tensor:
+def masked_gate_fwd(inter: torch.Tensor, gates: torch.Tensor, eid: torch.Tensor, perm=None, seg=None) -> torch.Tensor:
     """inter [..., I] * gates[..., expert_ids] (MoELayer.forward's mask matmul and multiply,
-    src/MoEBlock_origin.py:205-212), same dtype and shape as inter."""
-    I, E = inter.shape[-1], gates.shape[-1]
-    x = _mg_rows(inter, I)
-    g = _mg_rows(gates.float(), E)
-    _need_gpu("masked_gate_fwd", x, g, eid)
-    out = torch.empty_like(x)
-    rc = L.lib().pp_masked_gate_fwd(_vp(x), _mg_dtype(x), _vp(g), _vp(eid), x.shape[0], I, E, _vp(out),
-                                    _stream(x))
-    L.check(rc, "masked_gate_fwd")
-    return out.view(inter.shape)
+    src/MoEBlock_origin.py:205-212), same dtype and shape as inter
+    (``torch.ops.prunepath.masked_gate``; no autograd here: see ``masked_gate``)."""
+    if perm is None or seg is None:
+        perm = seg = torch.empty(0, dtype=torch.int32, device=eid.device)
+    x = inter.contiguous()
+    _mg_dtype(x)
+    with torch.no_grad():
+        return L.torch_ops().masked_gate(x, gates.float().contiguous(), eid, perm, seg)
 
 
 def masked_gate_bwd(d_out: torch.Tensor, inter: torch.Tensor, gates: torch.Tensor, eid: torch.Tensor,
                     perm: torch.Tensor, seg: torch.Tensor, need_d_inter: bool = True):
-    """(d_inter or None, d_gates fp32) of masked_gate_fwd."""
-    I, E = inter.shape[-1], gates.shape[-1]
-    x = _mg_rows(inter, I)
-    go = _mg_rows(d_out.to(inter.dtype), I)
-    g = _mg_rows(gates.float(), E)
-    _need_gpu("masked_gate_bwd", go, x, g, eid, perm, seg)
-    d_inter = torch.empty_like(x) if need_d_inter else None
-    d_gates = torch.empty(x.shape[0], E, dtype=torch.float32, device=x.device)
-    rc = L.lib().pp_masked_gate_bwd(_vp(go), _vp(x), _mg_dtype(x), _vp(g), _vp(eid), _vp(perm), _vp(seg),
-                                    x.shape[0], I, E, _vp(d_inter), _vp(d_gates), _stream(x))
-    L.check(rc, "masked_gate_bwd")
-    return (d_inter.view(inter.shape) if d_inter is not None else None), d_gates.view(gates.shape)
+    """(d_inter or None, d_gates fp32) of masked_gate_fwd (``torch.ops.prunepath.masked_gate_bwd``)."""
+    x = inter.contiguous()
+    _mg_dtype(x)
+    d_inter, d_gates = L.torch_ops().masked_gate_bwd(d_out.to(x.dtype).contiguous(), x, gates.float().contiguous(),
+                                                     eid, perm, seg, need_d_inter)
+    return (d_inter if need_d_inter else None), d_gates
 
 
-class _MaskedGate(torch.autograd.Function):
-    @staticmethod
-    def forward(ctx, inter, gates, eid, perm, seg):
-        ctx.save_for_backward(inter, gates, eid, perm, seg)
-        return masked_gate_fwd(inter, gates, eid)
+def _mg_setup_context(ctx, inputs, output):
+    inter, gates, eid, perm, seg = inputs
+    ctx.save_for_backward(inter, gates, eid, perm, seg)
 
-    @staticmethod
-    def backward(ctx, d_out):
-        inter, gates, eid, perm, seg = ctx.saved_tensors
-        d_inter, d_gates = masked_gate_bwd(d_out, inter, gates, eid, perm, seg, ctx.needs_input_grad[0])
-        return d_inter, d_gates.to(gates.dtype), None, None, None
+
+def _mg_backward(ctx, d_out):
+    inter, gates, eid, perm, seg = ctx.saved_tensors
+    d_inter, d_gates = L.torch_ops().masked_gate_bwd(d_out.contiguous(), inter, gates, eid, perm, seg,
+                                                     bool(ctx.needs_input_grad[0]))
+    return (d_inter if ctx.needs_input_grad[0] else None), d_gates, None, None, None
+
+
+_MG_AUTOGRAD = False
+
+
+def _register_masked_gate_autograd() -> None:
+    global _MG_AUTOGRAD
+    if not _MG_AUTOGRAD:
+        L.torch_ops()  # loads the extension (defines prunepath::masked_gate)
+        torch.library.register_autograd("prunepath::masked_gate", _mg_backward, setup_context=_mg_setup_context)
+        _MG_AUTOGRAD = True
 
 
 def masked_gate(inter: torch.Tensor, gates: torch.Tensor, layout) -> torch.Tensor:
     """Differentiable masked gating: inter * (gates @ experts_masks) with the HIP forward
-    and backward kernels; ``layout`` from masked_gate_layout."""
+    and backward kernels (``torch.ops.prunepath.masked_gate``, autograd registered on the
+    op); ``layout`` from masked_gate_layout. gates of any float dtype (computed in fp32)."""
     eid, perm, seg = layout
-    return _MaskedGate.apply(inter, gates, eid, perm, seg)
+    _register_masked_gate_autograd()
+    x = inter.contiguous()
+    _mg_dtype(x)
+    return L.torch_ops().masked_gate(x, gates.float().contiguous(), eid, perm, seg)

@@ -161,7 +161,7 @@ def test_masked_layer_eval_statistics(pkg):
     H, I, E = 256, 1024, 16
     cfg = types.SimpleNamespace(hidden_size=H, intermediate_size=I)
     layer = pkg.MoELayer(cfg, types.SimpleNamespace(tau=0.7), E).to(dev())
-    assert float(layer.mlp_router[0].weight.abs().sum()) == 0.0  # router_weights_init: zeros
+    assert float(layer.mlp_router[0].weight.detach().abs().sum()) == 0.0  # router_weights_init: zeros
     with torch.no_grad():
         layer.mlp_router[0].weight.normal_(0, 0.1)
     layer.eval()

@@ -15,7 +15,8 @@ import torch
 from conftest import import_pkg
 
 OPS = ["route", "route_logits", "bucket", "pack_experts", "pack_router", "decode_workspace_init", "moe_decode",
-       "moe_decode_into", "moe_decode_batch", "moe_decode_batch_into", "moe_prefill", "moe_prefill_into"]
+       "moe_decode_into", "moe_decode_batch", "moe_decode_batch_into", "moe_prefill", "moe_prefill_into",
+       "masked_gate", "masked_gate_bwd"]
 
 
 @pytest.fixture(scope="module")
@@ -57,6 +58,16 @@ def test_meta_shapes(P):
     bws = torch.empty(lib.pp_decode_batch_workspace_bytes(H, E, G), dtype=torch.uint8, device=m)
     yb = P.moe_decode_batch(x, rp, None, E, G, 0.7, packed, ws, bws)
     assert yb.shape == (N, H) and yb.dtype == torch.bfloat16
+    inter = torch.empty(2, N, 1024, dtype=torch.bfloat16, device=m)
+    gts = torch.empty(2, N, E, device=m)
+    eid = torch.empty(1024, dtype=torch.int32, device=m)
+    seg = torch.empty(E + 1, dtype=torch.int32, device=m)
+    mg = P.masked_gate(inter, gts, eid, eid, seg)
+    assert mg.shape == inter.shape and mg.dtype == torch.bfloat16
+    di, dg = P.masked_gate_bwd(inter, inter, gts, eid, eid, seg, True)
+    assert di.shape == inter.shape and dg.shape == gts.shape and dg.dtype == torch.float32
+    di, _ = P.masked_gate_bwd(inter, inter, gts, eid, eid, seg, False)
+    assert di.numel() == 0
 
 
 def test_meta_symbolic_sizes(P):
@@ -125,6 +136,15 @@ def test_opcheck_all_ops(P):
         (P.moe_prefill, (x, rp, None, E, G, 0.7, packed)),
         (P.moe_prefill_into, (x, rp, None, E, G, 0.7, packed, wsp, outp)),
     ]
+    # the masked training gating (autograd registered on masked_gate from ops.py)
+    I = 1024
+    lay = pkg.ops.masked_gate_layout(torch.randperm(I, device=x.device) % E, E)
+    pkg.ops._register_masked_gate_autograd()
+    inter = torch.randn(x.shape[0], I, device=x.device, requires_grad=True)
+    gts = torch.rand(x.shape[0], E, device=x.device, requires_grad=True)
+    cases += [(P.masked_gate, (inter, gts, *lay)),
+              (P.masked_gate, (inter.detach().bfloat16(), gts.detach(), *lay)),
+              (P.masked_gate_bwd, (inter.detach(), inter.detach(), gts.detach(), *lay, True))]
     for op, args in cases:
         print(f"opcheck {op}", flush=True)
         opcheck(op, args)
