@@ -31,6 +31,7 @@
 // completion (s_waitcnt vmcnt(0)) before the dependent atomic. Agent-scope fences are
 // avoided on purpose: on gfx950 each one writes back and invalidates the L2, which
 // hundreds of workgroups cannot afford inside a 10 us kernel.
+#include <algorithm>
 #include <cstddef>
 #include <mutex>
 
@@ -1954,6 +1955,18 @@ static int decode_check_args(const void* x, int x_dtype, int H, const float* rou
   return PP_OK;
 }
 
+// Default grid of the two-phase kernels: as few workgroups as keep every workgroup's output
+// rows within one pass of eight (H / 8), but at least three quarters of the CUs (the
+// record stream needs the memory parallelism), at most every CU. At H = 1536 on 256 CUs:
+// 192 workgroups of 8 rows (eight waves, one row each in phase 2) and ~1.7 records per
+// streaming wave: 11.25 us against 11.45 us with 256 workgroups of 6 rows (grids 200 to
+// 248: 11.34 to 11.56 us; 160: 12.5 us, two row passes).
+static int dec2_default_grid(int H) {
+  const int cus = pp_device_cus();
+  const int rows8 = (H / 8 + 7) / 8 * 8, q3 = (3 * cus / 4 + 7) / 8 * 8;
+  return std::max(8, std::min(cus, std::max(rows8, q3)));
+}
+
 // The launch shared by both entry points: st / acc = the state and the accumulators of
 // the workspace in use, hs = the stride of one accumulator copy, hclear = how much of
 // each copy of the previous call's set to clear.
@@ -1970,7 +1983,7 @@ static int decode_dispatch(const void* x, int x_dtype, int H, const float* route
     // grid is clamped to what the device holds at once (and to DEC2_WMAX); rows of the
     // output per workgroup are handled rp at a time, their down rows staged in LDS
     PP_REQUIRE(banks != nullptr, PP_ERR_INVALID, "pp_moe_decode: workspace without the E = 16 act banks");
-    int W = min(grid_in == 0 ? pp_device_cus() : grid_in, DEC2_WMAX);
+    int W = min(grid_in == 0 ? dec2_default_grid(H) : grid_in, DEC2_WMAX);
     const int nh = (H + W - 1) / W;
     const int rp = max(1, min(min(8, nh), DEC2_DOWN_LDS / (16 * G * 2)));
     const int slot_bytes = (rp * G * 2 + 1023) / 1024 * 1024;
