@@ -560,60 +560,89 @@ __global__ __launch_bounds__(512, 1) void route_logits_kernel(const XT* __restri
   for (int c = 0; c < RL_STAGES - 1; ++c) issue(c);
 
   const int t_l = lane & 15, g = lane >> 4;
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void_t*)smem;
   f32x4_t acc[TE];
 #pragma unroll
   for (int b = 0; b < TE; ++b) acc[b] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
   for (int c = 0; c < nch; ++c) {
     asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(R::DMA * (RL_STAGES - 2)) : "memory");
     issue(c + RL_STAGES - 1);
-    const unsigned char* st = smem + (c % RL_STAGES) * R::STAGE;
-    // x as bf16 for the GEMMs (fp32 x, first expert group only): thread -> row tid / 8,
-    // 16 values at (tid % 8) * 16
-    if (sizeof(XT) == 4 && xbf_out && blockIdx.y == 0 && tid < 256) {
-      const int r = tid >> 3, k16 = (tid & 7) * 16;
-      const int64_t t = tok0 + r;
-      if (t < N) {
-        uint32_t pk[8];
-#pragma unroll
-        for (int h = 0; h < 4; ++h) {
-          const float4 v = *(const float4*)(st + r * R::XROW + ((((k16 >> 2) + h) ^ (r & 15)) << 4));
-          pk[2 * h] = (uint32_t)f32_to_bf16(v.x) | ((uint32_t)f32_to_bf16(v.y) << 16);
-          pk[2 * h + 1] = (uint32_t)f32_to_bf16(v.z) | ((uint32_t)f32_to_bf16(v.w) << 16);
-        }
-        uint4* dst = (uint4*)(xbf_out + t * H + c * RL_KC + k16);
-        dst[0] = make_uint4(pk[0], pk[1], pk[2], pk[3]);
-        dst[1] = make_uint4(pk[4], pk[5], pk[6], pk[7]);
-      }
-    }
-    float xv[8], wv[TE][8];
+    // LDS reads through asm (lds_read16): ordered after this chunk's DMAs by the wait and
+    // barrier above; plain loads would make the compiler wait for every DMA in flight,
+    // the next chunks' included, before the first read
+    const uint32_t sb = lds0 + (uint32_t)((c % RL_STAGES) * R::STAGE);
+    u32x4 xq[2], wq[TE][2];
     {
       const int r = 16 * ta + t_l;
       if (sizeof(XT) == 4) {
         const int c0 = 8 * kq + 2 * g;
-        const float4 v0 = *(const float4*)(st + r * R::XROW + ((c0 ^ (r & 15)) << 4));
-        const float4 v1 = *(const float4*)(st + r * R::XROW + (((c0 + 1) ^ (r & 15)) << 4));
-        xv[0] = v0.x; xv[1] = v0.y; xv[2] = v0.z; xv[3] = v0.w;
-        xv[4] = v1.x; xv[5] = v1.y; xv[6] = v1.z; xv[7] = v1.w;
+        xq[0] = lds_read16(sb + r * R::XROW + ((c0 ^ (r & 15)) << 4));
+        xq[1] = lds_read16(sb + r * R::XROW + (((c0 + 1) ^ (r & 15)) << 4));
       } else {
-        const uint4 u = *(const uint4*)(st + r * R::XROW + (((4 * kq + g) ^ (r & 15)) << 4));
-        const uint32_t uw[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          xv[2 * i] = __uint_as_float(uw[i] << 16);
-          xv[2 * i + 1] = __uint_as_float(uw[i] & 0xffff0000u);
-        }
+        xq[0] = lds_read16(sb + r * R::XROW + (((4 * kq + g) ^ (r & 15)) << 4));
+        xq[1] = xq[0];
       }
     }
 #pragma unroll
     for (int b = 0; b < TE; ++b) {
       const int r = 16 * b + t_l;
       const int c0 = 8 * kq + 2 * g;
-      const unsigned char* ws = st + R::XB + r * R::WROW;
-      const float4 v0 = *(const float4*)(ws + ((c0 ^ (r & 15)) << 4));
-      const float4 v1 = *(const float4*)(ws + (((c0 + 1) ^ (r & 15)) << 4));
-      wv[b][0] = v0.x; wv[b][1] = v0.y; wv[b][2] = v0.z; wv[b][3] = v0.w;
-      wv[b][4] = v1.x; wv[b][5] = v1.y; wv[b][6] = v1.z; wv[b][7] = v1.w;
+      const uint32_t ws = sb + R::XB + r * R::WROW;
+      wq[b][0] = lds_read16(ws + ((c0 ^ (r & 15)) << 4));
+      wq[b][1] = lds_read16(ws + (((c0 + 1) ^ (r & 15)) << 4));
     }
+    // x as bf16 for the GEMMs (fp32 x, first expert group only): thread -> row tid / 8,
+    // 16 values at (tid % 8) * 16
+    if (sizeof(XT) == 4 && xbf_out && blockIdx.y == 0 && tid < 256) {
+      const int r = tid >> 3, k16 = (tid & 7) * 16;
+      const int64_t t = tok0 + r;
+      if (t < N) {
+        u32x4 v4[4];
+#pragma unroll
+        for (int h = 0; h < 4; ++h) v4[h] = lds_read16(sb + r * R::XROW + ((((k16 >> 2) + h) ^ (r & 15)) << 4));
+        lds_wait_all(v4[0], v4[1], v4[2], v4[3]);
+        uint32_t pk[8];
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+          pk[2 * h] = (uint32_t)f32_to_bf16(__uint_as_float(v4[h].x)) |
+                      ((uint32_t)f32_to_bf16(__uint_as_float(v4[h].y)) << 16);
+          pk[2 * h + 1] = (uint32_t)f32_to_bf16(__uint_as_float(v4[h].z)) |
+                          ((uint32_t)f32_to_bf16(__uint_as_float(v4[h].w)) << 16);
+        }
+        uint4* dst = (uint4*)(xbf_out + t * H + c * RL_KC + k16);
+        dst[0] = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+        dst[1] = make_uint4(pk[4], pk[5], pk[6], pk[7]);
+      }
+    }
+    lds_wait_all(xq[0], xq[1]);
+#pragma unroll
+    for (int b = 0; b < TE; ++b) lds_wait_all(wq[b][0], wq[b][1]);
+    float xv[8], wv[TE][8];
+    if (sizeof(XT) == 4) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        xv[4 * h] = __uint_as_float(xq[h].x);
+        xv[4 * h + 1] = __uint_as_float(xq[h].y);
+        xv[4 * h + 2] = __uint_as_float(xq[h].z);
+        xv[4 * h + 3] = __uint_as_float(xq[h].w);
+      }
+    } else {
+      const uint32_t uw[4] = {xq[0].x, xq[0].y, xq[0].z, xq[0].w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        xv[2 * i] = __uint_as_float(uw[i] << 16);
+        xv[2 * i + 1] = __uint_as_float(uw[i] & 0xffff0000u);
+      }
+    }
+#pragma unroll
+    for (int b = 0; b < TE; ++b)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        wv[b][4 * h] = __uint_as_float(wq[b][h].x);
+        wv[b][4 * h + 1] = __uint_as_float(wq[b][h].y);
+        wv[b][4 * h + 2] = __uint_as_float(wq[b][h].z);
+        wv[b][4 * h + 3] = __uint_as_float(wq[b][h].w);
+      }
 #pragma unroll
     for (int j = 0; j < 8; ++j)
 #pragma unroll

@@ -24,6 +24,26 @@ __device__ __forceinline__ void gv_wait(u32x4& a0, u32x4& a1, u32x4& b0, u32x4& 
   asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(a0), "+v"(a1), "+v"(b0), "+v"(b1) : "n"(N));
 }
 
+// 16-byte LDS read at a byte address, invisible to the compiler's memory model: it cannot
+// be ordered after (made to wait for) LDS-DMA writes the compiler sees as aliasing stores.
+// The caller orders it with its own waits (s_waitcnt vmcnt + s_barrier before, lds_wait_all
+// after).
+__device__ __forceinline__ u32x4 lds_read16(uint32_t lds_addr) {
+  u32x4 v;
+  asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(lds_addr));
+  return v;
+}
+template <typename T>
+__device__ __forceinline__ void lds_tie(T& v) {
+  asm volatile("" : "+v"(v));
+}
+// Every LDS read of this wave has returned; the values v... are used only after this point.
+template <typename... T>
+__device__ __forceinline__ void lds_wait_all(T&... v) {
+  asm volatile("s_waitcnt lgkmcnt(0)");
+  (lds_tie(v), ...);
+}
+
 __device__ __forceinline__ f32x16_t mfma32v(u32x4 a, u32x4 b, f32x16_t c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c,
                                                  0, 0, 0);
