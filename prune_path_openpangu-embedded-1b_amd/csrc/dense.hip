@@ -580,7 +580,6 @@ __global__ __launch_bounds__(512, 1) void route_logits_kernel(const XT* __restri
         xq[1] = lds_read16(sb + r * R::XROW + (((c0 + 1) ^ (r & 15)) << 4));
       } else {
         xq[0] = lds_read16(sb + r * R::XROW + (((4 * kq + g) ^ (r & 15)) << 4));
-        xq[1] = xq[0];
       }
     }
 #pragma unroll
@@ -614,7 +613,10 @@ __global__ __launch_bounds__(512, 1) void route_logits_kernel(const XT* __restri
         dst[1] = make_uint4(pk[4], pk[5], pk[6], pk[7]);
       }
     }
-    lds_wait_all(xq[0], xq[1]);
+    // no copy of a fragment may exist before its wait (a copy made earlier would hold the
+    // registers' old contents): bf16 x waits on its one fragment alone
+    if constexpr (sizeof(XT) == 4) lds_wait_all(xq[0], xq[1]);
+    else lds_wait_all(xq[0]);
 #pragma unroll
     for (int b = 0; b < TE; ++b) lds_wait_all(wq[b][0], wq[b][1]);
     float xv[8], wv[TE][8];

@@ -12,7 +12,7 @@
 // of the grouped GEMMs. Replaces moe_local_scan_kernel / moe_global_scan_kernel /
 // moe_dispatch_kernel (src/tl_kernel_optimized_Ultimate_PanGU.py:133-266) without the
 // 512-tile cap of the global scan (:176, 206-208) and without the host sync (:581).
-#include "pp_common.h"
+#include "gemm_lds.h"
 
 #define ROUTE_TOK 16   // tokens per workgroup (one 16-row MFMA tile)
 #define ROUTE_WAVES 4  // K split across the waves, then 4 selections per wave
@@ -202,10 +202,9 @@ struct Rt16 {
   static constexpr int STAGE = 16 * (XROW + RT16_RROW);
   static constexpr int DMA = sizeof(XT) == 4 ? 4 : 3;     // DMA instructions per wave per stage
 };
-typedef __attribute__((address_space(3))) void rt_lds_t;
 
 __device__ __forceinline__ void rt16_dma(const void* src, unsigned char* lds) {
-  __builtin_amdgcn_global_load_lds(src, (rt_lds_t*)lds, 16, 0, 0);
+  __builtin_amdgcn_global_load_lds(src, (lds_void_t*)lds, 16, 0, 0);
 }
 
 template <int N>
@@ -324,6 +323,7 @@ __global__ __launch_bounds__(64 * RT16_WAVES) void route16_kernel(
   if (tid < 16) cnt_s[tid] = 0;
   {
     __shared__ __align__(16) unsigned char stg[RT16_STAGES * Rt16<XT>::STAGE];
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void_t*)stg;
     const int t_l = lane & 15, g = lane >> 4;
     const int nst = (H + RT16_KC - 1) / RT16_KC;
     auto chunk_w = [&](int sidx) { return min(RT16_KC, H - sidx * RT16_KC); };
@@ -340,20 +340,23 @@ __global__ __launch_bounds__(64 * RT16_WAVES) void route16_kernel(
       if (sidx + 2 < nst) rt16_wait_barrier<2 * Rt16<XT>::DMA>();
       else if (sidx + 1 < nst) rt16_wait_barrier<Rt16<XT>::DMA>();
       else rt16_wait_barrier<0>();
-      unsigned char* st = stg + (sidx % RT16_STAGES) * Rt16<XT>::STAGE;
+      // LDS reads through asm (lds_read16): ordered after this chunk's DMAs by the wait and
+      // barrier above, and not made to wait for the later chunks' DMAs still in flight
+      const uint32_t sb = lds0 + (uint32_t)((sidx % RT16_STAGES) * Rt16<XT>::STAGE);
       const int kw = chunk_w(sidx);
       // x as bf16 for the grouped GEMMs (fp32 x only): thread -> row tid / 32, 8 values
       if (sizeof(XT) == 4 && xbf_out) {
         const int r = tid >> 5, k8 = (tid & 31) * 8;
         const int64_t t = tok0 + r;
         if (t < N && k8 < kw) {
-          const float4 v0 = *(const float4*)(st + r * Rt16<XT>::XROW + (((k8 >> 2) ^ r) << 4));
-          const float4 v1 = *(const float4*)(st + r * Rt16<XT>::XROW + ((((k8 >> 2) + 1) ^ r) << 4));
+          u32x4 v0 = lds_read16(sb + r * Rt16<XT>::XROW + (((k8 >> 2) ^ r) << 4));
+          u32x4 v1 = lds_read16(sb + r * Rt16<XT>::XROW + ((((k8 >> 2) + 1) ^ r) << 4));
+          lds_wait_all(v0, v1);
           uint4 pk;
-          pk.x = (uint32_t)f32_to_bf16(v0.x) | ((uint32_t)f32_to_bf16(v0.y) << 16);
-          pk.y = (uint32_t)f32_to_bf16(v0.z) | ((uint32_t)f32_to_bf16(v0.w) << 16);
-          pk.z = (uint32_t)f32_to_bf16(v1.x) | ((uint32_t)f32_to_bf16(v1.y) << 16);
-          pk.w = (uint32_t)f32_to_bf16(v1.z) | ((uint32_t)f32_to_bf16(v1.w) << 16);
+          pk.x = (uint32_t)f32_to_bf16(__uint_as_float(v0.x)) | ((uint32_t)f32_to_bf16(__uint_as_float(v0.y)) << 16);
+          pk.y = (uint32_t)f32_to_bf16(__uint_as_float(v0.z)) | ((uint32_t)f32_to_bf16(__uint_as_float(v0.w)) << 16);
+          pk.z = (uint32_t)f32_to_bf16(__uint_as_float(v1.x)) | ((uint32_t)f32_to_bf16(__uint_as_float(v1.y)) << 16);
+          pk.w = (uint32_t)f32_to_bf16(__uint_as_float(v1.z)) | ((uint32_t)f32_to_bf16(__uint_as_float(v1.w)) << 16);
           *(uint4*)(xbf_out + t * H + sidx * RT16_KC + k8) = pk;
         }
       }
@@ -362,30 +365,31 @@ __global__ __launch_bounds__(64 * RT16_WAVES) void route16_kernel(
                        stg + ((sidx + RT16_STAGES - 1) % RT16_STAGES) * Rt16<XT>::STAGE, w, lane);
       if (32 * w < kw) {  // this wave's K block of the chunk
         float xv[8], wv8[8];
+        const int c0 = 8 * w + 2 * g;
+        u32x4 xq[2], wq[2];
         if (sizeof(XT) == 4) {
-          const int c0 = 8 * w + 2 * g;
-          const float4 a0 = *(const float4*)(st + t_l * Rt16<XT>::XROW + ((c0 ^ t_l) << 4));
-          const float4 a1 = *(const float4*)(st + t_l * Rt16<XT>::XROW + (((c0 + 1) ^ t_l) << 4));
-          xv[0] = a0.x; xv[1] = a0.y; xv[2] = a0.z; xv[3] = a0.w;
-          xv[4] = a1.x; xv[5] = a1.y; xv[6] = a1.z; xv[7] = a1.w;
+          xq[0] = lds_read16(sb + t_l * Rt16<XT>::XROW + ((c0 ^ t_l) << 4));
+          xq[1] = lds_read16(sb + t_l * Rt16<XT>::XROW + (((c0 + 1) ^ t_l) << 4));
         } else {
-          const int c = 4 * w + g;
-          const uint4 u = *(const uint4*)(st + t_l * Rt16<XT>::XROW + ((c ^ t_l) << 4));
-          const uint32_t uw[4] = {u.x, u.y, u.z, u.w};
+          xq[0] = lds_read16(sb + t_l * Rt16<XT>::XROW + (((4 * w + g) ^ t_l) << 4));
+        }
+        const uint32_t rs = sb + 16 * Rt16<XT>::XROW + t_l * RT16_RROW;  // expert row l % 16
+        wq[0] = lds_read16(rs + ((c0 ^ t_l) << 4));
+        wq[1] = lds_read16(rs + (((c0 + 1) ^ t_l) << 4));
+        if constexpr (sizeof(XT) == 4) lds_wait_all(xq[0], xq[1], wq[0], wq[1]);
+        else lds_wait_all(xq[0], wq[0], wq[1]);
+        if (sizeof(XT) == 4) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) xv[i] = __uint_as_float(xq[i >> 2][i & 3]);
+        } else {
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            xv[2 * i] = __uint_as_float(uw[i] << 16);
-            xv[2 * i + 1] = __uint_as_float(uw[i] & 0xffff0000u);
+            xv[2 * i] = __uint_as_float(xq[0][i] << 16);
+            xv[2 * i + 1] = __uint_as_float(xq[0][i] & 0xffff0000u);
           }
         }
-        {
-          const unsigned char* rs = st + 16 * Rt16<XT>::XROW + t_l * RT16_RROW;  // expert row l % 16
-          const int c0 = 8 * w + 2 * g;
-          const float4 b0 = *(const float4*)(rs + ((c0 ^ t_l) << 4));
-          const float4 b1 = *(const float4*)(rs + (((c0 + 1) ^ t_l) << 4));
-          wv8[0] = b0.x; wv8[1] = b0.y; wv8[2] = b0.z; wv8[3] = b0.w;
-          wv8[4] = b1.x; wv8[5] = b1.y; wv8[6] = b1.z; wv8[7] = b1.w;
-        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) wv8[i] = __uint_as_float(wq[i >> 2][i & 3]);
 #pragma unroll
         for (int j = 0; j < 8; ++j) acc[j & 3] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[j], wv8[j], acc[j & 3], 0, 0, 0);
       }
