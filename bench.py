@@ -63,6 +63,8 @@ def parse():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the small-batch (config 3) and E=192/G=32 side measurements")
+    ap.add_argument("--side", default="all",
+                    help="side sections to run, comma-separated: eager, small, e192, masked, stack (default all)")
     ap.add_argument("--small-batch-only", action="store_true",
                     help="run only the config-3 small-batch section (both paths) and print its numbers")
     ap.add_argument("--grid", type=int, default=0, help="decode workgroups (0 = library default)")
@@ -310,6 +312,32 @@ def small_batch(ops, gi, torch, np, layers, dev, g, reps=1):
     return extra
 
 
+def mfma_ceiling(pkg, torch, iters=200, reps=20):
+    """bf16 MFMA rate on register operands (libpp_bench.so, measurement support built beside
+    the library): one 8-wave workgroup per CU, the dense GEMMs' 4 x 2 wave tile of
+    v_mfma_f32_32x32x16_bf16, random-sign and all-zero operands. The chip's clock under MFMA
+    load depends on the operand bits, so this is the rate the GEMMs' MFMA work can reach on
+    data like theirs; `iters` sets a launch near their length (tens of us)."""
+    import ctypes
+
+    import numpy as np
+    lib = ctypes.CDLL(os.path.join(os.path.dirname(pkg.__file__), "libpp_bench.so"))
+    lib.ppb_mfma_rate.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                  ctypes.POINTER(ctypes.c_float)]
+    grid = torch.cuda.get_device_properties(0).multi_processor_count
+    flops = grid * 8.0 * iters * 8 * 32768.0
+    res = {"grid": grid, "waves_per_cu": 8, "iters": iters, "launches": reps}
+    for name, mode in (("random_sign", 1), ("zero", 0)):
+        ms = (ctypes.c_float * reps)()
+        rc = lib.ppb_mfma_rate(grid, iters, mode, reps, ms)
+        if rc:
+            raise RuntimeError(f"ppb_mfma_rate: HIP error {rc}")
+        med = float(np.median(np.frombuffer(ms, dtype=np.float32)))
+        res[name] = {"us_per_launch": med * 1e3, "tflops": flops / (med * 1e-3) / 1e12,
+                     "frac_of_peak": flops / (med * 1e-3) / 1e12 / PEAK_BF16_TFLOPS}
+    return res
+
+
 def main():
     args = parse()
     if args.pmc_summary:
@@ -508,135 +536,150 @@ def main():
             "mfma_util": (fl_gu + fl_dn) / ((gu_ms + dn_ms) * 1e-3) / (PEAK_BF16_TFLOPS * 1e12),
             "layer_mfma_util": (6.0 * P_mean * H * G) / (pf_ms * 1e-3) / (PEAK_BF16_TFLOPS * 1e12),
         }
+        # the MFMA rate reachable on random bf16 operands, beside the GEMMs' own rate
+        ceil = mfma_ceiling(pkg, torch)
+        prefill["mfma_ceiling"] = ceil
+        prefill["mfma_util_of_ceiling"] = ((fl_gu + fl_dn) / ((gu_ms + dn_ms) * 1e-3) / 1e12
+                                           / ceil["random_sign"]["tflops"])
 
     # ---------------- side measurements (not the headline value)
     extra = None
+    sides = set(args.side.split(","))
+
+    def want(name):
+        return "all" in sides or name in sides
+
     if not args.no_extra:
         extra = {}
-        extra["eager_decode"] = eager_decode(pkg, ops, torch, layers[0], xs[0], E, G, args.tau, dev, g)
-        extra.update(small_batch(ops, gi, torch, np, layers, dev, g))
-        # real-checkpoint shape: E=192 experts of G=32, one layer, decode bs=1 and prefill 2048
-        E2, G2 = 192, 32
-        l192 = []
-        NS = 8
-        for l in range(NS):
-            g.manual_seed(2000 + l)
-            wg = torch.randn(I, H, device=dev, generator=g) * 0.02
-            wu = torch.randn(I, H, device=dev, generator=g) * 0.02
-            wd = torch.randn(H, I, device=dev, generator=g) * 0.02
-            wr = torch.randn(E2, H, device=dev, generator=g) * 0.02
-            perm = torch.randperm(I, device=dev, generator=g).to(torch.int32)
-            l192.append((ops.pack_experts(wg, wu, wd, E2, G2, perm=perm, layout="linear"),
-                         ops.pack_router(wr, layout="linear"), ops.decode_workspace(H, E2, dev)))
-            del wg, wu, wd
-        R = 64
-        xd = torch.randn(R, H, device=dev, generator=g)
-        od = torch.empty(R, H, dtype=torch.bfloat16, device=dev)
-        kk = []
-        for r in range(R):
-            packed, rp, ws = l192[r % NS]
-            ops.moe_decode(xd[r], rp, None, E2, G2, args.tau, packed, ws, out=od[r:r + 1])
-            kk.append(ops.decode_state(ws, E2)["k"])
-        gd = torch.cuda.CUDAGraph()
-        sd_ = torch.cuda.Stream()
-        sd_.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(sd_):
-            with torch.cuda.graph(gd, stream=sd_):
-                for r in range(R):
-                    packed, rp, ws = l192[r % NS]
-                    ops.moe_decode(xd[r], rp, None, E2, G2, args.tau, packed, ws, out=od[r:r + 1])
-        torch.cuda.current_stream().wait_stream(sd_)
-        gd.replay()
-        torch.cuda.synchronize()
-        e0.record()
-        gd.replay()
-        e1.record()
-        torch.cuda.synchronize()
-        us = e0.elapsed_time(e1) * 1000.0 / R
-        k2 = float(np.mean(kk))
-        byt = k2 * 3 * H * G2 * 2 + 192 * H * 4 + H * 6
-        extra["e192_g32_decode"] = {"us_per_layer": us, "k_mean": k2, "hbm_gbs": byt / (us * 1e-6) / 1e9,
-                                    "weight_sets": NS}
-        # the same shape's prefill (2048 tokens): G = 32 takes the dense form (router logits,
-        # selection, dense gate/up over every neuron with the gate 0 for unselected experts,
-        # dense down), one pass; calls rotate over the weight sets, graph-replayed like the
-        # configured shape's prefill
-        if not args.no_prefill:
-            Np, Rp = args.prefill_tokens, 2 * NS
-            xp2 = torch.randn(Rp, Np, H, device=dev, generator=g)
-            wsp = torch.empty(ops.prefill_workspace_bytes(Np, H, E2, G2), dtype=torch.uint8, device=dev)
-            opf = torch.empty(Np, H, dtype=torch.bfloat16, device=dev)
-            P2 = 0
-            for r in range(Rp):
-                packed, rp, _ = l192[r % NS]
-                P2 += int(ops.route(xp2[r], rp, E2, args.tau)["count"].sum())
-                ops.moe_prefill(xp2[r], rp, None, E2, G2, args.tau, packed, workspace=wsp, out=opf)
-            torch.cuda.synchronize()
-            gq = torch.cuda.CUDAGraph()
-            sq = torch.cuda.Stream()
-            sq.wait_stream(torch.cuda.current_stream())
-            with torch.cuda.stream(sq):
-                with torch.cuda.graph(gq, stream=sq):
-                    for r in range(Rp):
-                        packed, rp, _ = l192[r % NS]
-                        ops.moe_prefill(xp2[r], rp, None, E2, G2, args.tau, packed, workspace=wsp, out=opf)
-            torch.cuda.current_stream().wait_stream(sq)
-            gq.replay()
+        if want("eager"):
+            extra["eager_decode"] = eager_decode(pkg, ops, torch, layers[0], xs[0], E, G, args.tau, dev, g)
+        if want("small"):
+            extra.update(small_batch(ops, gi, torch, np, layers, dev, g))
+        if want("e192"):
+            # real-checkpoint shape: E=192 experts of G=32, one layer, decode bs=1 and prefill 2048
+            E2, G2 = 192, 32
+            l192 = []
+            NS = 8
+            for l in range(NS):
+                g.manual_seed(2000 + l)
+                wg = torch.randn(I, H, device=dev, generator=g) * 0.02
+                wu = torch.randn(I, H, device=dev, generator=g) * 0.02
+                wd = torch.randn(H, I, device=dev, generator=g) * 0.02
+                wr = torch.randn(E2, H, device=dev, generator=g) * 0.02
+                perm = torch.randperm(I, device=dev, generator=g).to(torch.int32)
+                l192.append((ops.pack_experts(wg, wu, wd, E2, G2, perm=perm, layout="linear"),
+                             ops.pack_router(wr, layout="linear"), ops.decode_workspace(H, E2, dev)))
+                del wg, wu, wd
+            R = 64
+            xd = torch.randn(R, H, device=dev, generator=g)
+            od = torch.empty(R, H, dtype=torch.bfloat16, device=dev)
+            kk = []
+            for r in range(R):
+                packed, rp, ws = l192[r % NS]
+                ops.moe_decode(xd[r], rp, None, E2, G2, args.tau, packed, ws, out=od[r:r + 1])
+                kk.append(ops.decode_state(ws, E2)["k"])
+            gd = torch.cuda.CUDAGraph()
+            sd_ = torch.cuda.Stream()
+            sd_.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(sd_):
+                with torch.cuda.graph(gd, stream=sd_):
+                    for r in range(R):
+                        packed, rp, ws = l192[r % NS]
+                        ops.moe_decode(xd[r], rp, None, E2, G2, args.tau, packed, ws, out=od[r:r + 1])
+            torch.cuda.current_stream().wait_stream(sd_)
+            gd.replay()
             torch.cuda.synchronize()
             e0.record()
-            gq.replay()
-            e1.record()
-            torch.cuda.synchronize()
-            ms2 = e0.elapsed_time(e1) / Rp
-            P2 /= Rp
-            dense_fl = 6.0 * Np * H * (E2 * G2)
-            extra["e192_g32_prefill"] = {
-                "tokens": Np, "tau": args.tau, "pairs_mean": P2, "ms_per_call": ms2,
-                "tokens_per_s": Np / (ms2 * 1e-3), "form": "dense (G % 64 != 0)", "weight_sets": NS,
-                "layer_mfma_util": 6.0 * P2 * H * G2 / (ms2 * 1e-3) / (PEAK_BF16_TFLOPS * 1e12),
-                "dense_flops": dense_fl,
-                "dense_mfma_util": dense_fl / (ms2 * 1e-3) / (PEAK_BF16_TFLOPS * 1e12)}
-            del wsp, opf, xp2, gq
-        del l192
-        # masked training path: the expert gating of MoELayer.forward and its backward on
-        # a training batch of 16 x 1024 tokens, bf16 activations [16384, 6144] (200 MB per
-        # tensor, beyond the MALL); bytes = activations read + written (+ gates)
-        torch.cuda.empty_cache()
-        Nt = 16384
-        ids = torch.randperm(I, device=dev, generator=g) % E
-        lay = ops.masked_gate_layout(ids, E)
-        inter = torch.randn(Nt, I, device=dev, generator=g).to(torch.bfloat16)
-        d_o = torch.randn(Nt, I, device=dev, generator=g).to(torch.bfloat16)
-        gts = torch.rand(Nt, E, device=dev, generator=g)
-        mg = {}
-        for name, fn, byt in (
-                ("fwd", lambda: ops.masked_gate_fwd(inter, gts, lay[0]), 2 * Nt * I * 2 + Nt * E * 4),
-                ("bwd", lambda: ops.masked_gate_bwd(d_o, inter, gts, *lay), 3 * Nt * I * 2 + 2 * Nt * E * 4)):
-            fn()
-            torch.cuda.synchronize()
-            R = 10
-            gm = torch.cuda.CUDAGraph()
-            sm = torch.cuda.Stream()
-            sm.wait_stream(torch.cuda.current_stream())
-            with torch.cuda.stream(sm):
-                with torch.cuda.graph(gm, stream=sm):
-                    for _ in range(R):
-                        fn()
-            torch.cuda.current_stream().wait_stream(sm)
-            gm.replay()
-            torch.cuda.synchronize()
-            e0.record()
-            gm.replay()
+            gd.replay()
             e1.record()
             torch.cuda.synchronize()
             us = e0.elapsed_time(e1) * 1000.0 / R
-            mg[name] = {"us": us, "hbm_gbs": byt / (us * 1e-6) / 1e9, "frac": byt / (us * 1e-6) / 1e9 / PEAK_HBM_GBS}
-            del gm
-        extra["masked_gate_train"] = {"rows": Nt, "intermediate": I, "experts": E, "dtype": "bf16", **mg}
-        del inter, d_o, gts
-        # config 5: 26-layer decoder-shaped stack, 1024-token prompt + 128 greedy steps
-        torch.cuda.empty_cache()
-        extra["decoder_stack"] = pkg.decoder_stack.run(prompt_len=1024, steps=128, layers=26, tau=args.tau)
+            k2 = float(np.mean(kk))
+            byt = k2 * 3 * H * G2 * 2 + 192 * H * 4 + H * 6
+            extra["e192_g32_decode"] = {"us_per_layer": us, "k_mean": k2, "hbm_gbs": byt / (us * 1e-6) / 1e9,
+                                        "weight_sets": NS}
+            # the same shape's prefill (2048 tokens): G = 32 takes the dense form (router logits,
+            # selection, dense gate/up over every neuron with the gate 0 for unselected experts,
+            # dense down), one pass; calls rotate over the weight sets, graph-replayed like the
+            # configured shape's prefill
+            if not args.no_prefill:
+                Np, Rp = args.prefill_tokens, 2 * NS
+                xp2 = torch.randn(Rp, Np, H, device=dev, generator=g)
+                wsp = torch.empty(ops.prefill_workspace_bytes(Np, H, E2, G2), dtype=torch.uint8, device=dev)
+                opf = torch.empty(Np, H, dtype=torch.bfloat16, device=dev)
+                P2 = 0
+                for r in range(Rp):
+                    packed, rp, _ = l192[r % NS]
+                    P2 += int(ops.route(xp2[r], rp, E2, args.tau)["count"].sum())
+                    ops.moe_prefill(xp2[r], rp, None, E2, G2, args.tau, packed, workspace=wsp, out=opf)
+                torch.cuda.synchronize()
+                gq = torch.cuda.CUDAGraph()
+                sq = torch.cuda.Stream()
+                sq.wait_stream(torch.cuda.current_stream())
+                with torch.cuda.stream(sq):
+                    with torch.cuda.graph(gq, stream=sq):
+                        for r in range(Rp):
+                            packed, rp, _ = l192[r % NS]
+                            ops.moe_prefill(xp2[r], rp, None, E2, G2, args.tau, packed, workspace=wsp, out=opf)
+                torch.cuda.current_stream().wait_stream(sq)
+                gq.replay()
+                torch.cuda.synchronize()
+                e0.record()
+                gq.replay()
+                e1.record()
+                torch.cuda.synchronize()
+                ms2 = e0.elapsed_time(e1) / Rp
+                P2 /= Rp
+                dense_fl = 6.0 * Np * H * (E2 * G2)
+                extra["e192_g32_prefill"] = {
+                    "tokens": Np, "tau": args.tau, "pairs_mean": P2, "ms_per_call": ms2,
+                    "tokens_per_s": Np / (ms2 * 1e-3), "form": "dense (G % 64 != 0)", "weight_sets": NS,
+                    "layer_mfma_util": 6.0 * P2 * H * G2 / (ms2 * 1e-3) / (PEAK_BF16_TFLOPS * 1e12),
+                    "dense_flops": dense_fl,
+                    "dense_mfma_util": dense_fl / (ms2 * 1e-3) / (PEAK_BF16_TFLOPS * 1e12)}
+                del wsp, opf, xp2, gq
+            del l192
+        if want("masked"):
+            # masked training path: the expert gating of MoELayer.forward and its backward on
+            # a training batch of 16 x 1024 tokens, bf16 activations [16384, 6144] (200 MB per
+            # tensor, beyond the MALL); bytes = activations read + written (+ gates)
+            torch.cuda.empty_cache()
+            Nt = 16384
+            ids = torch.randperm(I, device=dev, generator=g) % E
+            lay = ops.masked_gate_layout(ids, E)
+            inter = torch.randn(Nt, I, device=dev, generator=g).to(torch.bfloat16)
+            d_o = torch.randn(Nt, I, device=dev, generator=g).to(torch.bfloat16)
+            gts = torch.rand(Nt, E, device=dev, generator=g)
+            mg = {}
+            for name, fn, byt in (
+                    ("fwd", lambda: ops.masked_gate_fwd(inter, gts, lay[0]), 2 * Nt * I * 2 + Nt * E * 4),
+                    ("bwd", lambda: ops.masked_gate_bwd(d_o, inter, gts, *lay), 3 * Nt * I * 2 + 2 * Nt * E * 4)):
+                fn()
+                torch.cuda.synchronize()
+                R = 10
+                gm = torch.cuda.CUDAGraph()
+                sm = torch.cuda.Stream()
+                sm.wait_stream(torch.cuda.current_stream())
+                with torch.cuda.stream(sm):
+                    with torch.cuda.graph(gm, stream=sm):
+                        for _ in range(R):
+                            fn()
+                torch.cuda.current_stream().wait_stream(sm)
+                gm.replay()
+                torch.cuda.synchronize()
+                e0.record()
+                gm.replay()
+                e1.record()
+                torch.cuda.synchronize()
+                us = e0.elapsed_time(e1) * 1000.0 / R
+                mg[name] = {"us": us, "hbm_gbs": byt / (us * 1e-6) / 1e9, "frac": byt / (us * 1e-6) / 1e9 / PEAK_HBM_GBS}
+                del gm
+            extra["masked_gate_train"] = {"rows": Nt, "intermediate": I, "experts": E, "dtype": "bf16", **mg}
+            del inter, d_o, gts
+        if want("stack"):
+            # config 5: 26-layer decoder-shaped stack, 1024-token prompt + 128 greedy steps
+            torch.cuda.empty_cache()
+            extra["decoder_stack"] = pkg.decoder_stack.run(prompt_len=1024, steps=128, layers=26, tau=args.tau)
 
     # ---------------- CPU baseline: the reference's dense masked layer, torch fp32 on the host
     cpu = None if args.no_cpu else cpu_baseline(args)
