@@ -31,7 +31,6 @@
 #include "gemm_lds.h"
 
 #define DG_MAX_GRID 256  // workgroups of a GEMM launch; also the split workspace's part slots
-#define DG_GX 8          // experts a 128-neuron column tile can touch (G >= 32: at most 5)
 #ifndef DG_GU_GR
 #define DG_GU_GR (1 << 30)  // gate/up items: every row tile of a column tile, then the next
 #endif
@@ -115,6 +114,17 @@ __device__ __forceinline__ void dg_read(u32x4 (&v)[N], uint32_t base) {
   }
 }
 
+// Epilogue rows per pass: the largest multiple of 32 that divides the wave tile's wm rows
+// and is at most rp0 (what the wave's staging holds).
+__host__ __device__ constexpr int dg_pass_rows(int wm, int rp0) {
+  int r = wm;
+  while (r > 32 && (r > rp0 || wm % r != 0)) r -= 32;
+  return r;
+}
+static_assert(dg_pass_rows(128, 96) == 64 && dg_pass_rows(128, 128) == 128 && dg_pass_rows(64, 192) == 64 &&
+                  dg_pass_rows(128, 64) == 64,
+              "epilogue pass rows");
+
 // Item -> (row tile rt, launch column tile ctl): row tiles in groups of gr, each group
 // taken column by column (gr >= n_rt: every row tile of a column, then the next column).
 // The workgroups of one XCD take consecutive items, so gr sets the block of row x column
@@ -128,20 +138,24 @@ __device__ __forceinline__ void dg_tile(int item, int n_rt, int n_ct, int gr, in
   rt = q * gr + (r - ctl * rows);
 }
 
-template <int MODE, int BM, int BN, int BK, int STAGES, int NW, int WR>
-__global__ __launch_bounds__(NW * 64, 1) void dense_gemm_kernel(DgArgs p) {
+template <int MODE, int BM, int BN, int BK, int STAGES, int NW, int WR, int WPC>
+__global__ __launch_bounds__(NW * 64, WPC) void dense_gemm_kernel(DgArgs p) {
   using C = Dg<BM, BN, BK, NW, WR>;
   constexpr int NB2 = BN / 2;  // MODE 0: neurons of a column tile (their gate and up rows)
+  // MODE 0: experts a column tile can touch, rounded up to a power of two (G >= 32: a
+  // 128-neuron tile touches at most 5, a 64-neuron tile 3)
+  constexpr int GX = NB2 > 64 ? 8 : 4;
   static_assert(BM == 128 || BM == 256, "tile rows");
   static_assert(NW == 4 || NW == 8, "waves");
   static_assert(C::MI >= 1 && C::NJ >= 2 && (MODE == 1 || C::NJ % 2 == 0) && C::MI * 32 * WR == BM &&
                     C::NJ * 32 * C::WN == BN && C::NIA * NW * C::RPI == BM && C::NIB * NW * C::RPI == BN,
                 "tile shape");
-  static_assert(MODE == 1 || (NB2 + 31) / 32 + 1 <= DG_GX, "experts a column tile can touch");
-  static_assert(STAGES >= 2 && STAGES * C::STAGE + (MODE == 0 ? BM * DG_GX * 4 : 0) <= 160 * 1024 - 64, "LDS");
+  static_assert(MODE == 1 || (NB2 + 31) / 32 + 1 <= GX, "experts a column tile can touch");
+  static_assert(STAGES >= 2 && WPC * (STAGES * C::STAGE + (MODE == 0 ? BM * GX * 4 : 0) + 64) <= 160 * 1024,
+                "LDS of WPC workgroups per CU");
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ int role_s;
-  __shared__ float gate_s[MODE == 0 ? BM * DG_GX : 1];  // MODE 0 epilogue: the tile's router gates
+  __shared__ float gate_s[MODE == 0 ? BM * GX : 1];  // MODE 0 epilogue: the tile's router gates
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform, in an SGPR
   const int wm = w / C::WN, wn = w % C::WN;
@@ -271,8 +285,8 @@ __global__ __launch_bounds__(NW * 64, 1) void dense_gemm_kernel(DgArgs p) {
         for (int q = 0; q < 16; ++q) acc[i][j][q] = 0.0f;
     // MODE 0: the tile's router gates (rows x the experts its 128 neurons touch), loaded at
     // the item's first block and written to gate_s at its second: ready for the epilogue
-    // without a memory round trip there (gate_s[r * DG_GX + k]: row r, expert e_lo + k)
-    constexpr int NGL = MODE == 0 ? BM * DG_GX / C::NT : 1;
+    // without a memory round trip there (gate_s[r * GX + k]: row r, expert e_lo + k)
+    constexpr int NGL = MODE == 0 ? BM * GX / C::NT : 1;
     float gl[NGL];
     const int kb_first = part ? sc.kb_lo : 0;
     auto gates_store = [&]() {
@@ -292,7 +306,7 @@ __global__ __launch_bounds__(NW * 64, 1) void dense_gemm_kernel(DgArgs p) {
         const int64_t tt0 = (int64_t)rt * BM;
 #pragma unroll
         for (int c = 0; c < NGL; ++c) {
-          const int idx = tid + c * C::NT, r = idx / DG_GX, k = idx % DG_GX;
+          const int idx = tid + c * C::NT, r = idx / GX, k = idx % GX;
           gl[c] = (k < ne && tt0 + r < p.N) ? p.gates[(tt0 + r) * p.E + e_lo + k] : 0.0f;
         }
       } else if (MODE == 0 && kb == kb_first + 1) {
@@ -421,7 +435,7 @@ __global__ __launch_bounds__(NW * 64, 1) void dense_gemm_kernel(DgArgs p) {
               if (MODE == 0) {
                 const int n = ct * NB2 + wn * (C::WC / 2) + col;
                 if (n >= p.Ipad) continue;
-                const float gt = n < p.I ? gate_s[(wm * C::WM + rl) * DG_GX + n / p.G - ct * NB2 / p.G] : 0.0f;
+                const float gt = n < p.I ? gate_s[(wm * C::WM + rl) * GX + n / p.G - ct * NB2 / p.G] : 0.0f;
                 const float a = gt == 0.0f ? 0.0f : dg_silu(sv[h]) * tv[h] * gt;
                 p.out[(t0 + rl) * p.Ipad + n] = f32_to_bf16(a);
               } else {
@@ -453,7 +467,7 @@ __global__ __launch_bounds__(NW * 64, 1) void dense_gemm_kernel(DgArgs p) {
       constexpr int GB = GB0 < NB ? GB0 : NB;            // blocks per pass
       constexpr int RW = GB * 64;                        // bytes of an LDS row
       constexpr int RP0 = C::EPW / RW / 32 * 32;
-      constexpr int RP = RP0 < C::WM ? RP0 : C::WM;      // rows per pass
+      constexpr int RP = dg_pass_rows(C::WM, RP0);       // rows per pass
       static_assert(GB >= 1 && RP >= 32 && C::WM % RP == 0, "epilogue passes");
       const int c0 = MODE == 0 ? ct * NB2 + wn * (C::WC / 2) : ct * BN + wn * C::WC;  // first column
       const int ncol = MODE == 0 ? p.Ipad : p.H;
@@ -483,7 +497,7 @@ __global__ __launch_bounds__(NW * 64, 1) void dense_gemm_kernel(DgArgs p) {
 #pragma unroll
                 for (int q = 0; q < 16; ++q) {
                   const int rl = i * 32 + mfma32_row(q, ln);
-                  const float gt = real ? gate_s[(wm * C::WM + rl) * DG_GX + ek] : 0.0f;
+                  const float gt = real ? gate_s[(wm * C::WM + rl) * GX + ek] : 0.0f;
                   const float a = gt == 0.0f ? 0.0f : dg_silu(gv[q]) * uv[q] * gt;
                   *(bf16_t*)(ep + (rl - hf * RP) * RW + (nl - jg * 32) * 2) = f32_to_bf16(a);
                 }
@@ -744,7 +758,9 @@ int pp_route_impl(const void* x, int x_dtype, const float* logits_in, int64_t N,
 #ifndef DG_GU_BM
 #define DG_GU_BM 256
 #endif
+#ifndef DG_GU_BN
 #define DG_GU_BN 256  // both gate/up launches: 128-neuron column tiles
+#endif
 #ifndef DG_GU_BK
 #define DG_GU_BK 64
 #endif
@@ -795,6 +811,15 @@ int pp_route_impl(const void* x, int x_dtype, const float* logits_in, int64_t N,
 #endif
 #ifndef DG_DN_NW
 #define DG_DN_NW DG_NW
+#endif
+#ifndef DG_GU_WPC
+#define DG_GU_WPC 1  // workgroups per CU of each launch
+#endif
+#ifndef DG_GT_WPC
+#define DG_GT_WPC 1
+#endif
+#ifndef DG_DN_WPC
+#define DG_DN_WPC 1
 #endif
 #define DG_SYNC_WORDS (4 * DG_MAX_GRID)   // per GEMM launch: 2 counters per tail item
 // one part's fp32 partial sums: a tile of either K-split launch (gate/up tail, down)
@@ -848,10 +873,11 @@ static int dense_grid() {
   return std::max(8, std::min(DG_MAX_GRID, g));
 }
 
-template <int MODE, int BM, int BN, int BK, int ST, int NW, int WR>
-static int dense_gemm_launch(const DgArgs& a, hipStream_t st) {
-  dense_gemm_kernel<MODE, BM, BN, BK, ST, NW, WR>
-      <<<dense_grid(), NW * 64, ST * Dg<BM, BN, BK, NW, WR>::STAGE, st>>>(a);
+template <int MODE, int BM, int BN, int BK, int ST, int NW, int WR, int WPC>
+static int dense_gemm_launch(DgArgs a, hipStream_t st) {
+  if (WPC > 1) a.part = nullptr, a.sync = nullptr;  // the split slots are sized for dense_grid() parts
+  dense_gemm_kernel<MODE, BM, BN, BK, ST, NW, WR, WPC>
+      <<<dense_grid() * WPC, NW * 64, ST * Dg<BM, BN, BK, NW, WR>::STAGE, st>>>(a);
   return pp_check_launch(MODE == 0 ? "dense_gemm_kernel (gate/up)" : "dense_gemm_kernel (down)");
 }
 
@@ -901,7 +927,7 @@ static int dense_pass(const void* x, int x_dtype, int64_t n, int H, const float*
   a.Ipad = Ipad;
   // gate/up: column tiles [0, ct_main) in whole rounds of 256-row tiles, no K split; the
   // rest as 128-row tiles
-  const int grid = dense_grid();
+  const int grid = dense_grid() * DG_GU_WPC;
   const int ntc = (Ipad + DG_GU_BN / 2 - 1) / (DG_GU_BN / 2);
   const int64_t nrt = (n + DG_GU_BM - 1) / DG_GU_BM;
   const int ct_main = nrt * ntc >= grid ? (int)((nrt * ntc) / grid * grid / nrt) : 0;
@@ -911,12 +937,12 @@ static int dense_pass(const void* x, int x_dtype, int64_t n, int H, const float*
     m.sync = nullptr;
     m.ct_lo = 0;
     m.ct_hi = ct_main;
-    if ((rc = dense_gemm_launch<0, DG_GU_BM, DG_GU_BN, DG_GU_BK, DG_GU_ST, DG_GU_NW, DG_GU_WR>(m, st))) return rc;
+    if ((rc = dense_gemm_launch<0, DG_GU_BM, DG_GU_BN, DG_GU_BK, DG_GU_ST, DG_GU_NW, DG_GU_WR, DG_GU_WPC>(m, st))) return rc;
   }
   if (ct_main < ntc) {
     a.ct_lo = ct_main;
     a.ct_hi = ntc;
-    if ((rc = dense_gemm_launch<0, DG_GT_BM, DG_GU_BN, DG_GT_BK, DG_GT_ST, DG_GT_NW, DG_GT_WR>(a, st))) return rc;
+    if ((rc = dense_gemm_launch<0, DG_GT_BM, DG_GU_BN, DG_GT_BK, DG_GT_ST, DG_GT_NW, DG_GT_WR, DG_GT_WPC>(a, st))) return rc;
   }
   a.a = act;
   a.b = (const bf16_t*)packed + (int64_t)I * 3 * H;  // down_t
@@ -925,7 +951,7 @@ static int dense_pass(const void* x, int x_dtype, int64_t n, int H, const float*
   a.out = out;
   a.ct_lo = 0;
   a.ct_hi = (H + DG_DN_BN - 1) / DG_DN_BN;
-  return dense_gemm_launch<1, DG_DN_BM, DG_DN_BN, DG_DN_BK, DG_DN_ST, DG_DN_NW, DG_DN_WR>(a, st);
+  return dense_gemm_launch<1, DG_DN_BM, DG_DN_BN, DG_DN_BK, DG_DN_ST, DG_DN_NW, DG_DN_WR, DG_DN_WPC>(a, st);
 }
 
 // The whole dense-form prefill over N tokens in passes (inputs validated by the caller).

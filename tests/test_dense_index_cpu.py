@@ -151,7 +151,7 @@ SHAPES = [
 @pytest.mark.parametrize("mode", [0, 1])
 @pytest.mark.parametrize("BM,BK,NW,BN,WR", [(256, 64, 8, 256, 2), (256, 32, 8, 256, 2), (256, 64, 4, 256, 2),
                                           (128, 64, 8, 256, 2), (256, 32, 8, 384, 4), (128, 64, 8, 128, 4),
-                                          (256, 64, 8, 192, 4)])
+                                          (256, 64, 8, 192, 4), (256, 32, 4, 128, 2), (128, 32, 4, 128, 2)])
 def test_dense_gemm_addresses(mode, N, H, E, G, BM, BK, NW, BN, WR):
     if mode == 0 and (BN // (NW // WR)) // 32 % 2:
         pytest.skip("gate/up needs an even number of 32-column blocks per wave")
@@ -165,13 +165,14 @@ def test_dense_gemm_planted_swizzle_fails():
 
 @pytest.mark.parametrize("BM,BN,BK,NW,WR,ST", [(256, 256, 64, 8, 2, 2), (256, 256, 32, 8, 2, 4),
                                                 (256, 384, 32, 8, 4, 3), (128, 256, 64, 8, 2, 3),
-                                                (256, 192, 64, 8, 4, 2), (128, 128, 64, 8, 4, 4)])
+                                                (256, 192, 64, 8, 4, 2), (128, 128, 64, 8, 4, 4),
+                                                (256, 128, 32, 4, 2, 3), (128, 128, 32, 4, 2, 3)])
 def test_dense_gemm_epilogue_bounds(BM, BN, BK, NW, WR, ST):
     """The epilogue through LDS: passes of RP rows x GB 32-column blocks; every accumulator
     lands once in the wave's share of the free stage (in range of it), the 16-byte row
     chunks read back cover what was written, global stores stay inside [N, Ipad] / [N, H]
-    and the gate reads inside the staged [BM][8] gates."""
-    DG_GX = 8
+    and the gate reads inside the staged [BM][GX] gates (GX 8 for 128-neuron column tiles, 4
+    for 64-neuron ones)."""
     ROWB = BK * 2
     STAGE = BM * ROWB + BN * ROWB
     EPW = STAGE // NW
@@ -179,6 +180,7 @@ def test_dense_gemm_epilogue_bounds(BM, BN, BK, NW, WR, ST):
     WM, WC = BM // WR, BN // WN
     MI, NJ = WM // 32, WC // 32
     NB2 = BN // 2
+    GX = 8 if NB2 > 64 else 4
     for (N, H, E, G) in SHAPES:
         I = E * G
         Ipad = (I + 63) // 64 * 64
@@ -188,7 +190,10 @@ def test_dense_gemm_epilogue_bounds(BM, BN, BK, NW, WR, ST):
             NB = NJ // 2 if mode == 0 else NJ
             GB = min(EPW // (32 * 64), NB)
             RW = GB * 64
-            RP = min(EPW // RW // 32 * 32, WM)
+            RP0 = EPW // RW // 32 * 32
+            RP = WM  # dg_pass_rows: the largest multiple of 32 dividing WM that is <= RP0
+            while RP > 32 and (RP > RP0 or WM % RP):
+                RP -= 32
             assert GB >= 1 and RP >= 32 and WM % RP == 0 and RP * RW <= EPW
             cpr = RW // 16
             assert (RP * cpr) % 64 == 0
@@ -198,7 +203,7 @@ def test_dense_gemm_epilogue_bounds(BM, BN, BK, NW, WR, ST):
             for ct in range(n_ct):
                 e_lo = ct * NB2 // G
                 ne = min(E, (ct * NB2 + NB2 - 1) // G + 1) - e_lo
-                assert ne <= DG_GX
+                assert ne <= GX
                 for rt in range(n_rt):
                     for wm in range(WR):
                         for wn in range(WN):
