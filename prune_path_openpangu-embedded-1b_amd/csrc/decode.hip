@@ -1220,6 +1220,10 @@ __global__ __launch_bounds__(512) void decode2p_kernel(
     }
   };
   if (wv == 0) {
+    // the first pass's down rows, all on this wave (idle during the stream): a streaming
+    // wave that also DMAs would wait for its DMAs before its first dot (loads complete in
+    // issue order)
+    if (h0 < h1 && k > 0) dma_rows(h0, min(h1, h0 + rp), 0, 1);
     if (b == 0) {
       // once every workgroup of the call has marked itself alive (so has read the epoch),
       // advance the epoch: the next call uses the other bank
@@ -1266,9 +1270,6 @@ __global__ __launch_bounds__(512) void decode2p_kernel(
       us = wave_sum_dpp(us);
       if (lane < DEC2_REPS) st_rlx(&bank[lane * DEC2_RS + t], dec2_word(pp_silu(gs) * us * Lg_s[t / G]));
     };
-    // this wave's share of the first pass's down rows, then its records (loads complete
-    // in issue order, so the records' waits do not hold the DMAs back)
-    if (h0 < h1 && k > 0) dma_rows(h0, min(h1, h0 + rp), wv - 1, NS);
     if (t0 < T) load_rec(ga, ua, t0);
     if (t1 < T) load_rec(gb, ub, t1);
     for (int t = t0; t < T; t += 2 * Q) {
