@@ -986,15 +986,17 @@ __global__ __launch_bounds__(512) void decode16_kernel(
 
   // ---- phase 2: every act word of the call into LDS (bounded wait; replica b % DEC2_REPS),
   // then the rows. Polling starts once this workgroup's own records are published (its
-  // polls would otherwise compete with the record stream at the memory side). Wave 0,
-  // idle during the stream, first runs this code once dry (one poll round, no waits, no
-  // output): the instruction cache is cold at each launch, and the dry pass brings the
-  // code in before the real pass needs it.
+  // polls would otherwise compete with the record stream at the memory side). Wave NW-1
+  // (one of the streaming waves with the fewest records, so the first to finish) first
+  // runs this code once dry (one poll round, no waits, no output): the instruction cache
+  // is cold at each launch, and the dry pass brings the code in before the real pass
+  // needs it. (Wave 0 is busy with the down-row DMAs until late in the stream: a dry
+  // pass there delays the workgroup's first real poll.)
   const int k = k_s;
   const int T = k * G;
   const uint32_t* rbank = bank + (b % DEC2_REPS) * DEC2_RS;
 #pragma nounroll
-  for (int pass = wv == 0 ? 0 : 1; pass < 2; ++pass) {
+  for (int pass = wv == NW - 1 ? 0 : 1; pass < 2; ++pass) {
     const bool dry = pass == 0;
     if (!dry) __syncthreads();
     // every word of this thread loaded at once (T <= 16 * G <= 16 * NT), then the words
@@ -1201,29 +1203,37 @@ __global__ __launch_bounds__(512) void decode2p_kernel(
   // down rows [r0, r1) of ranks 0 .. k-1 -> LDS, one wave: rank s's (row, chunk) c at LDS chunk
   // s * (per + 1) + c; the chunk after each rank is padding (it fetches the rank's last
   // chunk again), so ranks sit an odd number of chunks apart and the row sums' reads of
-  // consecutive ranks fall in different LDS banks
-  // (instructions part, part + nparts, ... of the list: the waves 1..NW-1 share it)
-  auto dma_rows = [&](int r0, int r1, int part, int nparts) {
-    const int per = (r1 - r0) * cpr, pp = per + 1, nq = k * pp, step = 64 * nparts;
-    const int first = 64 * part + lane;
-    int s = first / pp, rem = first - s * pp;  // LDS chunk c0 + lane = (rank s, chunk rem)
-    for (int c0 = 64 * part; c0 < nq; c0 += step) {
-      const bool in = c0 + lane < nq;
-      const int sq = in ? s : k - 1, rq = in ? min(rem, per - 1) : per - 1;
-      const unsigned char* src = (const unsigned char*)(down_t + ((int64_t)L_s[sq] * H + r0) * G) + 16 * rq;
-      __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(dn_s + 16 * c0), 16, 0, 2);
-      rem += step;
-      while (rem >= pp) {
-        rem -= pp;
-        ++s;
+  // consecutive ranks fall in different LDS banks. Four DMA instructions per round: their
+  // (rank, chunk) and expert ids are computed and read from LDS together, so one LDS round
+  // trip serves four instructions (the issue loop was otherwise the DMAs' bottleneck:
+  // E=192 decode 18.9 -> 17.9 us). rank = floor(c / pp) as umulhi(c, floor((2^32-1)/pp)+1),
+  // exact for c * pp < 2^32 (here c < 6208, 5 <= pp <= 513)
+  auto dma_rows = [&](int r0, int r1) {
+    const int per = (r1 - r0) * cpr, pp = per + 1, nq = k * pp;
+    const uint32_t magic = 0xffffffffu / (uint32_t)pp + 1u;
+    const bf16_t* base = down_t + (int64_t)r0 * G;
+    for (int c0 = 0; c0 < nq; c0 += 256) {
+      uint32_t e[4];
+      int rq[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int c = min(c0 + 64 * j + lane, nq - 1);
+        const int s = (int)__umulhi((uint32_t)c, magic);
+        rq[j] = min(c - s * pp, per - 1);
+        e[j] = (uint32_t)L_s[s];
       }
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (c0 + 64 * j < nq)
+          __builtin_amdgcn_global_load_lds(base + ((int64_t)e[j] * H * G + 8 * rq[j]),
+                                           (__attribute__((address_space(3))) void*)(dn_s + 16 * (c0 + 64 * j)), 16, 0, 2);
     }
   };
   if (wv == 0) {
     // the first pass's down rows, all on this wave (idle during the stream): a streaming
     // wave that also DMAs would wait for its DMAs before its first dot (loads complete in
     // issue order)
-    if (h0 < h1 && k > 0) dma_rows(h0, min(h1, h0 + rp), 0, 1);
+    if (h0 < h1 && k > 0) dma_rows(h0, min(h1, h0 + rp));
     if (b == 0) {
       // once every workgroup of the call has marked itself alive (so has read the epoch),
       // advance the epoch: the next call uses the other bank
@@ -1284,10 +1294,20 @@ __global__ __launch_bounds__(512) void decode2p_kernel(
   }
 
   // ---- phase 2: every act word of the call into LDS (replica b % DEC2_REPS, bounded
-  // wait), then the rows
-  __syncthreads();
+  // wait), then the rows. Wave NW-1 (among the streaming waves with the fewest records)
+  // first runs this code once dry (one poll round, no waits, no output; its row sum is
+  // row 0's, discarded): the instruction cache is cold at each launch. Each lane reads
+  // four ranks' operands before adding their products (in rank order), one LDS round trip
+  // per four ranks.
   const uint32_t* rbank = bank + (b % DEC2_REPS) * DEC2_RS;
-  {
+  // lanes: (sub, chunk) with sub = lane / cpr when cpr divides 64 (spl ranks per wave
+  // pass), else one rank at a time; row r0 + wv of the pass on wave wv
+  const int spl = (64 % cpr == 0) ? 64 / cpr : 1;
+  const int sub = lane / cpr, cc = lane - sub * cpr;
+#pragma nounroll
+  for (int pass = wv == NW - 1 ? 0 : 1; pass < 2; ++pass) {
+    const bool dry = pass == 0;
+    if (!dry) __syncthreads();
     bool fail = false;
     uint32_t v[16];  // T <= E*G <= 16 * NT
 #pragma unroll
@@ -1296,7 +1316,7 @@ __global__ __launch_bounds__(512) void decode2p_kernel(
       v[u] = i < T ? ld_rlx(&rbank[i]) : 1u;
     }
     uint32_t n = 0;
-    while (!fail) {
+    while (!dry && !fail) {
       bool pending = false;
 #pragma unroll
       for (int u = 0; u < 16; ++u) pending |= v[u] == 0u;
@@ -1313,52 +1333,68 @@ __global__ __launch_bounds__(512) void decode2p_kernel(
     // act of (rank s, neuron g) to act_s[s * (G + 4) + g]: rows padded so the row sums'
     // reads of consecutive ranks fall in different banks; word tid + NT u walks (s, g)
     // by NT per step
-    int sa = tid / G, ga = tid - sa * G;
-    const int ds = NT / G, dg = NT - ds * G;
+    {
+      int sa = tid / G, ga = tid - sa * G;
+      const int ds = NT / G, dg = NT - ds * G;
 #pragma unroll
-    for (int u = 0; u < 16; ++u) {
-      if (tid + NT * u < T) act_s[sa * (G + 4) + ga] = __uint_as_float(~v[u]);
-      sa += ds;
-      ga += dg;
-      if (ga >= G) {
-        ga -= G;
-        ++sa;
-      }
-    }
-    if (fail) fail_s = 1;
-  }
-  vm_wait();  // wave 0's down-row DMAs have landed
-  __syncthreads();
-  const bool failed = fail_s != 0;
-  if (failed && tid == 0) {
-    __hip_atomic_fetch_or(&st->error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    st_rlx(&st->error_call, epoch + 1u);
-  }
-  // lanes: (sub, chunk) with sub = lane / cpr when cpr divides 64 (spl ranks per wave
-  // pass), else one rank at a time; row r0 + wv of the pass on wave wv
-  const int spl = (64 % cpr == 0) ? 64 / cpr : 1;
-  const int sub = lane / cpr, cc = lane - sub * cpr;
-  for (int r0 = h0; r0 < h1; r0 += rp) {
-    const int r1 = min(h1, r0 + rp), nr = r1 - r0;
-    if (r0 != h0) {  // later passes (grids smaller than H / rp): DMA, then compute
-      __syncthreads();
-      if (wv == 0 && k > 0) dma_rows(r0, r1, 0, 1);
-      vm_wait();
-      __syncthreads();
-    }
-    if (wv < nr) {
-      float acc = 0.0f;
-      if (sub < spl) {
-        for (int s = sub; s < k; s += spl) {
-          const uint4 w = *(const uint4*)(dn_s + 16 * (s * (nr * cpr + 1) + wv * cpr + cc));
-          const float4 a0 = *(const float4*)(act_s + s * (G + 4) + 8 * cc);
-          const float4 a1 = *(const float4*)(act_s + s * (G + 4) + 8 * cc + 4);
-          const float av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-          acc += dot8(w, av);
+      for (int u = 0; u < 16; ++u) {
+        if (tid + NT * u < T) act_s[sa * (G + 4) + ga] = __uint_as_float(~v[u]);
+        sa += ds;
+        ga += dg;
+        if (ga >= G) {
+          ga -= G;
+          ++sa;
         }
       }
-      acc = wave_sum_dpp(acc);
-      if (lane == 0) out[r0 + wv] = failed ? (bf16_t)0x7fc0 : f32_to_bf16(acc);
+    }
+    bool failed = false;
+    if (!dry) {
+      if (fail) fail_s = 1;
+      vm_wait();  // wave 0's down-row DMAs have landed
+      __syncthreads();
+      failed = fail_s != 0;
+      if (failed && tid == 0) {
+        __hip_atomic_fetch_or(&st->error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        st_rlx(&st->error_call, epoch + 1u);
+      }
+    }
+    for (int r0 = h0; r0 < h1; r0 += rp) {
+      const int r1 = min(h1, r0 + rp), nr = r1 - r0;
+      if (r0 != h0) {  // later passes (grids smaller than H / rp): DMA, then compute
+        if (dry) break;
+        __syncthreads();
+        if (wv == 0 && k > 0) dma_rows(r0, r1);
+        vm_wait();
+        __syncthreads();
+      }
+      const int wr = dry ? 0 : wv;
+      if (wr < nr) {
+        float acc = 0.0f;
+        if (sub < spl) {
+          // four ranks' operands read before their products are added (in rank order)
+          const float4* a4 = (const float4*)act_s;
+          const int g4 = (G + 4) >> 2, rs = nr * cpr + 1;
+          for (int s0 = sub; s0 < k; s0 += 4 * spl) {
+            uint4 w[4];
+            float4 a0[4], a1[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const int s = min(s0 + j * spl, k - 1);
+              w[j] = *(const uint4*)(dn_s + 16 * (s * rs + wr * cpr + cc));
+              a0[j] = a4[s * g4 + 2 * cc];
+              a1[j] = a4[s * g4 + 2 * cc + 1];
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const float av[8] = {a0[j].x, a0[j].y, a0[j].z, a0[j].w, a1[j].x, a1[j].y, a1[j].z, a1[j].w};
+              const float d = dot8(w[j], av);
+              if (s0 + j * spl < k) acc += d;
+            }
+          }
+        }
+        acc = wave_sum_dpp(acc);
+        if (lane == 0 && !dry) out[r0 + wr] = failed ? (bf16_t)0x7fc0 : f32_to_bf16(acc);
+      }
     }
   }
 }
