@@ -1671,19 +1671,32 @@ __global__ __launch_bounds__(512) void decodeb_kernel(
   const int cpr = nk / 8, RSB = 16 * (cpr + 1);  // staged row: cpr chunks + one pad chunk
   // down rows [p0, p0 + nr) of the slice -> LDS: row rho at rho * RSB, chunk c (8 union
   // neurons a0 + 8c ..) at + 16 c; the pad chunk fetches the row's last chunk again.
-  // Instructions part, part + nparts, ... of the flat list (64 chunks each).
+  // Instructions part, part + nparts, ... of the flat list (64 chunks each), four per round
+  // (one LDS round trip for their expert ids); the divisions by cpr + 1 and G as
+  // multiply-high by floor((2^32-1)/d)+1, exact for n * d < 2^32 (n < 9280 and d <= 65,
+  // n < 8192 and d <= 512 here)
+  const uint32_t mag_c = 0xffffffffu / (uint32_t)(cpr + 1) + 1u, mag_g = 0xffffffffu / (uint32_t)G + 1u;
   auto dma_rows = [&](int p0, int nr, int part, int nparts) {
     if (cpr == 0) return;
-    const int total = nr * (cpr + 1);
-    for (int i0 = 64 * part; i0 < total; i0 += 64 * nparts) {
-      const int f = min(i0 + lane, total - 1);
-      const int rho = f / (cpr + 1);
-      const int c = min(f - rho * (cpr + 1), cpr - 1);
-      const int q = a0 + 8 * c;
-      const int e = ul_s[q / G], g = q - (q / G) * G;
-      const bf16_t* src = down_t + ((size_t)e * H + p0 + rho) * G + g;
-      __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(dn_s + 16 * i0), 16, 0,
-                                       DECB_NT);
+    const int total = nr * (cpr + 1), step = 64 * nparts;
+    for (int i00 = 64 * part; i00 < total; i00 += 4 * step) {
+      int e[4], off[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int f = min(i00 + j * step + lane, total - 1);
+        const int rho = (int)__umulhi((uint32_t)f, mag_c);
+        const int c = min(f - rho * (cpr + 1), cpr - 1);
+        const int q = a0 + 8 * c;
+        const int ue = (int)__umulhi((uint32_t)q, mag_g);
+        e[j] = ul_s[ue];
+        off[j] = (p0 + rho) * G + q - ue * G;
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (i00 + j * step < total)
+          __builtin_amdgcn_global_load_lds(down_t + (size_t)e[j] * H * G + off[j],
+                                           (__attribute__((address_space(3))) void*)(dn_s + 16 * (i00 + j * step)), 16,
+                                           0, DECB_NT);
     }
   };
 

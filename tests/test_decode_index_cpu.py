@@ -11,6 +11,8 @@ its rank with a multiply-high by a magic number instead of a division. Checked h
   the host launches with;
 * the multiply-high division equals floor division over every (c, pp) the kernel can form;
 * a planted mistake (the magic number without its + 1) fails the image check.
+The batch kernel's down-row DMAs (decodeb_kernel, dma_rows: rows of one slice of union
+neurons, spread over the eight waves) are checked the same way.
 """
 import numpy as np
 import pytest
@@ -96,3 +98,57 @@ def test_multiply_high_division_exact_over_kernel_range():
     for pp in range(5, 8 * 64 + 2):
         m = np.uint64(magic_of(pp))
         assert np.array_equal((c * m) >> np.uint64(32), c // np.uint64(pp)), pp
+
+
+def batch_dma_image(nr, cpr, a0, G, H, p0, ul, part, nparts):
+    """decodeb_kernel's dma_rows (csrc/decode.hip): LDS chunk -> source element of down_t, one
+    wave's share (instructions part, part + nparts, ...), four instructions per round."""
+    mag_c = magic_of(cpr + 1)
+    mag_g = magic_of(G)
+    total, step = nr * (cpr + 1), 64 * nparts
+    img = {}
+    for i00 in range(64 * part, total, 4 * step):
+        for j in range(4):
+            if i00 + j * step >= total:
+                continue
+            for lane in range(64):
+                f = min(i00 + j * step + lane, total - 1)
+                rho = (f * mag_c) >> 32
+                c = min(f - rho * (cpr + 1), cpr - 1)
+                q = a0 + 8 * c
+                ue = (q * mag_g) >> 32
+                assert ue < len(ul), "union expert index out of range"
+                img[i00 + j * step + lane] = ul[ue] * H * G + (p0 + rho) * G + q - ue * G
+    return img
+
+
+@pytest.mark.parametrize("G,nu,slice_", [(384, 16, 0), (384, 16, 15), (384, 11, 7), (256, 16, 3), (512, 5, 2), (96, 9, 4)])
+def test_batch_dma_image(G, nu, slice_):
+    """Every wave's share together covers each staged row chunk with down_t[e][p0 + rho] at the
+    slice's union neurons; sources inside down_t; writes inside the kernel's LDS."""
+    H, E, NW, DECB_SMEM = 1536, 16, 8, 8 * 3 * 2 * 24 * 128
+    T = nu * G
+    ul = list(np.random.default_rng(G + nu).permutation(E)[:nu])
+    nblk = T // 16
+    q, rem = divmod(nblk, 16)  # pp_split over the 16 slices
+    sb0 = slice_ * q + min(slice_, rem)
+    sb1 = sb0 + q + (1 if slice_ < rem else 0)
+    a0, nk = 16 * sb0, 16 * (sb1 - sb0)
+    cpr = nk // 8
+    if cpr == 0:
+        return
+    rows = 96
+    while rows > 1 and ((rows * (G // 8 + 1) + 63) // 64 * 64) * 16 > DECB_SMEM:
+        rows -= 1
+    p0 = 8 * 37
+    img = {}
+    for wv in range(NW):
+        part = batch_dma_image(rows, cpr, a0, G, H, p0, ul, wv, NW)
+        assert not set(part) & set(img), "two waves write one LDS chunk"
+        img.update(part)
+    assert max(img) * 16 + 16 <= DECB_SMEM
+    assert all(0 <= v and v + 8 <= E * H * G for v in img.values())
+    for rho in range(rows):
+        for c in range(cpr):
+            qn = a0 + 8 * c
+            assert img[rho * (cpr + 1) + c] == ul[qn // G] * H * G + (p0 + rho) * G + qn % G, (rho, c)
