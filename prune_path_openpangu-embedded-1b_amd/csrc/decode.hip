@@ -251,8 +251,8 @@ __device__ void local_logits(const XT* __restrict__ x, int H, const float* __res
     float a2[2];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
-      a2[i] = __fadd_rn(b5 ? part[i + 2] : part[i], __shfl_xor(b5 ? part[i] : part[i + 2], 32, PP_WAVE));
-    float t = __fadd_rn(b4 ? a2[1] : a2[0], __shfl_xor(b4 ? a2[0] : a2[1], 16, PP_WAVE));
+      a2[i] = __fadd_rn(b5 ? part[i + 2] : part[i], pl_xor32f(b5 ? part[i] : part[i + 2], lane));
+    float t = __fadd_rn(b4 ? a2[1] : a2[0], pl_xor16f(b4 ? a2[0] : a2[1], lane));
     t = row16_sum(t);
     const int e = e0 + 4 * wv + 2 * b5 + b4;
     if ((lane & 15) == 0 && e < E) lg_s[e] = bias ? __fadd_rn(t, bias[e]) : t;
@@ -777,10 +777,10 @@ __device__ __forceinline__ bool sel16_wave(float xl, float m, float tau, float* 
     cum += before ? (double)pq[i] : 0.0;
     exact &= (int)(pq[i] == 0.0f) | (int)(pq[i] >= 0x1p-29f);
   }
-  rank += __shfl_xor(rank, 16, PP_WAVE);
-  cum += __shfl_xor(cum, 16, PP_WAVE);
-  rank += __shfl_xor(rank, 32, PP_WAVE);
-  cum += __shfl_xor(cum, 32, PP_WAVE);
+  rank += (int)pl_xor16((uint32_t)rank, lane);
+  cum += pl_xor16d(cum, lane);
+  rank += (int)pl_xor32((uint32_t)rank, lane);
+  cum += pl_xor32d(cum, lane);
   const float tau32 = tau;
   int k;
   bool sel;

@@ -77,18 +77,6 @@ __device__ __forceinline__ float load_as_f32<bf16_t>(const bf16_t* p, int64_t i)
   return bf16_to_f32(p[i]);
 }
 
-// ---------------------------------------------------------------- wave reductions
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, PP_WAVE);
-  return v;
-}
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, PP_WAVE));
-  return v;
-}
-
 // DPP lane moves inside 16-lane rows: a VALU operand modifier, no LDS round trip
 // (__shfl_xor is a ds_bpermute, about a hundred cycles each).
 #define PP_DPP_XOR1 0xB1   // quad_perm [1,0,3,2]: lane i^1
@@ -122,6 +110,50 @@ __device__ __forceinline__ float row16_max(float v) {
   v = fmaxf(v, dpp_mov<PP_DPP_ROR4>(v));
   v = fmaxf(v, dpp_mov<PP_DPP_XOR2>(v));
   return fmaxf(v, dpp_mov<PP_DPP_XOR1>(v));
+}
+// The value of lane l ^ 16 (l ^ 32) without an LDS round trip: v_permlane16_swap
+// (v_permlane32_swap) of a register with itself swaps its odd and even 16-lane rows (its
+// upper and lower halves) between the two results; a lane takes the result holding its
+// partner's row (lane layout checked on the device).
+__device__ __forceinline__ uint32_t pl_xor16(uint32_t v, int lane) {
+  const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  return ((lane >> 4) & 1) ? r[0] : r[1];
+}
+__device__ __forceinline__ uint32_t pl_xor32(uint32_t v, int lane) {
+  const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return lane >= 32 ? r[0] : r[1];
+}
+__device__ __forceinline__ float pl_xor16f(float v, int lane) {
+  return __uint_as_float(pl_xor16(__float_as_uint(v), lane));
+}
+__device__ __forceinline__ float pl_xor32f(float v, int lane) {
+  return __uint_as_float(pl_xor32(__float_as_uint(v), lane));
+}
+__device__ __forceinline__ double pl_xor16d(double v, int lane) {
+  const unsigned long long u = (unsigned long long)__double_as_longlong(v);
+  return __longlong_as_double(
+      (long long)(((unsigned long long)pl_xor16((uint32_t)(u >> 32), lane) << 32) | pl_xor16((uint32_t)u, lane)));
+}
+__device__ __forceinline__ double pl_xor32d(double v, int lane) {
+  const unsigned long long u = (unsigned long long)__double_as_longlong(v);
+  return __longlong_as_double(
+      (long long)(((unsigned long long)pl_xor32((uint32_t)(u >> 32), lane) << 32) | pl_xor32((uint32_t)u, lane)));
+}
+
+// ---------------------------------------------------------------- wave reductions
+// The xor butterfly over 32, 16, 8, 4, 2, 1 (the same pairs and order, so the same bits):
+// the two cross-row steps by permlane swaps, the row steps by DPP.
+__device__ __forceinline__ float wave_sum(float v) {
+  const int lane = (int)__lane_id();
+  v += pl_xor32f(v, lane);
+  v += pl_xor16f(v, lane);
+  return row16_sum(v);
+}
+__device__ __forceinline__ float wave_max(float v) {
+  const int lane = (int)__lane_id();
+  v = fmaxf(v, pl_xor32f(v, lane));
+  v = fmaxf(v, pl_xor16f(v, lane));
+  return row16_max(v);
 }
 // Whole-wave maximum (rows by DPP, then the four row maxima read as scalars); fmaxf is
 // order-free, so the value equals wave_max's. Wave-uniform.
@@ -507,9 +539,8 @@ static __device__ void select_one_token(LG lg, int E, float tau, SelScratch* ss,
         const float t = __shfl(e, (d + li) & 63, PP_WAVE);
         if (li < E - d) acc = __fadd_rn(acc, t);
       }
-#pragma unroll
-      for (int o = 8; o >= 1; o >>= 1) acc = __fadd_rn(acc, __shfl_xor(acc, o, PP_WAVE));
-      S = __shfl(acc, 0, PP_WAVE);
+      acc = row16_sum(acc);  // the xor 8, 4, 2, 1 butterfly, by DPP
+      S = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), 0));
     }
     const float p = act ? __fmul_rn(e, __fdiv_rn(1.0f, S)) : 0.0f;
     int rank = 0;
@@ -553,9 +584,8 @@ static __device__ void select_one_token(LG lg, int E, float tau, SelScratch* ss,
     for (; d < full_end; d += 16) acc = __fadd_rn(acc, ss->e[d + lane]);
     if (E - d > 0 && lane < E - d) acc = __fadd_rn(acc, ss->e[d + lane]);
   }
-#pragma unroll
-  for (int o = 8; o >= 1; o >>= 1) acc = __fadd_rn(acc, __shfl_xor(acc, o, PP_WAVE));
-  const float S = __shfl(acc, 0, PP_WAVE);
+  acc = row16_sum(acc);  // the xor 8, 4, 2, 1 butterfly, by DPP
+  const float S = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), 0));
   const float r = __fdiv_rn(1.0f, S);
   float pv[PP_MAX_EXPERTS / PP_WAVE];
 #pragma unroll
@@ -637,7 +667,7 @@ __device__ __forceinline__ unsigned long long sel_key(float p, int j) {
 
 // Value of lane (lane ^ j) for a 64-bit key: DPP for j = 1, 2 (quad permutes), 4 (quad
 // reverse then half-row mirror, two involutions) and 8 (the half-row rotation, i ^ 8
-// whichever way it turns), the LDS permute for 16 and 32. j is a constant after
+// whichever way it turns), permlane swaps for 16 and 32. j is a constant after
 // unrolling. (A rotation-based xor 4 depends on the rotation's direction: taken the
 // wrong way round it pairs the wrong lanes and the sort loses keys.)
 template <int CTRL>
@@ -660,8 +690,14 @@ __device__ __forceinline__ unsigned long long key_xor(unsigned long long v, int 
   } else if (j == 8) {
     a = dpp_u32<PP_DPP_ROR8>(lo);
     b = dpp_u32<PP_DPP_ROR8>(hi);
+  } else if (j == 16) {
+    const int lane = (int)__lane_id();
+    a = pl_xor16(lo, lane);
+    b = pl_xor16(hi, lane);
   } else {
-    return __shfl_xor(v, j, PP_WAVE);
+    const int lane = (int)__lane_id();
+    a = pl_xor32(lo, lane);
+    b = pl_xor32(hi, lane);
   }
   return ((unsigned long long)b << 32) | a;
 }

@@ -250,9 +250,7 @@ __device__ __forceinline__ void route16_select(const float (*lg_s)[16], float (*
   const int rr = 4 * w + (lane >> 4), j = lane & 15;
   const int64_t t = tok0 + rr;
   const float xl = lg_s[rr][j];
-  float m = xl;
-#pragma unroll
-  for (int o = 8; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, PP_WAVE));
+  const float m = row16_max(xl);  // order-free: the same value as the xor butterfly
   const float e = pp_expf_u10(__fsub_rn(xl, m));
   ev_s[rr][j] = e;
   wave_sync_lds();

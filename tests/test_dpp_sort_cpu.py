@@ -1,6 +1,6 @@
 """CPU restatement of the workgroup rank computation of the E > 16 decode selection
 (select_one_token_wg in csrc/pp_common.h): per 64-lane wave a bitonic sort of 64-bit
-keys whose partner exchanges use DPP lane moves for xor 1, 2, 4 and 8 and the LDS permute
+keys whose partner exchanges use DPP lane moves for xor 1, 2, 4 and 8 and permlane swaps
 for 16 and 32, then each key's rank = its place in its run + the number of smaller keys in
 every other run (binary search). No GPU.
 
@@ -54,14 +54,45 @@ def _decode_quad_perm(ctrl):
     return [(ctrl >> (2 * k)) & 3 for k in range(4)]
 
 
+def permlane_swap(rows):
+    """v_permlane16_swap (rows = 16) / v_permlane32_swap (rows = 32) of a register with
+    itself, as source lanes of the two results (ISA: the odd rows / the upper half of the
+    first operand are swapped with the even rows / the lower half of the second): returns
+    (src of result 0, src of result 1)."""
+    lanes = np.arange(WAVE)
+    blk = lanes // rows
+    r0 = np.where(blk % 2 == 1, lanes - rows, lanes)  # odd blocks take the even block below
+    r1 = np.where(blk % 2 == 0, lanes + rows, lanes)  # even blocks take the odd block above
+    return r0, r1
+
+
+def pl_xor(j):
+    """pl_xor16 / pl_xor32 (csrc/pp_common.h): a lane takes result 0 in odd blocks of j
+    lanes, result 1 in even ones."""
+    r0, r1 = permlane_swap(j)
+    lanes = np.arange(WAVE)
+    return np.where((lanes // j) % 2 == 1, r0, r1)
+
+
 def lane_maps(direction):
     """Source lane of every lane for the partner exchange of distance j, as the kernel
-    does it (key_xor): DPP for j = 1, 2, 4, 8, the LDS permute (exact xor) otherwise."""
+    does it (key_xor): DPP for j = 1, 2, 4, 8, permlane swaps for 16 and 32."""
     m = {1: quad_perm(XOR1), 2: quad_perm(XOR2), 4: then(quad_perm(QREV), half_mirror()),
          8: row_ror(8, direction)}
     for j in (16, 32):
-        m[j] = np.arange(WAVE) ^ j
+        m[j] = pl_xor(j)
     return m
+
+
+def test_permlane_selection_is_xor():
+    """A planted mistake (the two results taken the other way round) must not pair i with
+    i ^ j: the selection in pl_xor16 / pl_xor32 is what makes the swap an xor."""
+    lanes = np.arange(WAVE)
+    for j in (16, 32):
+        r0, r1 = permlane_swap(j)
+        wrong = np.where((lanes // j) % 2 == 1, r1, r0)
+        assert not np.array_equal(wrong, lanes ^ j)
+        np.testing.assert_array_equal(pl_xor(j), lanes ^ j)
 
 
 def test_dpp_controls_encode_the_quad_perms():
