@@ -2005,16 +2005,15 @@ static int decode_check_args(const void* x, int x_dtype, int H, const float* rou
   return PP_OK;
 }
 
-// Default grid of the two-phase kernels: as few workgroups as keep every workgroup's output
-// rows within one pass of eight (H / 8), but at least three quarters of the CUs (the
-// record stream needs the memory parallelism), at most every CU. At H = 1536 on 256 CUs:
-// 192 workgroups of 8 rows (eight waves, one row each in phase 2) and ~1.7 records per
-// streaming wave: 11.25 us against 11.45 us with 256 workgroups of 6 rows (grids 200 to
-// 248: 11.34 to 11.56 us; 160: 12.5 us, two row passes).
+// Default grid of the E = 16 two-phase kernel: one workgroup per CU. The record stream
+// and the row sums gain from every CU: at H = 1536 on 256 CUs, 256 workgroups of 6 rows
+// take 10.65 us against 11.04 us with 192 of 8 rows (224: 10.71; 232-248, rows 6 and 7
+// mixed: 10.76-10.87; 176, two row passes: 12.2); at H = 512, 1024, 2048, 3072 and 4096
+// 256 workgroups are as fast as any smaller default (within 0.02 us). (With the dry
+// phase-2 pass on wave 0, which issues the down-row DMAs, 192 had been faster than 256.)
 static int dec2_default_grid(int H) {
-  const int cus = pp_device_cus();
-  const int rows8 = (H / 8 + 7) / 8 * 8, q3 = (3 * cus / 4 + 7) / 8 * 8;
-  return std::max(8, std::min(cus, std::max(rows8, q3)));
+  (void)H;
+  return std::max(8, pp_device_cus());
 }
 
 // The launch shared by both entry points: st / acc = the state and the accumulators of
