@@ -719,6 +719,11 @@ __device__ __forceinline__ float dec16_logits(const XT* __restrict__ x, const fl
 // together (the host clamps W to the device's capacity); waits are bounded: a timeout
 // sets error bit 1 and the workgroup writes NaN.
 #define DEC2_REPS 4            // replicas of the act words (a line is polled by W / DEC2_REPS workgroups)
+// decode2p_kernel publishes and polls replica 0 only (the bank keeps DEC2_REPS replica
+// slots for decode16_kernel): at E = 192, G = 32 its 2400 act words per call polled by 256
+// workgroups take 16.77 us with one replica, 16.87 with two, 17.01 with four and 17.34
+// with eight, where decode16 is fastest with two to four (10.60-10.65 us; one: 10.89)
+#define DEC2P_REPS 1
 #define DEC2_WMAX 1024         // workgroups per call at most (alive words per bank)
 #define DEC2_GMAX 512          // neurons per expert at most (acts of one call fit LDS: 16 * 512 words)
 #define DEC2_RS (16 * DEC2_GMAX)  // words per act replica: a fixed layout, whatever the call's G
@@ -1278,7 +1283,7 @@ __global__ __launch_bounds__(512) void decode2p_kernel(
       }
       gs = wave_sum_dpp(gs);
       us = wave_sum_dpp(us);
-      if (lane < DEC2_REPS) st_rlx(&bank[lane * DEC2_RS + t], dec2_word(pp_silu(gs) * us * Lg_s[t / G]));
+      if (lane < DEC2P_REPS) st_rlx(&bank[lane * DEC2_RS + t], dec2_word(pp_silu(gs) * us * Lg_s[t / G]));
     };
     if (t0 < T) load_rec(ga, ua, t0);
     if (t1 < T) load_rec(gb, ub, t1);
@@ -1293,13 +1298,13 @@ __global__ __launch_bounds__(512) void decode2p_kernel(
     }
   }
 
-  // ---- phase 2: every act word of the call into LDS (replica b % DEC2_REPS, bounded
+  // ---- phase 2: every act word of the call into LDS (replica b % DEC2P_REPS, bounded
   // wait), then the rows. Wave NW-1 (among the streaming waves with the fewest records)
   // first runs this code once dry (one poll round, no waits, no output; its row sum is
   // row 0's, discarded): the instruction cache is cold at each launch. Each lane reads
   // four ranks' operands before adding their products (in rank order), one LDS round trip
   // per four ranks.
-  const uint32_t* rbank = bank + (b % DEC2_REPS) * DEC2_RS;
+  const uint32_t* rbank = bank + (b % DEC2P_REPS) * DEC2_RS;
   // lanes: (sub, chunk) with sub = lane / cpr when cpr divides 64 (spl ranks per wave
   // pass), else one rank at a time; row r0 + wv of the pass on wave wv
   const int spl = (64 % cpr == 0) ? 64 / cpr : 1;
