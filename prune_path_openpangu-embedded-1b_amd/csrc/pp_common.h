@@ -702,9 +702,147 @@ __device__ __forceinline__ unsigned long long key_xor(unsigned long long v, int 
   return ((unsigned long long)b << 32) | a;
 }
 
+// This wave's LDS writes visible to its other lanes (LDS executes a wave's operations in order)
+__device__ __forceinline__ void sel_lds_sync() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_wave_barrier();
+}
+template <int NS, typename LG>
+static __device__ void select_one_token_w1(LG lg, int E, float tau, SelScratch* ss, unsigned long long* keys,
+                                           int lane) {
+  constexpr int N = 64 * NS;
+  const int E16 = (E + 15) & ~15;
+  float x[NS];
+#pragma unroll
+  for (int q = 0; q < NS; ++q) {
+    const int i = lane + 64 * q;
+    x[q] = i < E ? lg(i) : -__builtin_huge_valf();
+  }
+  float m = x[0];
+#pragma unroll
+  for (int q = 1; q < NS; ++q) m = fmaxf(m, x[q]);
+  m = wave_max(m);
+  float e[NS];
+#pragma unroll
+  for (int q = 0; q < NS; ++q) e[q] = lane + 64 * q < E ? pp_expf_u10(__fsub_rn(x[q], m)) : 0.0f;
+  // row sum in the fixed order: lane j < 16 adds e[16 c + j], c = 0, 1, ... (chunk c sits in
+  // row c % 4 of slot c / 4), then the xor 8, 4, 2, 1 butterfly
+  float acc = 0.0f;
+#pragma unroll
+  for (int c = 0; c < N / 16; ++c) {
+    if (16 * c >= E16) break;
+    float v = e[c >> 2];
+    if ((c & 3) == 1) v = pl_xor16f(v, lane);
+    else if ((c & 3) == 2) v = pl_xor32f(v, lane);
+    else if ((c & 3) == 3) v = pl_xor16f(pl_xor32f(v, lane), lane);
+    acc = c == 0 ? v : __fadd_rn(acc, v);
+  }
+  acc = row16_sum(acc);
+  const float S = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), 0));
+  const float r = __fdiv_rn(1.0f, S);
+  unsigned long long key[NS];
+#pragma unroll
+  for (int q = 0; q < NS; ++q) {
+    const int i = lane + 64 * q;
+    const float p = __fmul_rn(e[q], r);
+    if (i < E) ss->e[i] = p;
+    key[q] = i < E ? sel_key(p, i) : ~0ull;
+  }
+#pragma unroll
+  for (int k2 = 2; k2 <= N; k2 <<= 1)
+#pragma unroll
+    for (int j = k2 >> 1; j > 0; j >>= 1) {
+      if (j >= 64) {
+        const int js = j >> 6;
+#pragma unroll
+        for (int q = 0; q < NS; ++q)
+          if ((q & js) == 0) {
+            const int q2 = q | js;
+            const bool up = ((64 * q + lane) & k2) == 0;  // ascending block
+            const unsigned long long a = key[q], b = key[q2];
+            const bool lt = b < a;
+            const unsigned long long lo = lt ? b : a, hi = lt ? a : b;
+            key[q] = up ? lo : hi;
+            key[q2] = up ? hi : lo;
+          }
+      } else {
+#pragma unroll
+        for (int q = 0; q < NS; ++q) {
+          const int n = 64 * q + lane;
+          const unsigned long long o = key_xor(key[q], j);
+          const bool keep_min = ((n & j) == 0) == ((n & k2) == 0);
+          key[q] = ((o < key[q]) == keep_min) ? o : key[q];
+        }
+      }
+    }
+#pragma unroll
+  for (int q = 0; q < NS; ++q) keys[64 * q + lane] = key[q];
+  sel_lds_sync();
+  // sorted positions: rank n holds expert (uint32)key; keys strictly increase over the E
+  // real ones (unique by their index bits), else the network lost or duplicated a key
+  bool bad = false;
+  float v[NS];
+  bool exact = true;
+#pragma unroll
+  for (int q = 0; q < NS; ++q) {
+    const int n = 64 * q + lane;
+    const int idx = (int)(uint32_t)key[q];
+    if (n < E) {
+      bad |= idx >= E || (n + 1 < E && !(key[q] < keys[min(n + 1, N - 1)]));
+      ss->order[n] = idx;
+      v[q] = ss->e[min(idx, E - 1)];
+      ss->srt[n] = v[q];
+    } else {
+      v[q] = 0.0f;
+    }
+    exact = exact && (v[q] == 0.0f || v[q] >= 0x1p-29f);
+  }
+  bad = __any(bad);
+  int k;
+  if (__all(exact)) {
+    double carry = 0.0;
+    int c = 0;
+    const float tau32 = tau;
+#pragma unroll
+    for (int q = 0; q < NS; ++q) {
+      const double incl = carry + wave_incl_scan_f64((double)v[q]);
+      c += __popcll(__ballot(64 * q + lane < E && (float)incl < tau32));
+      const unsigned long long u = (unsigned long long)__double_as_longlong(incl);
+      const uint32_t clo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, 63);
+      const uint32_t chi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), 63);
+      carry = __longlong_as_double((long long)(((unsigned long long)chi << 32) | clo));
+    }
+    k = c > 0 ? c : 1;
+  } else {
+    sel_lds_sync();
+    k = tau_cut([&](int q) { return ss->srt[q]; }, E, tau);
+  }
+  if (lane == 0) {
+    ss->k = k;
+    ss->bad = bad ? 1 : 0;
+  }
+  sel_lds_sync();
+  if (lane == 0) ss->tie = (k < E && ss->srt[k - 1] == ss->srt[k]) ? 1 : 0;
+}
+
 template <typename LG>
 static __device__ void select_one_token_wg(LG lg, int E, float tau, SelScratch* ss, unsigned long long* keys,
                                            float* red, int tid, int nthreads) {
+  if (E <= 128) {  // uniform: the one-wave form, the other waves wait
+    if ((tid >> 6) == 0) {
+      if (E <= 64) select_one_token_w1<1>(lg, E, tau, ss, keys, tid & 63);
+      else select_one_token_w1<2>(lg, E, tau, ss, keys, tid & 63);
+    }
+    wg_lds_barrier();
+    if (ss->tie) {  // uniform
+      if (tid == 0) {
+        for (int j = 0; j < E; ++j) { ss->srt[j] = ss->e[j]; ss->order[j] = j; }
+        kv_introsort(ss->srt, ss->order, E, ss->stk);
+      }
+      wg_lds_barrier();
+    }
+    return;
+  }
   const int lane = tid & 63, wv = tid >> 6, nw = nthreads >> 6;
   const int E16 = (E + 15) & ~15;
   const float x = tid < E ? lg(tid) : -__builtin_huge_valf();

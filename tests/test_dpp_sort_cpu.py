@@ -1,5 +1,5 @@
 """CPU restatement of the workgroup rank computation of the E > 16 decode selection
-(select_one_token_wg in csrc/pp_common.h): per 64-lane wave a bitonic sort of 64-bit
+(select_one_token_wg in csrc/pp_common.h; above E = 128): per 64-lane wave a bitonic sort of 64-bit
 keys whose partner exchanges use DPP lane moves for xor 1, 2, 4 and 8 and permlane swaps
 for 16 and 32, then each key's rank = its place in its run + the number of smaller keys in
 every other run (binary search). No GPU.
@@ -191,6 +191,69 @@ def test_wg_ranks_equal_a_plain_sort(E, direction):
         np.testing.assert_array_equal(order, np.argsort(keys, kind="stable"))
         # torch's descending order with NaN first and equal values by index
         assert sorted(order.tolist()) == list(range(E))
+
+
+def w1_sort(keys, maps, NS):
+    """select_one_token_w1's network (csrc/pp_common.h), E <= 64 * NS: key i in slot
+    i // 64 of lane i % 64 (padding ~0), bitonic over positions n = 64 q + lane: partner
+    n ^ j in another lane (the exchange maps) for j < 64, in the other slot of the same
+    lane for j >= 64. Returns the keys in position order."""
+    N = 64 * NS
+    allk = np.full(N, np.uint64(0xFFFFFFFFFFFFFFFF))
+    allk[:keys.size] = keys
+    key = allk.reshape(NS, WAVE).copy()
+    lanes = np.arange(WAVE)
+    k2 = 2
+    while k2 <= N:
+        j = k2 >> 1
+        while j > 0:
+            if j >= 64:
+                js = j >> 6
+                for q in range(NS):
+                    if q & js:
+                        continue
+                    q2 = q | js
+                    up = ((64 * q + lanes) & k2) == 0
+                    lo, hi = np.minimum(key[q], key[q2]), np.maximum(key[q], key[q2])
+                    key[q], key[q2] = np.where(up, lo, hi), np.where(up, hi, lo)
+            else:
+                for q in range(NS):
+                    n = 64 * q + lanes
+                    o = key[q][maps[j]]
+                    keep_min = ((n & j) == 0) == ((n & k2) == 0)
+                    key[q] = np.where((o < key[q]) == keep_min, o, key[q])
+            j >>= 1
+        k2 <<= 1
+    return key.reshape(-1)
+
+
+@pytest.mark.parametrize("direction", [+1, -1])
+@pytest.mark.parametrize("E", [17, 24, 32, 63, 64, 65, 96, 100, 127, 128])
+def test_one_wave_sort_equals_a_plain_sort(E, direction):
+    """The one-wave form (E <= 128): sorted positions are the ranks, the first E of them
+    the real keys strictly increasing (the kernel's sortedness check), the same order as
+    the multi-wave form and a plain sort."""
+    rng = np.random.default_rng(E * 5 + (direction > 0))
+    maps = lane_maps(direction)
+    NS = 1 if E <= 64 else 2
+    for p in _rows(E, rng):
+        keys = sel_key(p, np.arange(E))
+        srt = w1_sort(keys, maps, NS)
+        order = (srt[:E] & np.uint64(0xFFFFFFFF)).astype(np.int64)
+        assert (srt[1:E] > srt[:E - 1]).all()
+        np.testing.assert_array_equal(order, np.argsort(keys, kind="stable"))
+        np.testing.assert_array_equal(order, wg_ranks(keys, maps)[0])
+
+
+def test_one_wave_sort_with_a_wrong_exchange_fails_the_sortedness_check():
+    """xor 4 as a row rotation breaks the network: the first E positions are no longer
+    strictly increasing, which the kernel reports through its bad flag."""
+    E = 100
+    maps = lane_maps(+1)
+    maps[4] = row_ror(4, +1)
+    keys = sel_key(np.random.default_rng(3).standard_normal(E).astype(np.float32), np.arange(E))
+    srt = w1_sort(keys, maps, 2)
+    assert not (srt[1:E] > srt[:E - 1]).all()
 
 
 def test_a_wrong_exchange_is_caught_by_the_permutation_check():
