@@ -1300,8 +1300,8 @@ __global__ __launch_bounds__(512) void decode2p_kernel(
 
   // ---- phase 2: every act word of the call into LDS (replica b % DEC2P_REPS, bounded
   // wait), then the rows. Wave NW-1 (among the streaming waves with the fewest records)
-  // first runs this code once dry (one poll round, no waits, no output; its row sum is
-  // row 0's, discarded): the instruction cache is cold at each launch. Each lane reads
+  // first runs the polls and act writes once dry (one poll round, no waits): the
+  // instruction cache is cold at each launch. Each lane reads
   // four ranks' operands before adding their products (in rank order), one LDS round trip
   // per four ranks.
   const uint32_t* rbank = bank + (b % DEC2P_REPS) * DEC2_RS;
@@ -1363,16 +1363,18 @@ __global__ __launch_bounds__(512) void decode2p_kernel(
         st_rlx(&st->error_call, epoch + 1u);
       }
     }
+    if (dry) continue;  // on to the real pass: the dry one covers the polls and the act
+                        // writes (a dry row sum delayed the real pass: 16.8 -> 16.5 us
+                        // without it at E = 192)
     for (int r0 = h0; r0 < h1; r0 += rp) {
       const int r1 = min(h1, r0 + rp), nr = r1 - r0;
       if (r0 != h0) {  // later passes (grids smaller than H / rp): DMA, then compute
-        if (dry) break;
         __syncthreads();
         if (wv == 0 && k > 0) dma_rows(r0, r1);
         vm_wait();
         __syncthreads();
       }
-      const int wr = dry ? 0 : wv;
+      const int wr = wv;
       if (wr < nr) {
         float acc = 0.0f;
         if (sub < spl) {
