@@ -1081,10 +1081,11 @@ __global__ __launch_bounds__(512) void decode16_kernel(
 // workgroup e < E computes logit e and publishes it as a word (~bits, 0 = not yet written)
 // in DEC2_LREPS replicas kept in this call's act bank, and every workgroup gathers the E
 // words of replica b % DEC2_LREPS (the bank is cleared by the previous call, so no tags).
-// Selection by wave 0 (E <= 16) or by the whole workgroup. No speculation. The down rows
-// of the k selected experts are one flat list of 16-byte chunks, DMA'd by the streaming
-// waves into contiguous LDS (a G = 32 row is only 64 bytes); phase 2 sums each output row over
-// (rank, chunk) items spread over the lanes, in a fixed order.
+// Selection by wave 0 (E <= 16) or by the workgroup selection (one wave up to E = 128).
+// No speculation. The down rows of the k selected experts are one flat list of 16-byte
+// chunks, DMA'd by wave 0 (idle during the stream) into contiguous LDS (a G = 32 row is
+// only 64 bytes); phase 2 sums each output row over (rank, chunk) items spread over the
+// lanes, in a fixed order. Act words in one replica (DEC2P_REPS).
 template <typename XT, int CPL, bool LOCAL>
 __global__ __launch_bounds__(512) void decode2p_kernel(
     const XT* __restrict__ x, int H, const float* __restrict__ router, const float* __restrict__ bias, int E,
