@@ -123,19 +123,23 @@ int pp_bucket(const uint8_t* mask, const float* gates, int64_t n_tokens, int E, 
  * GEMVs over the selected experts' neurons, silu(g)*u*gate, down GEMV, bf16 output.
  * Replaces TauSparseMoE.forward_decode with moe_router_select_kernel_decode and
  * moe_decode_swiglu_fused_kernel (src/tl_kernel_optimized_Ultimate_PanGU.py:335-462, 494-530).
- * Two kernels, by shape:
+ * Three kernels, by shape:
  *   E = 16, H % 512 == 0, G <= 512 (the configured shape): two phases in one launch.
  *     The gate/up records are spread over all workgroups and every act
  *     silu(g.x)*(u.x)*gate is published to the workspace; each workgroup then writes
  *     its own rows of the output as a fixed-order sum over the selected experts' down
  *     rows. Every workgroup waits for acts from all the others, so the grid is clamped
- *     to the workgroups the device holds at once (occupancy calculator) and to 1024.
- *   any other shape: each workgroup accumulates its records' act * down into a partial
+ *     to the workgroups the device holds at once (occupancy calculator) and to 1024;
+ *     the automatic grid is one workgroup per CU.
+ *   other shapes with E*G <= 8192 and G <= 512 (the checkpoint's E = 192, G = 32 among
+ *     them): the same two phases; with E > 16 or 16*H > 32768 each logit is computed
+ *     and published by its own workgroup and every workgroup gathers all E of them.
+ *   the rest: each workgroup accumulates its records' act * down into a partial
  *     output, partials are summed in 64-bit fixed point (value * 2^32) and the last
- *     workgroup writes bf16. Shapes with (E > 16 or 16*H > 32768) publish each logit
- *     from its own workgroup and every workgroup waits for all E of them, so the E
- *     router workgroups must be resident together: checked from the occupancy
- *     calculator before the launch (PP_ERR_UNSUPPORTED otherwise).
+ *     workgroup writes bf16.
+ *   Where logits are published, the E router workgroups must be resident together:
+ *   checked from the occupancy calculator before the launch (PP_ERR_UNSUPPORTED
+ *   otherwise).
  * Both sum in an order that does not depend on timing: the bf16 output is the same bits
  * on every call. A wait that cannot finish (e.g. other work holding the device) ends
  * after a bounded spin with error bit 1 and NaN outputs, never a hang.
