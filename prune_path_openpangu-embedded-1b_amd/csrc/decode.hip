@@ -1781,20 +1781,25 @@ __global__ __launch_bounds__(512) void decodeb_kernel(
       }
     }
     wg_lds_barrier();
-    // published in fragment order: 16 B = 8 neurons of one token
+    // published in fragment order (16 B = 8 neurons of one token) by wave 0 alone, whose
+    // store counter then covers every act store of the workgroup
     const int ng = nq / 8;
-    for (int it = tid; it < N * ng; it += NT) {
-      const int t = it / ng, gi = it - t * ng;
-      const int k = nb0 + 8 * gi;  // union neuron of the group (a multiple of 8)
-      decb_st16(r_af, decb_frag(k >> 4, t >> 5, (t & 31) + 32 * ((k >> 3) & 1)),
-                *(const uint4*)(act_s + t * 32 + 8 * gi));
-    }
-    wg_lds_barrier();  // the acts are read out: the rings may be refilled
+    if (wv == 0)
+      for (int it = lane; it < N * ng; it += 64) {
+        const int t = it / ng, gi = it - t * ng;
+        const int k = nb0 + 8 * gi;  // union neuron of the group (a multiple of 8)
+        decb_st16(r_af, decb_frag(k >> 4, t >> 5, (t & 31) + 32 * ((k >> 3) & 1)),
+                  *(const uint4*)(act_s + t * 32 + 8 * gi));
+      }
+    wg_lds_barrier();  // the acts are read out (and their stores issued): the rings may be refilled
   }
-  vm_wait();  // this thread's act stores
-  __syncthreads();
-  if (tid == 0) st_rlx(&aflag[b], tag);
-  dma_rows(hr0, min(rows_pp, hr1 - hr0), wv, NW);  // the first pass's down rows (LDS is free)
+  if (wv == 0) {
+    vm_wait();  // the act stores
+    if (lane == 0) st_rlx(&aflag[b], tag);
+    dma_rows(hr0, min(rows_pp, hr1 - hr0), 7, 8);
+  } else {  // the first pass's down rows (LDS is free), behind the act stores
+    dma_rows(hr0, min(rows_pp, hr1 - hr0), wv - 1, NW);
+  }
 
   // ---- D: partial sums of rows [hr0, hr1) over slice s
   {
